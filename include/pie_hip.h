@@ -1,0 +1,189 @@
+/*
+ * pie_hip.h — C ABI of the MI355X (gfx950) per-layer kernels of Pie's Python backend.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, element strides (in elements, not bytes) and sizes;
+ *   - enqueues its kernels asynchronously on `stream` (a hipStream_t; NULL = the null stream);
+ *   - never allocates, frees or synchronises, so it may be recorded into a HIP graph;
+ *   - returns PIE_HIP_OK (0) or a nonzero PIE_HIP_E* code; pie_hip_last_error() then holds a
+ *     message for the calling thread.
+ *
+ * bf16 buffers are passed as uint16_t (raw bfloat16 bits). int32 index buffers are int32_t.
+ *
+ * Reference interfaces each function replaces are cited as file:line of zyma98/pie
+ * (paths relative to the repository root) or of the torch / flashinfer API those files call.
+ */
+#ifndef PIE_HIP_H
+#define PIE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t pie_bf16;
+
+enum {
+  PIE_HIP_OK = 0,
+  PIE_HIP_EINVAL = 1,  /* bad size, stride, null pointer or unsupported parameter */
+  PIE_HIP_ELAUNCH = 2, /* the HIP runtime rejected the launch */
+};
+
+/* Message describing the last nonzero return on this thread ("" if none). */
+const char* pie_hip_last_error(void);
+
+/* ABI version; bumped whenever a signature below changes. */
+int pie_hip_abi_version(void);
+
+/*
+ * RMSNorm over the last dimension:
+ *   y[r,:] = bf16( f32(x[r,:]) * rsqrt(mean_j f32(x[r,j])^2 + eps) * f32(w) )
+ * Replaces torch.nn.functional.rms_norm(x, [cols], w, eps) at
+ *   pie/src/pie_worker/model/llama3.py:555-560, :618-623, :504-509 and qwen3.py:538-543, :605-610.
+ * y may alias x (same strides).
+ */
+int pie_hip_rmsnorm(const pie_bf16* x, int64_t x_row_stride,
+                    const pie_bf16* w,
+                    pie_bf16* y, int64_t y_row_stride,
+                    int64_t rows, int64_t cols, float eps, void* stream);
+
+/*
+ * Residual add followed by RMSNorm of the sum:
+ *   s = bf16(f32(r) + f32(x));  y = rmsnorm(s)
+ * Replaces `residual + down` / `residual + attn_proj` (llama3.py:586, :710; qwen3.py:571, :710)
+ * together with the next layer's fun.rms_norm (llama3.py:555/:618). Both the new residual
+ * stream s and the normalised y are written. s may alias r or x.
+ */
+int pie_hip_fused_add_rmsnorm(const pie_bf16* x, int64_t x_row_stride,
+                              const pie_bf16* r, int64_t r_row_stride,
+                              pie_bf16* s, int64_t s_row_stride,
+                              pie_bf16* y, int64_t y_row_stride,
+                              const pie_bf16* w,
+                              int64_t rows, int64_t cols, float eps, void* stream);
+
+/*
+ * Per-head RMSNorm of q [T,Hq,D] (weight qw[D]) and k [T,Hkv,D] (weight kw[D]) in one launch.
+ * Replaces the two fun.rms_norm calls at qwen3.py:651-662 (normalized_shape=[D]).
+ * Inputs may be strided views (token stride, head stride; innermost stride 1).
+ * Outputs may alias inputs.
+ */
+int pie_hip_qk_rmsnorm(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                       pie_bf16* q_out, int64_t qo_tok_stride, int64_t qo_head_stride,
+                       const pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                       pie_bf16* k_out, int64_t ko_tok_stride, int64_t ko_head_stride,
+                       const pie_bf16* qw, const pie_bf16* kw,
+                       int64_t T, int64_t Hq, int64_t Hkv, int64_t D, float eps, void* stream);
+
+/*
+ * SiLU-and-mul over gate_up [rows, 2I] (gate = cols [0,I), up = cols [I,2I)):
+ *   out = bf16( f32(bf16(silu(f32(gate)))) * f32(up) )
+ * Replaces `gate, up = torch.split(gate_up, [I, I], -1); fun.silu(gate) * up`
+ * at llama3.py:569-572 and qwen3.py:553-556.
+ */
+int pie_hip_silu_and_mul(const pie_bf16* gate_up, int64_t in_row_stride,
+                         pie_bf16* out, int64_t out_row_stride,
+                         int64_t rows, int64_t I, void* stream);
+
+/*
+ * Token-embedding gather: out[t,:] = W[ids[t],:] (bit copy).
+ * Replaces fun.embedding(token_ids, W) at llama3.py:471 and qwen3.py:468-472.
+ * Ids outside [0, V) produce a zero row (torch raises instead; a graph-capturable kernel
+ * cannot, so the Python wrapper offers an explicit host-side check).
+ */
+int pie_hip_embedding(const int32_t* ids, int64_t T,
+                      const pie_bf16* W, int64_t V, int64_t H, int64_t w_row_stride,
+                      pie_bf16* out, int64_t out_row_stride, void* stream);
+
+/*
+ * Rotary embedding applied in place to q [T,Hq,D] and k [T,Hkv,D] at positions pos[T].
+ * inv_freq is a HOST array of rotary_dim/2 fp32 inverse frequencies (<= 256 entries); it is
+ * copied into the kernel arguments, so no device table exists.
+ * interleave=0 rotates (v[i], v[i+rotary_dim/2]) (NeoX half split); interleave=1 rotates
+ * (v[2i], v[2i+1]). Dimensions >= rotary_dim are left untouched.
+ * Replaces flashinfer.apply_rope_pos_ids_inplace (qwen3.py:665-670) and
+ * flashinfer.apply_llama31_rope_pos_ids_inplace (llama3.py:660-669); the frequency rules
+ * are computed on the host by pie_hip_rope_inv_freq / pie_hip_llama31_inv_freq.
+ */
+int pie_hip_rope_inplace(pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                         pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                         const int32_t* pos, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                         int64_t rotary_dim, int interleave, const float* inv_freq,
+                         void* stream);
+
+/*
+ * Host helpers: fill inv_freq[rotary_dim/2] (computed in float64, rounded to fp32).
+ *   standard:  f_i = 1 / (rope_scale * theta^(2i/rotary_dim))
+ *   llama31:   f_i = theta^(-2i/rotary_dim), then wavelength-based smoothing with
+ *              (rope_scale, low_freq_factor, high_freq_factor, old_context_len)
+ * Follow pie/src/flashinfer_metal/kernels/metal_rope.metal:63-89 and
+ * flashinfer_metal/ops.py:285-346.
+ */
+int pie_hip_rope_inv_freq(float* inv_freq, int64_t rotary_dim, float rope_scale, float rope_theta);
+int pie_hip_llama31_inv_freq(float* inv_freq, int64_t rotary_dim, float rope_scale,
+                             float rope_theta, float low_freq_factor, float high_freq_factor,
+                             float old_context_len);
+
+/*
+ * Paged KV append: for token t, b = batch_indices[t], p = positions[t],
+ *   page = kv_indices[kv_indptr[b] + p / page_size], slot = p % page_size,
+ *   k_cache[page*page_stride + slot*slot_stride + h*head_stride + d] = k[t,h,d]   (same for v).
+ * Tokens whose batch index, logical page or physical page is out of range are skipped, as in
+ * pie/src/flashinfer_metal/kernels/metal_append_paged_kv_cache.metal:51-70.
+ * Cache strides cover the reference layouts: NHD [pages,2,P,Hkv,D] (llama3.py:966-979) gives
+ * page_stride=2*P*Hkv*D, slot_stride=Hkv*D, head_stride=D, v_cache=k_cache+P*Hkv*D; HND and
+ * split (k_cache, v_cache) tensors are other stride choices.
+ * Replaces flashinfer.append_paged_kv_cache (llama3.py:675-685, qwen3.py:674-684).
+ */
+int pie_hip_paged_kv_append(const pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                            const pie_bf16* v, int64_t v_tok_stride, int64_t v_head_stride,
+                            const int32_t* batch_indices, const int32_t* positions,
+                            const int32_t* kv_indices, const int32_t* kv_indptr,
+                            int64_t batch_size,
+                            pie_bf16* k_cache, pie_bf16* v_cache, int64_t num_pages,
+                            int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                            int64_t page_size, int64_t T, int64_t Hkv, int64_t D, void* stream);
+
+/*
+ * Fused RoPE (in place on q and k, positions pos[T]) + paged append of the rotated k and raw
+ * v: one HBM pass over q/k/v instead of two. Equivalent to pie_hip_rope_inplace followed by
+ * pie_hip_paged_kv_append with the same arguments (llama3.py:660-685 call order).
+ */
+int pie_hip_rope_append(pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                        pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                        const pie_bf16* v, int64_t v_tok_stride, int64_t v_head_stride,
+                        const int32_t* pos, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                        int64_t rotary_dim, int interleave, const float* inv_freq,
+                        const int32_t* batch_indices, const int32_t* positions,
+                        const int32_t* kv_indices, const int32_t* kv_indptr,
+                        int64_t batch_size,
+                        pie_bf16* k_cache, pie_bf16* v_cache, int64_t num_pages,
+                        int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                        int64_t page_size, void* stream);
+
+/*
+ * seq_lens[b] = (kv_indptr[b+1]-kv_indptr[b]-1)*page_size + last_page_len[b], or 0 when the
+ * request holds no page. Replaces flashinfer.get_seq_lens (llama3.py:745-749;
+ * spec pie/src/flashinfer_metal/ops.py:392-407).
+ */
+int pie_hip_get_seq_lens(const int32_t* kv_indptr, const int32_t* last_page_len,
+                         int64_t batch_size, int64_t page_size, int32_t* seq_lens, void* stream);
+
+/*
+ * For every token t in request b (append_indptr[b] <= t < append_indptr[b+1]):
+ *   batch_indices[t] = b,  positions[t] = seq_lens[b] - (append_indptr[b+1]-append_indptr[b])
+ *                                          + (t - append_indptr[b]).
+ * Tokens t < nnz outside every request are left untouched.
+ * Replaces flashinfer.get_batch_indices_positions (llama3.py:751-755;
+ * spec pie/src/flashinfer_metal/ops.py:410-436).
+ */
+int pie_hip_get_batch_indices_positions(const int32_t* append_indptr, const int32_t* seq_lens,
+                                        int64_t batch_size, int64_t nnz,
+                                        int32_t* batch_indices, int32_t* positions,
+                                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PIE_HIP_H */

@@ -1,0 +1,209 @@
+/*
+ * CPU oracle for the per-layer hot path of Pie's Python backend. TEST INFRASTRUCTURE ONLY:
+ * it is the checker that the GPU kernels are compared with, never a compute path of the
+ * product. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.
+ *
+ * Arithmetic is float64 (the "exact" value) with bf16 round-to-nearest-even on output, except
+ * where the reference itself rounds an intermediate to bf16 (the residual sum, silu before
+ * the multiply), which is reproduced bit for bit. bf16 values are passed as uint16_t bits.
+ *
+ * Reference behaviour restated (paths relative to the zyma98/pie repository root):
+ *   rmsnorm            torch rms_norm decomposition, torch/_decomp/decompositions.py:1760-1810,
+ *                      called at pie/src/pie_worker/model/llama3.py:555-560, qwen3.py:651-662
+ *   add_rmsnorm        `residual + down` (llama3.py:586) then the next rms_norm (llama3.py:555)
+ *   silu_and_mul       `fun.silu(gate) * up` after torch.split (llama3.py:569-572)
+ *   embedding          fun.embedding(ids, W) (llama3.py:471)
+ *   rope               pie/src/flashinfer_metal/kernels/metal_rope.metal:26-107
+ *   inv_freq_llama31   metal_rope.metal:63-89
+ *   append             pie/src/flashinfer_metal/kernels/metal_append_paged_kv_cache.metal:23-107
+ *   seq_lens           pie/src/flashinfer_metal/ops.py:392-407
+ *   batch_indices_positions  pie/src/flashinfer_metal/ops.py:410-436
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ bf16 */
+static float bf2f(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* fp32 -> bf16, round to nearest even; NaN stays NaN (quiet). */
+static uint16_t f2bf(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+/* float64 -> bf16 in one rounding (no intermediate fp32 rounding). */
+static uint16_t d2bf(double d) {
+  if (isnan(d)) return 0x7fc0;
+  float f = (float)d; /* RNE to 24 bits; fix the rare double-rounding tie below */
+  uint16_t h = f2bf(f);
+  /* If f landed exactly on a bf16 halfway point, decide the tie from the exact value. */
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0xffffu) == 0x8000u && isfinite(f)) {
+    double lo = bf2f((uint16_t)(u >> 16));
+    double hi = bf2f((uint16_t)((u >> 16) + 1));
+    if (fabs(d - lo) < fabs(hi - d)) h = (uint16_t)(u >> 16);
+    else if (fabs(d - lo) > fabs(hi - d)) h = (uint16_t)((u >> 16) + 1);
+  }
+  return h;
+}
+
+uint16_t oracle_f32_to_bf16(float f) { return f2bf(f); }
+float oracle_bf16_to_f32(uint16_t h) { return bf2f(h); }
+uint16_t oracle_f64_to_bf16(double d) { return d2bf(d); }
+
+/* ------------------------------------------------------------------ RMSNorm */
+static void norm_row(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t cols, double eps) {
+  double ss = 0.0;
+  for (int64_t j = 0; j < cols; ++j) {
+    double v = bf2f(x[j]);
+    ss += v * v;
+  }
+  double rstd = 1.0 / sqrt(ss / (double)cols + eps);
+  for (int64_t j = 0; j < cols; ++j) y[j] = d2bf((double)bf2f(x[j]) * rstd * (double)bf2f(w[j]));
+}
+
+/* Rows addressed as (token, head): row r = t*heads + h at offset t*ts + h*hs. */
+void oracle_rmsnorm(const uint16_t* x, int64_t x_ts, int64_t x_hs, const uint16_t* w, uint16_t* y,
+                    int64_t y_ts, int64_t y_hs, int64_t T, int64_t heads, int64_t cols, double eps) {
+  for (int64_t t = 0; t < T; ++t)
+    for (int64_t h = 0; h < heads; ++h)
+      norm_row(x + t * x_ts + h * x_hs, w, y + t * y_ts + h * y_hs, cols, eps);
+}
+
+void oracle_add_rmsnorm(const uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* s,
+                        uint16_t* y, int64_t rows, int64_t cols, double eps) {
+  for (int64_t i = 0; i < rows; ++i) {
+    for (int64_t j = 0; j < cols; ++j) {
+      /* torch bf16 add: fp32 sum of the two widened values, one RNE rounding */
+      float sum = bf2f(r[i * cols + j]) + bf2f(x[i * cols + j]);
+      s[i * cols + j] = f2bf(sum);
+    }
+    norm_row(s + i * cols, w, y + i * cols, cols, eps);
+  }
+}
+
+/* ------------------------------------------------------------------ SiLU-and-mul */
+/* mode 0: torch's rounding, bf16(bf16(silu(g)) * up); mode 1: single rounding of silu(g)*up. */
+void oracle_silu_and_mul(const uint16_t* gu, int64_t in_rs, uint16_t* out, int64_t rows,
+                         int64_t I, int mode) {
+  for (int64_t i = 0; i < rows; ++i)
+    for (int64_t j = 0; j < I; ++j) {
+      double g = bf2f(gu[i * in_rs + j]);
+      double u = bf2f(gu[i * in_rs + I + j]);
+      double s = g / (1.0 + exp(-g));
+      if (mode == 0) out[i * I + j] = d2bf((double)bf2f(d2bf(s)) * u);
+      else out[i * I + j] = d2bf(s * u);
+    }
+}
+
+/* ------------------------------------------------------------------ embedding */
+/* Returns the number of ids outside [0, V); their rows are zero-filled. */
+int64_t oracle_embedding(const int32_t* ids, int64_t T, const uint16_t* W, int64_t V, int64_t H,
+                         uint16_t* out) {
+  int64_t bad = 0;
+  for (int64_t t = 0; t < T; ++t) {
+    if (ids[t] < 0 || ids[t] >= V) {
+      memset(out + t * H, 0, (size_t)H * 2);
+      ++bad;
+    } else {
+      memcpy(out + t * H, W + (int64_t)ids[t] * H, (size_t)H * 2);
+    }
+  }
+  return bad;
+}
+
+/* ------------------------------------------------------------------ RoPE */
+void oracle_inv_freq_std(double* f, int64_t rd, double scale, double theta) {
+  for (int64_t i = 0; i < rd / 2; ++i) f[i] = 1.0 / (scale * pow(theta, (2.0 * i) / (double)rd));
+}
+
+void oracle_inv_freq_llama31(double* f, int64_t rd, double scale, double theta, double lo,
+                             double hi, double L) {
+  for (int64_t i = 0; i < rd / 2; ++i) {
+    double base = 1.0 / pow(theta, (2.0 * i) / (double)rd);
+    double wavelen = 2.0 * M_PI / base;
+    if (wavelen > L / lo) f[i] = base / scale;
+    else if (wavelen < L / hi) f[i] = base;
+    else {
+      double smooth = (L / wavelen - lo) / (hi - lo);
+      f[i] = (1.0 - smooth) * base / scale + smooth * base;
+    }
+  }
+}
+
+static void rope_head(uint16_t* v, int64_t rd, int interleave, double p, const double* f) {
+  for (int64_t i = 0; i < rd / 2; ++i) {
+    int64_t ix = interleave ? 2 * i : i, iy = interleave ? 2 * i + 1 : i + rd / 2;
+    double a = p * f[i], c = cos(a), s = sin(a);
+    double x = bf2f(v[ix]), y = bf2f(v[iy]);
+    v[ix] = d2bf(x * c - y * s);
+    v[iy] = d2bf(x * s + y * c);
+  }
+}
+
+/* In place on q [T,Hq,D] and k [T,Hkv,D] (strided: token stride, head stride; unit inner). */
+void oracle_rope(uint16_t* q, int64_t q_ts, int64_t q_hs, uint16_t* k, int64_t k_ts, int64_t k_hs,
+                 const int32_t* pos, int64_t T, int64_t Hq, int64_t Hkv, int64_t rd,
+                 int interleave, const double* inv_freq) {
+  for (int64_t t = 0; t < T; ++t) {
+    double p = (double)pos[t];
+    for (int64_t h = 0; h < Hq; ++h) rope_head(q + t * q_ts + h * q_hs, rd, interleave, p, inv_freq);
+    for (int64_t h = 0; h < Hkv; ++h) rope_head(k + t * k_ts + h * k_hs, rd, interleave, p, inv_freq);
+  }
+}
+
+/* ------------------------------------------------------------------ paged append */
+/* Returns the number of tokens written (skipped tokens follow the Metal kernel's checks). */
+int64_t oracle_append(const uint16_t* k, int64_t k_ts, int64_t k_hs, const uint16_t* v, int64_t v_ts,
+                      int64_t v_hs, const int32_t* bidx, const int32_t* pos,
+                      const int32_t* kv_indices, const int32_t* kv_indptr, int64_t B,
+                      uint16_t* kc, uint16_t* vc, int64_t num_pages, int64_t page_stride,
+                      int64_t slot_stride, int64_t head_stride, int64_t P, int64_t T, int64_t Hkv,
+                      int64_t D) {
+  int64_t written = 0;
+  for (int64_t t = 0; t < T; ++t) {
+    int64_t b = bidx[t], p = pos[t];
+    if (b < 0 || b >= B || p < 0) continue;
+    int64_t logical = (int64_t)kv_indptr[b] + p / P;
+    if (logical >= kv_indptr[b + 1]) continue;
+    int64_t page = kv_indices[logical];
+    if (page < 0 || page >= num_pages) continue;
+    int64_t base = page * page_stride + (p % P) * slot_stride;
+    for (int64_t h = 0; h < Hkv; ++h) {
+      memcpy(kc + base + h * head_stride, k + t * k_ts + h * k_hs, (size_t)D * 2);
+      memcpy(vc + base + h * head_stride, v + t * v_ts + h * v_hs, (size_t)D * 2);
+    }
+    ++written;
+  }
+  return written;
+}
+
+/* ------------------------------------------------------------------ index helpers */
+void oracle_seq_lens(const int32_t* indptr, const int32_t* last, int64_t B, int64_t P, int32_t* out) {
+  for (int64_t b = 0; b < B; ++b) {
+    int32_t np = indptr[b + 1] - indptr[b];
+    out[b] = np > 0 ? (int32_t)((np - 1) * P + last[b]) : 0;
+  }
+}
+
+void oracle_batch_indices_positions(const int32_t* indptr, const int32_t* seq_lens, int64_t B,
+                                    int64_t nnz, int32_t* bidx, int32_t* pos) {
+  for (int64_t b = 0; b < B; ++b) {
+    int32_t start = indptr[b], end = indptr[b + 1], n = end - start;
+    for (int32_t t = start; t < end && t < nnz; ++t) {
+      if (t < 0) continue;
+      bidx[t] = (int32_t)b;
+      pos[t] = seq_lens[b] - n + (t - start);
+    }
+  }
+}

@@ -1,0 +1,92 @@
+// Shared helpers for the gfx950 per-layer kernels: bf16 packing, wavefront reductions,
+// alignment checks, launch-error reporting. Every kernel in this library is HBM-bound
+// streaming work: 128-bit global loads/stores, fp32 math, no MFMA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/pie_hip.h"
+
+namespace pie {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+// ---------------------------------------------------------------- error reporting (host)
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+int num_cus();  // compute units of the current device (cached per device)
+
+#define PIE_REQUIRE(cond, ...)                                 \
+  do {                                                         \
+    if (!(cond)) return ::pie::set_error(PIE_HIP_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------- bf16 (device)
+// A uint4 carries 8 bf16 values; word i holds elements 2i (low half) and 2i+1 (high half).
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf1(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Round two fp32 values to nearest-even bf16 (v_cvt_pk_bf16_f32 on gfx950) and pack them.
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ uint16_t to_bf1(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+// Round an fp32 value to bf16 and return it widened back to fp32.
+__device__ __forceinline__ float round_bf(float f) { return bf1(to_bf1(f)); }
+
+__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
+  f[0] = bf_lo(v.x); f[1] = bf_hi(v.x); f[2] = bf_lo(v.y); f[3] = bf_hi(v.y);
+  f[4] = bf_lo(v.z); f[5] = bf_hi(v.z); f[6] = bf_lo(v.w); f[7] = bf_hi(v.w);
+}
+__device__ __forceinline__ uint4 pack8(const float* f) {
+  uint4 v;
+  v.x = pack_bf2(f[0], f[1]); v.y = pack_bf2(f[2], f[3]);
+  v.z = pack_bf2(f[4], f[5]); v.w = pack_bf2(f[6], f[7]);
+  return v;
+}
+
+// Streaming 128-bit accesses. Inputs read once and outputs never re-read by the kernel go
+// through the non-temporal path so they do not evict reused data (weights, page tables).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream(const void* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_stream(void* p, const uint4& v) {
+  const u32x4_t w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(p));
+}
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void st16(void* p, const uint4& v) { *reinterpret_cast<uint4*>(p) = v; }
+
+// ---------------------------------------------------------------- reductions (device)
+// Sum over each 16-lane DPP row, result broadcast to all 16 lanes (row_ror 8,4,2,1).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xF, 0xF, false));
+  return v;
+}
+// Full-wavefront sum, uniform result (scalar register).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  const int b = __builtin_bit_cast(int, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+}  // namespace pie

@@ -1,0 +1,340 @@
+// RMSNorm family for gfx950: plain rows, residual-add + RMSNorm, per-head q/k RMSNorm.
+//
+// Semantics follow torch's rms_norm decomposition (torch/_decomp/decompositions.py:1760-1810),
+// which is what fun.rms_norm computes at pie/src/pie_worker/model/llama3.py:555/:618 and
+// qwen3.py:651-662:   y = bf16( (f32(x) * rsqrt(mean(f32(x)^2) + eps)) * f32(w) ).
+// The residual add is torch's bf16 `residual + x`: s = bf16(f32(r) + f32(x)), and the norm is
+// taken of the rounded s (llama3.py:586 feeding the next layer's :555).
+//
+// Mapping. Rows of cols = NV*512 elements are held entirely in registers by ONE wavefront:
+// lane l owns the 16-byte vectors l, l+64, ..., so every load/store instruction of a wave
+// covers 1 KiB of contiguous row. The sum of squares is reduced with DPP row rotations and
+// four readlanes (no LDS, no barrier). The weight row is loaded once per wave and reused for
+// every row the wave visits. Per-head rows (D = 64/128/256) use 16-lane groups instead, four
+// rows per wave instruction. Any other shape takes a generic two-pass path (one wave per row).
+#include "common.h"
+
+namespace pie {
+namespace {
+
+// A set of rows addressed as (token, head): offset = t*tok_stride + h*head_stride.
+struct RowSet {
+  const uint16_t* in;
+  const uint16_t* res;  // residual input (fused add only)
+  uint16_t* sum;        // residual output s (fused add only)
+  uint16_t* out;
+  const uint16_t* w;
+  int64_t in_ts, in_hs, res_ts, res_hs, sum_ts, sum_hs, out_ts, out_hs;
+  int64_t heads;  // rows = T * heads
+  int64_t rows;
+};
+
+struct NormArgs {
+  RowSet set[2];  // q and k for the per-head norm; set[1].rows == 0 otherwise
+  int64_t cols;
+  float eps;
+};
+
+__device__ __forceinline__ void row_offsets(const RowSet& s, int64_t r, int64_t& oi, int64_t& orr,
+                                            int64_t& os, int64_t& oo) {
+  int64_t t = r, h = 0;
+  if (s.heads != 1) {
+    if (r < 0x7fffffff && s.heads < 0x7fffffff) {
+      t = (uint32_t)r / (uint32_t)s.heads;
+    } else {
+      t = r / s.heads;
+    }
+    h = r - t * s.heads;
+  }
+  oi = t * s.in_ts + h * s.in_hs;
+  orr = t * s.res_ts + h * s.res_hs;
+  os = t * s.sum_ts + h * s.sum_hs;
+  oo = t * s.out_ts + h * s.out_hs;
+}
+
+// ---------------------------------------------------------------- one wave per row, NV*512 cols
+template <int NV, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_rows_reg(NormArgs a) {
+  const RowSet& s = a.set[0];
+  const int lane = threadIdx.x & 63;
+  const int64_t wave0 = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
+  if (wave0 >= s.rows) return;
+
+  uint4 wv[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) wv[j] = ld16(s.w + (lane + 64 * j) * 8);
+
+  for (int64_t r = wave0; r < s.rows; r += nwaves) {
+    int64_t oi, orr, os, oo;
+    row_offsets(s, r, oi, orr, os, oo);
+    uint4 xv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) xv[j] = ld_stream(s.in + oi + (lane + 64 * j) * 8);
+    if constexpr (ADD) {
+      uint4 rv[NV];
+#pragma unroll
+      for (int j = 0; j < NV; ++j) rv[j] = ld_stream(s.res + orr + (lane + 64 * j) * 8);
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        float xf[8], rf[8];
+        unpack8(xv[j], xf);
+        unpack8(rv[j], rf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[e] = rf[e] + xf[e];
+        xv[j] = pack8(xf);  // s rounded to bf16: the norm below reads the rounded values
+        st_stream(s.sum + os + (lane + 64 * j) * 8, xv[j]);
+      }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      float xf[8];
+      unpack8(xv[j], xf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += xf[e] * xf[e];
+    }
+    const float rstd = rsqrtf(wave_sum(ss) / (float)a.cols + a.eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      float xf[8], wf[8];
+      unpack8(xv[j], xf);
+      unpack8(wv[j], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xf[e] = (xf[e] * rstd) * wf[e];
+      st_stream(s.out + oo + (lane + 64 * j) * 8, pack8(xf));
+    }
+  }
+}
+
+// ---------------------------------------------------------------- 16 lanes per row (D = 16*EPL)
+// EPL elements per lane: 4 (D=64, 8-byte accesses), 8 (D=128), 16 (D=256, two vectors).
+template <int EPL>
+struct Chunk;
+template <>
+struct Chunk<4> {
+  uint2 v;
+  __device__ void load(const uint16_t* p) { v = *reinterpret_cast<const uint2*>(p); }
+  __device__ void store(uint16_t* p) const { *reinterpret_cast<uint2*>(p) = v; }
+  __device__ void get(float* f) const { f[0] = bf_lo(v.x); f[1] = bf_hi(v.x); f[2] = bf_lo(v.y); f[3] = bf_hi(v.y); }
+  __device__ void set(const float* f) { v.x = pack_bf2(f[0], f[1]); v.y = pack_bf2(f[2], f[3]); }
+};
+template <>
+struct Chunk<8> {
+  uint4 v;
+  __device__ void load(const uint16_t* p) { v = ld16(p); }
+  __device__ void store(uint16_t* p) const { st16(p, v); }
+  __device__ void get(float* f) const { unpack8(v, f); }
+  __device__ void set(const float* f) { v = pack8(f); }
+};
+template <>
+struct Chunk<16> {
+  uint4 v0, v1;
+  __device__ void load(const uint16_t* p) { v0 = ld16(p); v1 = ld16(p + 8); }
+  __device__ void store(uint16_t* p) const { st16(p, v0); st16(p + 8, v1); }
+  __device__ void get(float* f) const { unpack8(v0, f); unpack8(v1, f + 8); }
+  __device__ void set(const float* f) { v0 = pack8(f); v1 = pack8(f + 8); }
+};
+
+template <int EPL>
+__global__ __launch_bounds__(256) void rmsnorm_heads16(NormArgs a) {
+  const int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;  // 16-lane group
+  const int sub = threadIdx.x & 15;
+  const int64_t total = a.set[0].rows + a.set[1].rows;
+  // Every lane of a wave must reach the DPP reduction: rows past the end compute on zeros.
+  const bool live = g < total;
+  const int which = (live && g >= a.set[0].rows) ? 1 : 0;
+  const RowSet& s = a.set[which];
+  const int64_t r = which ? g - a.set[0].rows : g;
+  int64_t oi = 0, orr, os, oo = 0;
+  if (live) row_offsets(s, r, oi, orr, os, oo);
+
+  Chunk<EPL> c, wc;
+  float f[EPL], wf[EPL];
+  if (live) {
+    c.load(s.in + oi + sub * EPL);
+    wc.load(s.w + sub * EPL);
+    c.get(f);
+    wc.get(wf);
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) f[e] = wf[e] = 0.f;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) ss += f[e] * f[e];
+  const float rstd = rsqrtf(row16_sum(ss) / (float)a.cols + a.eps);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) f[e] = (f[e] * rstd) * wf[e];
+  if (live) {
+    c.set(f);
+    c.store(s.out + oo + sub * EPL);
+  }
+}
+
+// ---------------------------------------------------------------- generic: one wave per row
+// VEC = 8: 16-byte accesses (cols % 8 == 0, all rows 16-byte aligned); VEC = 1: scalar.
+// Pass 1 reads the row (and writes s), pass 2 re-reads it from cache and writes y.
+template <int VEC, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_rows_generic(NormArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave0 = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
+  const int64_t total = a.set[0].rows + a.set[1].rows;
+  const int64_t nv = a.cols / VEC;
+  for (int64_t g = wave0; g < total; g += nwaves) {
+    const int which = g >= a.set[0].rows ? 1 : 0;
+    const RowSet& s = a.set[which];
+    const int64_t r = which ? g - a.set[0].rows : g;
+    int64_t oi, orr, os, oo;
+    row_offsets(s, r, oi, orr, os, oo);
+    const uint16_t* src = ADD ? s.sum + os : s.in + oi;
+    float ss = 0.f;
+    for (int64_t j = lane; j < nv; j += 64) {
+      float f[VEC];
+      if constexpr (VEC == 8) {
+        uint4 xv = ld16(s.in + oi + j * 8);
+        unpack8(xv, f);
+        if constexpr (ADD) {
+          float rf[8];
+          unpack8(ld16(s.res + orr + j * 8), rf);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = rf[e] + f[e];
+          xv = pack8(f);
+          unpack8(xv, f);
+          st16(s.sum + os + j * 8, xv);
+        }
+      } else {
+        f[0] = bf1(s.in[oi + j]);
+        if constexpr (ADD) {
+          const uint16_t sv = to_bf1(bf1(s.res[orr + j]) + f[0]);
+          s.sum[os + j] = sv;
+          f[0] = bf1(sv);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) ss += f[e] * f[e];
+    }
+    const float rstd = rsqrtf(wave_sum(ss) / (float)a.cols + a.eps);
+    for (int64_t j = lane; j < nv; j += 64) {
+      if constexpr (VEC == 8) {
+        float f[8], wf[8];
+        unpack8(ld16(src + j * 8), f);
+        unpack8(ld16(s.w + j * 8), wf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = (f[e] * rstd) * wf[e];
+        st16(s.out + oo + j * 8, pack8(f));
+      } else {
+        s.out[oo + j] = to_bf1((bf1(src[j]) * rstd) * bf1(s.w[j]));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- host side
+int64_t wave_grid(int64_t rows) {
+  // 4 waves per 256-thread block; cap the grid so waves loop over rows (weights stay in
+  // registers) once the device is full many times over.
+  const int64_t blocks = (rows + 3) / 4;
+  const int64_t cap = (int64_t)num_cus() * 32;
+  return blocks < cap ? blocks : cap;
+}
+
+bool rowset_vec_ok(const RowSet& s, bool add) {
+  bool ok = aligned16(s.in) && aligned16(s.out) && aligned16(s.w) &&
+            s.in_ts % 8 == 0 && s.in_hs % 8 == 0 && s.out_ts % 8 == 0 && s.out_hs % 8 == 0;
+  if (add)
+    ok = ok && aligned16(s.res) && aligned16(s.sum) && s.res_ts % 8 == 0 &&
+         s.res_hs % 8 == 0 && s.sum_ts % 8 == 0 && s.sum_hs % 8 == 0;
+  return ok;
+}
+
+template <bool ADD>
+int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
+  const int64_t rows = a.set[0].rows + a.set[1].rows;
+  if (rows == 0) return PIE_HIP_OK;
+  const bool vec = a.cols % 8 == 0 && rowset_vec_ok(a.set[0], ADD) &&
+                   (a.set[1].rows == 0 || rowset_vec_ok(a.set[1], ADD));
+  const dim3 blk(256);
+  if (vec && a.set[1].rows == 0 && a.cols % 512 == 0 && a.cols <= 16 * 512) {
+    const dim3 grd((unsigned)wave_grid(rows));
+    switch (a.cols / 512) {
+#define PIE_NV(n) \
+  case n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, ADD>), grd, blk, 0, st, a); break;
+      PIE_NV(1) PIE_NV(2) PIE_NV(3) PIE_NV(4) PIE_NV(5) PIE_NV(6) PIE_NV(7) PIE_NV(8)
+      PIE_NV(9) PIE_NV(10) PIE_NV(11) PIE_NV(12) PIE_NV(13) PIE_NV(14) PIE_NV(15) PIE_NV(16)
+#undef PIE_NV
+    }
+    return check_launch(name);
+  }
+  if (!ADD && vec && (a.cols == 64 || a.cols == 128 || a.cols == 256)) {
+    const int64_t threads = rows * 16;
+    const dim3 grd((unsigned)((threads + 255) / 256));
+    if (a.cols == 64) hipLaunchKernelGGL(rmsnorm_heads16<4>, grd, blk, 0, st, a);
+    else if (a.cols == 128) hipLaunchKernelGGL(rmsnorm_heads16<8>, grd, blk, 0, st, a);
+    else hipLaunchKernelGGL(rmsnorm_heads16<16>, grd, blk, 0, st, a);
+    return check_launch(name);
+  }
+  const dim3 grd((unsigned)wave_grid(rows));
+  if (vec) hipLaunchKernelGGL((rmsnorm_rows_generic<8, ADD>), grd, blk, 0, st, a);
+  else hipLaunchKernelGGL((rmsnorm_rows_generic<1, ADD>), grd, blk, 0, st, a);
+  return check_launch(name);
+}
+
+}  // namespace
+}  // namespace pie
+
+using namespace pie;
+
+extern "C" int pie_hip_rmsnorm(const pie_bf16* x, int64_t x_row_stride, const pie_bf16* w,
+                               pie_bf16* y, int64_t y_row_stride, int64_t rows, int64_t cols,
+                               float eps, void* stream) {
+  PIE_REQUIRE(rows >= 0 && cols > 0, "rmsnorm: bad shape rows=%lld cols=%lld", (long long)rows, (long long)cols);
+  if (rows == 0) return PIE_HIP_OK;
+  PIE_REQUIRE(x && w && y, "rmsnorm: null pointer");
+  PIE_REQUIRE(x_row_stride >= cols && y_row_stride >= cols, "rmsnorm: row stride smaller than cols");
+  NormArgs a{};
+  a.set[0] = RowSet{x, nullptr, nullptr, y, w, x_row_stride, 0, 0, 0, 0, 0, y_row_stride, 0, 1, rows};
+  a.cols = cols;
+  a.eps = eps;
+  return launch_rows<false>(a, (hipStream_t)stream, "rmsnorm");
+}
+
+extern "C" int pie_hip_fused_add_rmsnorm(const pie_bf16* x, int64_t x_row_stride,
+                                         const pie_bf16* r, int64_t r_row_stride,
+                                         pie_bf16* s, int64_t s_row_stride,
+                                         pie_bf16* y, int64_t y_row_stride,
+                                         const pie_bf16* w, int64_t rows, int64_t cols,
+                                         float eps, void* stream) {
+  PIE_REQUIRE(rows >= 0 && cols > 0, "fused_add_rmsnorm: bad shape rows=%lld cols=%lld", (long long)rows, (long long)cols);
+  if (rows == 0) return PIE_HIP_OK;
+  PIE_REQUIRE(x && r && s && y && w, "fused_add_rmsnorm: null pointer");
+  PIE_REQUIRE(x_row_stride >= cols && r_row_stride >= cols && s_row_stride >= cols && y_row_stride >= cols,
+              "fused_add_rmsnorm: row stride smaller than cols");
+  NormArgs a{};
+  a.set[0] = RowSet{x, r, s, y, w, x_row_stride, 0, r_row_stride, 0, s_row_stride, 0, y_row_stride, 0, 1, rows};
+  a.cols = cols;
+  a.eps = eps;
+  return launch_rows<true>(a, (hipStream_t)stream, "fused_add_rmsnorm");
+}
+
+extern "C" int pie_hip_qk_rmsnorm(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                  pie_bf16* q_out, int64_t qo_tok_stride, int64_t qo_head_stride,
+                                  const pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                                  pie_bf16* k_out, int64_t ko_tok_stride, int64_t ko_head_stride,
+                                  const pie_bf16* qw, const pie_bf16* kw, int64_t T, int64_t Hq,
+                                  int64_t Hkv, int64_t D, float eps, void* stream) {
+  PIE_REQUIRE(T >= 0 && Hq >= 0 && Hkv >= 0 && D > 0, "qk_rmsnorm: bad shape");
+  if (T == 0 || Hq + Hkv == 0) return PIE_HIP_OK;
+  PIE_REQUIRE(Hq == 0 || (q && q_out && qw), "qk_rmsnorm: null q pointer");
+  PIE_REQUIRE(Hkv == 0 || (k && k_out && kw), "qk_rmsnorm: null k pointer");
+  NormArgs a{};
+  a.set[0] = RowSet{q, nullptr, nullptr, q_out, qw, q_tok_stride, q_head_stride, 0, 0, 0, 0,
+                    qo_tok_stride, qo_head_stride, Hq ? Hq : 1, Hq ? T * Hq : 0};
+  a.set[1] = RowSet{k, nullptr, nullptr, k_out, kw, k_tok_stride, k_head_stride, 0, 0, 0, 0,
+                    ko_tok_stride, ko_head_stride, Hkv ? Hkv : 1, Hkv ? T * Hkv : 0};
+  if (Hq == 0) { a.set[0] = a.set[1]; a.set[1] = RowSet{}; }
+  a.cols = D;
+  a.eps = eps;
+  return launch_rows<false>(a, (hipStream_t)stream, "qk_rmsnorm");
+}

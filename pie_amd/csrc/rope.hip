@@ -1,0 +1,355 @@
+// RoPE on ragged q/k (in place) and the paged KV append, separately and fused, for gfx950.
+//
+// RoPE semantics: pie/src/flashinfer_metal/kernels/metal_rope.metal:26-107 (the in-repo
+// restatement of flashinfer.apply_rope_pos_ids_inplace / apply_llama31_rope_pos_ids_inplace,
+// called at pie/src/pie_worker/model/llama3.py:660-669 and qwen3.py:665-670):
+//   angle_i = float(pos[t]) * inv_freq[i];  x' = x cos - y sin;  y' = x sin + y cos
+// with (x, y) = (v[i], v[i + rd/2]) (interleave = 0) or (v[2i], v[2i+1]) (interleave = 1),
+// fp32 math, bf16 in/out. inv_freq is computed on the host in float64 (capi.hip).
+//
+// Append semantics: pie/src/flashinfer_metal/kernels/metal_append_paged_kv_cache.metal:23-107
+// (flashinfer.append_paged_kv_cache at llama3.py:675-685): token t goes to slot p % P of page
+// kv_indices[kv_indptr[b] + p / P]; tokens with an out-of-range batch index, logical page or
+// physical page are skipped.
+//
+// Mapping. A group of W wavefronts owns one token (W = 1, 2 or 4; a 256-thread block holds
+// 4/W tokens). The group first stages the token's cos/sin table (rd/2 angles) in LDS, one
+// sincos per pair, shared by all Hq+Hkv heads. Then every lane walks 16-byte units:
+//   q/k rope units: 8 pairs of one head (x chunk + y chunk, interleave = 0) or 4 pairs
+//                   (one chunk, interleave = 1), rotated in registers and stored back;
+//   k rope units in the fused kernel are also stored to the cache page (k is already in
+//   registers, so the append costs no extra read of k);
+//   k tail units (dims >= rd) and v units: 16-byte copies into the cache page.
+// A token's Hkv*D row in a page is contiguous for NHD, so the 64 lanes of a wave write whole
+// 1 KiB runs of a page: the scatter is coalesced per (page, slot).
+#include "common.h"
+
+namespace pie {
+namespace {
+
+constexpr int kMaxPairs = 256;
+
+struct HeadsDesc {
+  uint16_t* q;
+  uint16_t* k;
+  const uint16_t* v;
+  int64_t q_ts, q_hs, k_ts, k_hs, v_ts, v_hs;
+  int32_t Hq, Hkv, D, rd;
+};
+
+struct CacheDesc {
+  const int32_t* batch_indices;
+  const int32_t* positions;
+  const int32_t* kv_indices;
+  const int32_t* kv_indptr;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int64_t batch_size, num_pages, page_stride, slot_stride, head_stride;
+  int32_t page_size;
+};
+
+struct RopeAppendArgs {
+  HeadsDesc h;
+  CacheDesc c;
+  const int32_t* pos;
+  int64_t T;
+  int32_t wpt;         // waves per token (vector kernel)
+  int32_t interleave;  // pair layout (scalar kernel)
+  float inv_freq[kMaxPairs];
+};
+
+// Cache element offset of (token's page, slot), or -1 when the token is skipped.
+__device__ __forceinline__ int64_t slot_offset(const CacheDesc& c, int64_t t) {
+  const int b = c.batch_indices[t];
+  const int p = c.positions[t];
+  if (b < 0 || (int64_t)b >= c.batch_size || p < 0) return -1;
+  const int lo = c.kv_indptr[b], hi = c.kv_indptr[b + 1];
+  const int64_t logical = (int64_t)lo + p / c.page_size;
+  if (logical >= hi) return -1;
+  const int page = c.kv_indices[logical];
+  if (page < 0 || (int64_t)page >= c.num_pages) return -1;
+  return (int64_t)page * c.page_stride + (int64_t)(p % c.page_size) * c.slot_stride;
+}
+
+template <bool ROPE, bool APPEND, bool INTERLEAVE>
+__global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
+  __shared__ float2 tab[4][ROPE ? kMaxPairs : 1];
+  const int wpt = a.wpt;
+  const int tpb = 4 / wpt;
+  const int slot = (threadIdx.x >> 6) / wpt;               // token slot in block
+  const int gt = threadIdx.x - slot * wpt * 64;           // thread id inside the token group
+  const int gsize = wpt * 64;
+  const int64_t t = (int64_t)blockIdx.x * tpb + slot;
+  const bool live = t < a.T;
+  const HeadsDesc& h = a.h;
+  const int half = h.rd >> 1;
+
+  if constexpr (ROPE) {
+    if (live) {
+      const float p = (float)a.pos[t];
+      for (int i = gt; i < half; i += gsize) {
+        float sn, cs;
+        sincosf(p * a.inv_freq[i], &sn, &cs);
+        tab[slot][i] = make_float2(cs, sn);
+      }
+    }
+    __syncthreads();
+  }
+  if (!live) return;
+
+  int64_t kc = -1;
+  if constexpr (APPEND) kc = slot_offset(a.c, t);
+
+  const int uph = ROPE ? (INTERLEAVE ? h.rd >> 3 : h.rd >> 4) : 0;  // rope units per head
+  const int nq = ROPE ? h.Hq * uph : 0;
+  const int nk = ROPE ? h.Hkv * uph : 0;
+  const int tail = (h.D - (ROPE ? h.rd : 0)) >> 3;                 // k chunks past rd
+  const int nkt = APPEND ? h.Hkv * tail : 0;
+  const int dv = h.D >> 3;
+  const int nv = APPEND ? h.Hkv * dv : 0;
+  const int total = nq + nk + nkt + nv;
+  const float2* tb = tab[slot];
+
+  for (int u = gt; u < total; u += gsize) {
+    if (ROPE && u < nq + nk) {
+      const bool isq = u < nq;
+      const int uu = isq ? u : u - nq;
+      const int head = uu / uph, c = uu - head * uph;
+      uint16_t* base = isq ? h.q + t * h.q_ts + (int64_t)head * h.q_hs
+                           : h.k + t * h.k_ts + (int64_t)head * h.k_hs;
+      if constexpr (!INTERLEAVE) {
+        uint16_t* px = base + c * 8;
+        uint16_t* py = px + half;
+        float x[8], y[8];
+        unpack8(ld16(px), x);
+        unpack8(ld16(py), y);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float2 cs = tb[c * 8 + e];
+          const float xr = x[e] * cs.x - y[e] * cs.y;
+          const float yr = x[e] * cs.y + y[e] * cs.x;
+          x[e] = xr;
+          y[e] = yr;
+        }
+        const uint4 xo = pack8(x), yo = pack8(y);
+        st16(px, xo);
+        st16(py, yo);
+        if (APPEND && !isq && kc >= 0) {
+          uint16_t* dst = a.c.k_cache + kc + (int64_t)head * a.c.head_stride + c * 8;
+          st_stream(dst, xo);
+          st_stream(dst + half, yo);
+        }
+      } else {
+        uint16_t* px = base + c * 8;
+        float f[8];
+        unpack8(ld16(px), f);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const float2 cs = tb[c * 4 + m];
+          const float xr = f[2 * m] * cs.x - f[2 * m + 1] * cs.y;
+          const float yr = f[2 * m] * cs.y + f[2 * m + 1] * cs.x;
+          f[2 * m] = xr;
+          f[2 * m + 1] = yr;
+        }
+        const uint4 o = pack8(f);
+        st16(px, o);
+        if (APPEND && !isq && kc >= 0)
+          st_stream(a.c.k_cache + kc + (int64_t)head * a.c.head_stride + c * 8, o);
+      }
+      continue;
+    }
+    if constexpr (APPEND) {
+      if (kc < 0) break;
+      int uu = u - nq - nk;
+      if (uu < nkt) {
+        const int head = uu / tail, c = uu - head * tail;
+        const int d = (ROPE ? h.rd : 0) + c * 8;
+        const uint4 v = ld_stream(h.k + t * h.k_ts + (int64_t)head * h.k_hs + d);
+        st_stream(a.c.k_cache + kc + (int64_t)head * a.c.head_stride + d, v);
+      } else {
+        uu -= nkt;
+        const int head = uu / dv, c = uu - head * dv;
+        const uint4 v = ld_stream(h.v + t * h.v_ts + (int64_t)head * h.v_hs + c * 8);
+        st_stream(a.c.v_cache + kc + (int64_t)head * a.c.head_stride + c * 8, v);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- scalar fallbacks
+// Any alignment, any D / rd: one thread per (token, head, pair) or (token, head, element).
+__global__ __launch_bounds__(256) void rope_scalar(RopeAppendArgs a) {
+  const HeadsDesc& h = a.h;
+  const int half = h.rd >> 1;
+  const int64_t per_tok = (int64_t)(h.Hq + h.Hkv) * half;
+  const int64_t n = a.T * per_tok;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / per_tok;
+    const int rem = (int)(i - t * per_tok);
+    const int head = rem / half, pr = rem - head * half;
+    uint16_t* base = head < h.Hq ? h.q + t * h.q_ts + (int64_t)head * h.q_hs
+                                 : h.k + t * h.k_ts + (int64_t)(head - h.Hq) * h.k_hs;
+    uint16_t* px = base + (a.interleave ? 2 * pr : pr);
+    uint16_t* py = base + (a.interleave ? 2 * pr + 1 : pr + half);
+    float sn, cs;
+    sincosf((float)a.pos[t] * a.inv_freq[pr], &sn, &cs);
+    const float x = bf1(*px), y = bf1(*py);
+    *px = to_bf1(x * cs - y * sn);
+    *py = to_bf1(x * sn + y * cs);
+  }
+}
+
+__global__ __launch_bounds__(256) void append_scalar(RopeAppendArgs a) {
+  const HeadsDesc& h = a.h;
+  const int64_t per_tok = (int64_t)h.Hkv * h.D;
+  const int64_t n = a.T * per_tok;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / per_tok;
+    const int rem = (int)(i - t * per_tok);
+    const int head = rem / h.D, d = rem - head * h.D;
+    const int64_t kc = slot_offset(a.c, t);
+    if (kc < 0) continue;
+    const int64_t o = kc + (int64_t)head * a.c.head_stride + d;
+    a.c.k_cache[o] = h.k[t * h.k_ts + (int64_t)head * h.k_hs + d];
+    a.c.v_cache[o] = h.v[t * h.v_ts + (int64_t)head * h.v_hs + d];
+  }
+}
+
+// ---------------------------------------------------------------- host side
+bool heads_vec_ok(const uint16_t* p, int64_t ts, int64_t hs) {
+  return aligned16(p) && ts % 8 == 0 && hs % 8 == 0;
+}
+
+int pick_wpt(int64_t T) { return T >= 8192 ? 1 : (T >= 2048 ? 2 : 4); }
+
+int launch(RopeAppendArgs& a, bool rope, bool append, int interleave, hipStream_t st,
+           const char* name) {
+  if (a.T == 0) return PIE_HIP_OK;
+  const HeadsDesc& h = a.h;
+  bool vec = h.D % 8 == 0 && (interleave ? h.rd % 8 == 0 : h.rd % 16 == 0);
+  if (rope) vec = vec && (h.Hq == 0 || heads_vec_ok(h.q, h.q_ts, h.q_hs)) &&
+                  (h.Hkv == 0 || heads_vec_ok(h.k, h.k_ts, h.k_hs));
+  if (append)
+    vec = vec && heads_vec_ok(h.k, h.k_ts, h.k_hs) && heads_vec_ok(h.v, h.v_ts, h.v_hs) &&
+          aligned16(a.c.k_cache) && aligned16(a.c.v_cache) && a.c.page_stride % 8 == 0 &&
+          a.c.slot_stride % 8 == 0 && a.c.head_stride % 8 == 0;
+  if (vec) {
+    a.wpt = pick_wpt(a.T);
+    const int tpb = 4 / a.wpt;
+    const dim3 grd((unsigned)((a.T + tpb - 1) / tpb)), blk(256);
+#define PIE_RA(R, A, I) hipLaunchKernelGGL((rope_append_vec<R, A, I>), grd, blk, 0, st, a)
+    if (rope && append) { if (interleave) PIE_RA(true, true, true); else PIE_RA(true, true, false); }
+    else if (rope) { if (interleave) PIE_RA(true, false, true); else PIE_RA(true, false, false); }
+    else PIE_RA(false, true, false);
+#undef PIE_RA
+    return check_launch(name);
+  }
+  const dim3 blk(256);
+  const int64_t cap = (int64_t)num_cus() * 64;
+  if (rope && (h.Hq + h.Hkv) > 0 && h.rd > 0) {
+    a.interleave = interleave;
+    const int64_t n = a.T * (h.Hq + h.Hkv) * (h.rd / 2);
+    const int64_t b = (n + 255) / 256;
+    hipLaunchKernelGGL(rope_scalar, dim3((unsigned)(b < cap ? b : cap)), blk, 0, st, a);
+    int rc = check_launch(name);
+    if (rc) return rc;
+  }
+  if (append && h.Hkv > 0) {
+    const int64_t n = a.T * h.Hkv * h.D;
+    const int64_t b = (n + 255) / 256;
+    hipLaunchKernelGGL(append_scalar, dim3((unsigned)(b < cap ? b : cap)), blk, 0, st, a);
+    return check_launch(name);
+  }
+  return PIE_HIP_OK;
+}
+
+int fill_heads(RopeAppendArgs& a, pie_bf16* q, int64_t qts, int64_t qhs, pie_bf16* k, int64_t kts,
+               int64_t khs, const pie_bf16* v, int64_t vts, int64_t vhs, int64_t T, int64_t Hq,
+               int64_t Hkv, int64_t D, int64_t rd) {
+  PIE_REQUIRE(T >= 0 && T < (1ll << 31), "rope/append: bad token count %lld", (long long)T);
+  PIE_REQUIRE(Hq >= 0 && Hkv >= 0 && Hq + Hkv < (1 << 20) && D > 0 && D < (1 << 16),
+              "rope/append: bad head shape Hq=%lld Hkv=%lld D=%lld", (long long)Hq, (long long)Hkv, (long long)D);
+  PIE_REQUIRE(rd >= 0 && rd <= D && rd % 2 == 0 && rd / 2 <= kMaxPairs,
+              "rope: rotary_dim=%lld must be even, <= head_dim=%lld and <= %d", (long long)rd,
+              (long long)D, 2 * kMaxPairs);
+  a.h = HeadsDesc{q, k, v, qts, qhs, kts, khs, vts, vhs, (int32_t)Hq, (int32_t)Hkv, (int32_t)D, (int32_t)rd};
+  a.T = T;
+  return PIE_HIP_OK;
+}
+
+int fill_cache(RopeAppendArgs& a, const int32_t* bidx, const int32_t* pos, const int32_t* kv_indices,
+               const int32_t* kv_indptr, int64_t B, pie_bf16* kc, pie_bf16* vc, int64_t num_pages,
+               int64_t ps, int64_t ss, int64_t hs, int64_t P) {
+  PIE_REQUIRE(B >= 0 && num_pages >= 0 && P > 0 && P < (1 << 30), "append: bad batch/page shape");
+  PIE_REQUIRE(a.T == 0 || (bidx && pos && kv_indptr && kc && vc && (kv_indices || num_pages == 0)),
+              "append: null pointer");
+  PIE_REQUIRE(ps >= 0 && ss >= 0 && hs >= 0, "append: negative cache stride");
+  a.c = CacheDesc{bidx, pos, kv_indices, kv_indptr, kc, vc, B, num_pages, ps, ss, hs, (int32_t)P};
+  return PIE_HIP_OK;
+}
+
+}  // namespace
+}  // namespace pie
+
+using namespace pie;
+
+extern "C" int pie_hip_rope_inplace(pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                    pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                                    const int32_t* pos, int64_t T, int64_t Hq, int64_t Hkv,
+                                    int64_t D, int64_t rotary_dim, int interleave,
+                                    const float* inv_freq, void* stream) {
+  RopeAppendArgs a{};
+  int rc = fill_heads(a, q, q_tok_stride, q_head_stride, k, k_tok_stride, k_head_stride, nullptr,
+                      0, 0, T, Hq, Hkv, D, rotary_dim);
+  if (rc) return rc;
+  if (T == 0 || Hq + Hkv == 0 || rotary_dim == 0) return PIE_HIP_OK;
+  PIE_REQUIRE(pos && inv_freq && (Hq == 0 || q) && (Hkv == 0 || k), "rope: null pointer");
+  for (int64_t i = 0; i < rotary_dim / 2; ++i) a.inv_freq[i] = inv_freq[i];
+  return launch(a, true, false, interleave ? 1 : 0, (hipStream_t)stream, "rope_inplace");
+}
+
+extern "C" int pie_hip_paged_kv_append(const pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                                       const pie_bf16* v, int64_t v_tok_stride, int64_t v_head_stride,
+                                       const int32_t* batch_indices, const int32_t* positions,
+                                       const int32_t* kv_indices, const int32_t* kv_indptr,
+                                       int64_t batch_size, pie_bf16* k_cache, pie_bf16* v_cache,
+                                       int64_t num_pages, int64_t page_stride, int64_t slot_stride,
+                                       int64_t head_stride, int64_t page_size, int64_t T,
+                                       int64_t Hkv, int64_t D, void* stream) {
+  RopeAppendArgs a{};
+  int rc = fill_heads(a, nullptr, 0, 0, const_cast<pie_bf16*>(k), k_tok_stride, k_head_stride, v,
+                      v_tok_stride, v_head_stride, T, 0, Hkv, D, 0);
+  if (rc) return rc;
+  rc = fill_cache(a, batch_indices, positions, kv_indices, kv_indptr, batch_size, k_cache, v_cache,
+                  num_pages, page_stride, slot_stride, head_stride, page_size);
+  if (rc) return rc;
+  if (T == 0 || Hkv == 0) return PIE_HIP_OK;
+  PIE_REQUIRE(k && v, "append: null k/v");
+  return launch(a, false, true, 0, (hipStream_t)stream, "paged_kv_append");
+}
+
+extern "C" int pie_hip_rope_append(pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                   pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                                   const pie_bf16* v, int64_t v_tok_stride, int64_t v_head_stride,
+                                   const int32_t* pos, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                                   int64_t rotary_dim, int interleave, const float* inv_freq,
+                                   const int32_t* batch_indices, const int32_t* positions,
+                                   const int32_t* kv_indices, const int32_t* kv_indptr,
+                                   int64_t batch_size, pie_bf16* k_cache, pie_bf16* v_cache,
+                                   int64_t num_pages, int64_t page_stride, int64_t slot_stride,
+                                   int64_t head_stride, int64_t page_size, void* stream) {
+  RopeAppendArgs a{};
+  int rc = fill_heads(a, q, q_tok_stride, q_head_stride, k, k_tok_stride, k_head_stride, v,
+                      v_tok_stride, v_head_stride, T, Hq, Hkv, D, rotary_dim);
+  if (rc) return rc;
+  rc = fill_cache(a, batch_indices, positions, kv_indices, kv_indptr, batch_size, k_cache, v_cache,
+                  num_pages, page_stride, slot_stride, head_stride, page_size);
+  if (rc) return rc;
+  if (T == 0 || Hq + Hkv == 0) return PIE_HIP_OK;
+  PIE_REQUIRE(pos && inv_freq && (Hq == 0 || q) && (Hkv == 0 || (k && v)), "rope_append: null pointer");
+  for (int64_t i = 0; i < rotary_dim / 2; ++i) a.inv_freq[i] = inv_freq[i];
+  if (rotary_dim == 0) return launch(a, false, true, 0, (hipStream_t)stream, "rope_append");
+  return launch(a, true, Hkv > 0, interleave ? 1 : 0, (hipStream_t)stream, "rope_append");
+}

@@ -1,0 +1,331 @@
+"""Pins the CPU oracle (oracle/oracle.c) to independent sources of truth. CPU only.
+
+a1/a2/a3 RMSNorm, a2 residual add, a4 SiLU-and-mul, a5 embedding: the reference runs these as
+torch ops (pie/src/pie_worker/model/llama3.py:555, :586, :569-572, :471), so torch-CPU running
+the very same expressions is the reference implementation; it is compared here.
+a6/a7 RoPE: flashinfer is absent (an external wheel, no network), so the frequency rule is
+pinned to transformers' Llama-3 rope parameters and the rotation to HF's rotate-half form in
+float64, plus closed-form invariants. a8 append and a9 index helpers: brute-force Python loops
+restating pie/src/flashinfer_metal/ops.py:392-436 and metal_append_paged_kv_cache.metal:51-103.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from pie_amd import workloads as wl
+from tests._util import assert_bf16_close, assert_bits_equal, ulp_diff
+
+N, T_ = oracle.to_np, oracle.to_torch
+
+
+# ----------------------------------------------------------------------------- bf16 rounding
+def test_bf16_rounding_matches_torch():
+    g = torch.Generator().manual_seed(0)
+    x = torch.cat([torch.randn(100000, generator=g) * 10 ** torch.randint(-30, 30, (100000,), generator=g),
+                   torch.tensor([0.0, -0.0, float("inf"), -float("inf"), 1e-40, 3.4e38, 65504.0])])
+    want = x.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert_bits_equal(oracle.f32_to_bf16(x.numpy()), want, "vectorised f32->bf16")
+    lib = oracle._load()
+    got = np.array([lib.oracle_f32_to_bf16(float(v)) for v in x.numpy()[:2000]], dtype=np.uint16)
+    assert_bits_equal(got, want[:2000], "C f32->bf16")
+
+
+def test_f64_to_bf16_single_rounding():
+    lib = oracle._load()
+    # 1 + 2^-8 is a bf16 tie; a hair above must round up even though fp32 would land on the tie
+    assert lib.oracle_f64_to_bf16(1.0 + 2.0 ** -8 + 2.0 ** -40) == 0x3F81
+    assert lib.oracle_f64_to_bf16(1.0 + 2.0 ** -8 - 2.0 ** -40) == 0x3F80
+    assert lib.oracle_f64_to_bf16(1.0 + 2.0 ** -8) == 0x3F80  # exact tie: to even
+
+
+# ----------------------------------------------------------------------------- RMSNorm
+@pytest.mark.parametrize("T,H,eps", [(64, 2048, 1e-5), (17, 4096, 1e-6), (5, 896, 1e-6), (9, 100, 1e-5)])
+def test_rmsnorm_vs_torch(T, H, eps):
+    x, w = wl.normal((T, H), 1), wl.normal((H,), 2, 1.0, 0.1)
+    want = F.rms_norm(x, [H], w, eps)
+    got = oracle.rmsnorm(N(x), N(w), eps)
+    assert ulp_diff(got, N(want)).max() <= 1
+    assert_bf16_close(got, N(want), what="rmsnorm")
+
+
+def test_rmsnorm_invariants():
+    H = 512
+    x = wl.normal((8, H), 3)
+    w = wl.normal((H,), 4, 1.0, 0.1)
+    y = oracle.bf16_to_f32(oracle.rmsnorm(N(x), N(w), 1e-6))
+    # scale invariance: y(4x) == y(x) when eps << mean square (4 is exact in bf16)
+    y4 = oracle.bf16_to_f32(oracle.rmsnorm(N(x * 4), N(w), 1e-6))
+    np.testing.assert_allclose(y4, y, rtol=1e-2, atol=1e-2)
+    # constant row c -> w * sign(c)
+    c = torch.full((1, H), -3.0).to(torch.bfloat16)
+    yc = oracle.bf16_to_f32(oracle.rmsnorm(N(c), N(w), 1e-6))
+    np.testing.assert_allclose(yc[0], -oracle.bf16_to_f32(N(w)), rtol=1e-2)
+    # zero row -> zeros
+    z = torch.zeros((1, H), dtype=torch.bfloat16)
+    assert (oracle.bf16_to_f32(oracle.rmsnorm(N(z), N(w), 1e-6)) == 0).all()
+    # rows are independent
+    y_first = oracle.rmsnorm(N(x[:1]), N(w), 1e-6)
+    assert_bits_equal(y_first, oracle.rmsnorm(N(x), N(w), 1e-6)[:1])
+    # mean of squares of the normalised row (w = 1) is 1
+    ones = torch.ones(H, dtype=torch.bfloat16)
+    yn = oracle.bf16_to_f32(oracle.rmsnorm(N(x), N(ones), 0.0)).astype(np.float64)
+    np.testing.assert_allclose((yn ** 2).mean(-1), 1.0, rtol=1e-2)
+
+
+def test_per_head_rmsnorm_vs_torch():
+    c = wl.cfg5(B=16, V=64)
+    q, k, _ = wl.split_qkv(c["qkv"], 32, 8, 128)
+    want_q = F.rms_norm(q, [128], c["q_norm"], 1e-6)
+    got = oracle.rmsnorm(N(q), N(c["q_norm"]), 1e-6)
+    assert ulp_diff(got, N(want_q)).max() <= 1
+    want_k = F.rms_norm(k, [128], c["k_norm"], 1e-6)
+    assert ulp_diff(oracle.rmsnorm(N(k), N(c["k_norm"]), 1e-6), N(want_k)).max() <= 1
+
+
+def test_add_rmsnorm_vs_torch():
+    c = wl.cfg2(T=48, H=4096, I=64)
+    s_want = c["r"] + c["x"]
+    y_want = F.rms_norm(s_want, [4096], c["w"], 1e-5)
+    y, s = oracle.add_rmsnorm(N(c["x"]), N(c["r"]), N(c["w"]), 1e-5)
+    assert_bits_equal(s, N(s_want), "residual sum (bit-exact)")
+    assert ulp_diff(y, N(y_want)).max() <= 1
+
+
+# ----------------------------------------------------------------------------- SiLU-and-mul
+def test_silu_and_mul_vs_torch():
+    c = wl.cfg2(T=32, H=8, I=1536)
+    g, u = torch.split(c["gate_up"], [1536, 1536], -1)
+    want = F.silu(g) * u
+    got = oracle.silu_and_mul(N(c["gate_up"]), mode=0)
+    assert ulp_diff(got, N(want)).max() <= 1
+    assert (got == N(want)).mean() > 0.999
+    # single-rounding form stays inside the stated tolerance of torch's double rounding
+    assert_bf16_close(oracle.silu_and_mul(N(c["gate_up"]), mode=1), N(want), what="silu 1-round")
+
+
+def test_silu_special_values():
+    g = torch.tensor([0.0, 20.0, -20.0, 1.0], dtype=torch.bfloat16)
+    u = torch.tensor([3.0, 2.0, 5.0, 1.0], dtype=torch.bfloat16)
+    out = oracle.bf16_to_f32(oracle.silu_and_mul(N(torch.cat([g, u])[None])))[0]
+    assert out[0] == 0.0
+    assert out[1] == 40.0          # silu(g) == g for g >> 0
+    assert abs(out[2]) < 1e-6      # silu(g) ~ 0 for g << 0
+    assert abs(out[3] - 1.0 / (1.0 + math.exp(-1.0))) < 4e-3
+
+
+# ----------------------------------------------------------------------------- embedding
+def test_embedding_vs_torch():
+    c = wl.cfg4(V=1000, H=64, T=300)
+    got, bad = oracle.embedding(N(c["ids"]), N(c["W"]))
+    assert bad == 0
+    assert_bits_equal(got, N(F.embedding(c["ids"], c["W"])), "embedding")
+
+
+def test_embedding_out_of_range_rows_are_zero():
+    W = wl.normal((10, 16), 1)
+    ids = torch.tensor([0, 10, -1, 9], dtype=torch.int32)
+    got, bad = oracle.embedding(N(ids), N(W))
+    assert bad == 2
+    assert (got[1] == 0).all() and (got[2] == 0).all()
+    assert_bits_equal(got[[0, 3]], N(W)[[0, 9]])
+
+
+# ----------------------------------------------------------------------------- RoPE
+def _hf_llama3_inv_freq(D, theta, factor, lo, hi, L):
+    from transformers import LlamaConfig
+    from transformers.modeling_rope_utils import ROPE_INIT_FUNCTIONS
+    cfg = LlamaConfig(hidden_size=D * 4, num_attention_heads=4, head_dim=D,
+                      rope_parameters=dict(rope_type="llama3", rope_theta=theta, factor=factor,
+                                           low_freq_factor=lo, high_freq_factor=hi,
+                                           original_max_position_embeddings=L))
+    f, _ = ROPE_INIT_FUNCTIONS["llama3"](cfg, "cpu")
+    return f.double().numpy()
+
+
+@pytest.mark.parametrize("theta,factor", [(5e5, 8.0), (5e5, 32.0), (1e4, 4.0)])
+def test_llama31_inv_freq_vs_transformers(theta, factor):
+    want = _hf_llama3_inv_freq(128, theta, factor, 1.0, 4.0, 8192)
+    got = oracle.inv_freq_llama31(128, factor, theta, 1.0, 4.0, 8192)
+    np.testing.assert_allclose(got, want, rtol=2e-6)  # transformers evaluates in fp32
+    # all three bands occur for the Llama-3 constants
+    base = oracle.inv_freq_std(128, 1.0, theta)
+    assert (got == base).any() and np.isclose(got, base / factor).any()
+
+
+def test_llama31_reduces_to_standard_when_unscaled():
+    np.testing.assert_allclose(oracle.inv_freq_llama31(128, 1.0, 5e5, 1.0, 4.0, 8192),
+                               oracle.inv_freq_std(128, 1.0, 5e5), rtol=1e-15)
+
+
+def test_standard_inv_freq_closed_form():
+    f = oracle.inv_freq_std(64, 2.0, 1e6)
+    assert f[0] == 0.5
+    np.testing.assert_allclose(f, 0.5 * 1e6 ** (-np.arange(0, 64, 2) / 64), rtol=1e-14)
+
+
+def _hf_rotate_half(x, pos, inv_freq, interleave=False):
+    """HF apply_rotary_pos_emb in float64 on [T,H,D] (rotate_half; interleaved via reshape)."""
+    x = x.double()
+    ang = pos.double()[:, None] * torch.from_numpy(inv_freq)[None, :]
+    cos, sin = torch.cos(ang)[:, None, :], torch.sin(ang)[:, None, :]
+    if interleave:
+        x1, x2 = x[..., 0::2], x[..., 1::2]
+        out = torch.empty_like(x)
+        out[..., 0::2] = x1 * cos - x2 * sin
+        out[..., 1::2] = x2 * cos + x1 * sin
+        return out
+    cos, sin = torch.cat([cos, cos], -1), torch.cat([sin, sin], -1)
+    x1, x2 = x[..., : x.shape[-1] // 2], x[..., x.shape[-1] // 2:]
+    return x * cos + torch.cat([-x2, x1], -1) * sin
+
+
+@pytest.mark.parametrize("interleave", [False, True])
+def test_rope_vs_hf_rotate_half(interleave):
+    T, Hq, Hkv, D = 40, 4, 2, 128
+    q, k = wl.normal((T, Hq, D), 1), wl.normal((T, Hkv, D), 2)
+    pos = torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(3)).to(torch.int32)
+    f = oracle.inv_freq_llama31(D, 8.0, 5e5, 1.0, 4.0, 8192)
+    gq, gk = oracle.rope(N(q), N(k), N(pos), f, interleave=interleave)
+    wq = _hf_rotate_half(q, pos, f, interleave).float().to(torch.bfloat16)
+    wk = _hf_rotate_half(k, pos, f, interleave).float().to(torch.bfloat16)
+    assert ulp_diff(gq, N(wq)).max() <= 1
+    assert ulp_diff(gk, N(wk)).max() <= 1
+
+
+def test_rope_partial_rotary_dim_leaves_tail():
+    T, H, D, rd = 6, 2, 128, 64
+    q, k = wl.normal((T, H, D), 4), wl.normal((T, H, D), 5)
+    pos = torch.arange(T, dtype=torch.int32) * 100
+    f = oracle.inv_freq_std(rd, 1.0, 1e4)
+    gq, _ = oracle.rope(N(q), N(k), N(pos), f, rotary_dim=rd)
+    assert_bits_equal(gq[..., rd:], N(q)[..., rd:], "tail untouched")
+    wq = _hf_rotate_half(q[..., :rd], pos, f).float().to(torch.bfloat16)
+    assert ulp_diff(gq[..., :rd], N(wq)).max() <= 1
+
+
+def test_rope_invariants():
+    T, H, D = 16, 3, 128
+    q, k = wl.normal((T, H, D), 6), wl.normal((T, H, D), 7)
+    f = oracle.inv_freq_std(D, 1.0, 1e6)
+    # pos = 0 is the identity, bit for bit
+    z = np.zeros(T, np.int32)
+    gq, gk = oracle.rope(N(q), N(k), z, f)
+    assert_bits_equal(gq, N(q))
+    # each rotated pair keeps its norm
+    pos = np.arange(T, dtype=np.int32) * 37
+    gq, _ = oracle.rope(N(q), N(k), pos, f)
+    a, b = oracle.bf16_to_f32(N(q)).astype(np.float64), oracle.bf16_to_f32(gq).astype(np.float64)
+    na = a[..., :64] ** 2 + a[..., 64:] ** 2
+    nb = b[..., :64] ** 2 + b[..., 64:] ** 2
+    np.testing.assert_allclose(nb, na, rtol=2e-2, atol=1e-2)
+    # composition R(a) R(b) = R(a + b) in float64 (via the HF form, no bf16 in between)
+    x = torch.randn(T, H, D, dtype=torch.float64, generator=torch.Generator().manual_seed(8))
+    p1 = torch.arange(T, dtype=torch.int32) * 3
+    p2 = torch.arange(T, dtype=torch.int32) * 5
+    two = _hf_rotate_half(_hf_rotate_half(x, p1, f), p2, f)
+    one = _hf_rotate_half(x, p1 + p2, f)
+    torch.testing.assert_close(two, one, rtol=1e-9, atol=1e-9)
+
+
+# ----------------------------------------------------------------------------- paged append
+def _brute_append(k, v, bidx, pos, cache, kv_indices, kv_indptr, P):
+    """Loop restatement of metal_append_paged_kv_cache.metal:51-103 (NHD)."""
+    B = len(kv_indptr) - 1
+    for t in range(k.shape[0]):
+        b, p = int(bidx[t]), int(pos[t])
+        if b < 0 or b >= B or p < 0:
+            continue
+        logical = int(kv_indptr[b]) + p // P
+        if logical >= int(kv_indptr[b + 1]):
+            continue
+        page = int(kv_indices[logical])
+        if page < 0 or page >= cache.shape[0]:
+            continue
+        cache[page, 0, p % P] = k[t]
+        cache[page, 1, p % P] = v[t]
+
+
+def test_append_vs_brute_force():
+    pb = wl.paged_batch(torch.tensor([0, 5, 31, 16], dtype=torch.int32),
+                        torch.tensor([3, 20, 1, 0], dtype=torch.int32), 16, 24, 1)
+    T, Hkv, D = int(pb.lens.sum()), 2, 16
+    k, v = N(wl.normal((T, Hkv, D), 1)), N(wl.normal((T, Hkv, D), 2))
+    bidx, pos = N(pb.batch_indices), N(pb.positions)
+    # poison: one token with an out-of-range batch index, one past its pages
+    bidx[0] = 7
+    pos[4] = 10_000
+    c1 = N(wl.sentinel_cache((24, 2, 16, Hkv, D)))
+    c2 = c1.copy()
+    n = oracle.append(k, v, bidx, pos, c1, N(pb.kv_indices), N(pb.kv_indptr))
+    _brute_append(k, v, bidx, pos, c2, N(pb.kv_indices), N(pb.kv_indptr), 16)
+    assert n == T - 2
+    assert_bits_equal(c1, c2, "append")
+    assert (c1 == wl.SENTINEL_BITS).any()  # untouched pages keep the sentinel
+
+
+def test_append_hnd_matches_nhd_transposed():
+    pb = wl.paged_batch(torch.tensor([3, 0], dtype=torch.int32), torch.tensor([9, 17], dtype=torch.int32), 8, 10, 2)
+    T, Hkv, D = int(pb.lens.sum()), 3, 8
+    k, v = N(wl.normal((T, Hkv, D), 3)), N(wl.normal((T, Hkv, D), 4))
+    nhd = N(wl.sentinel_cache((10, 2, 8, Hkv, D)))
+    hnd = N(wl.sentinel_cache((10, 2, Hkv, 8, D)))
+    args = (N(pb.batch_indices), N(pb.positions))
+    oracle.append(k, v, *args, nhd, N(pb.kv_indices), N(pb.kv_indptr), "NHD")
+    oracle.append(k, v, *args, hnd, N(pb.kv_indices), N(pb.kv_indptr), "HND")
+    assert_bits_equal(hnd.transpose(0, 1, 3, 2, 4), nhd)
+
+
+# ----------------------------------------------------------------------------- index helpers
+def _brute_seq_lens(indptr, last, P):
+    """flashinfer_metal/ops.py:392-407."""
+    out = []
+    for i in range(len(indptr) - 1):
+        n = indptr[i + 1] - indptr[i]
+        out.append((n - 1) * P + last[i] if n > 0 else 0)
+    return np.array(out, np.int32)
+
+
+def _brute_batch_pos(indptr, seq_lens, nnz):
+    """flashinfer_metal/ops.py:410-436."""
+    b = np.full(nnz, -1, np.int32)
+    p = np.full(nnz, -1, np.int32)
+    for i in range(len(indptr) - 1):
+        s, e = indptr[i], indptr[i + 1]
+        b[s:e] = i
+        p[s:e] = np.arange(seq_lens[i] - (e - s), seq_lens[i])
+    return b, p
+
+
+def test_index_helpers_vs_brute_force():
+    rng = np.random.default_rng(5)
+    npages = rng.integers(0, 6, 40)
+    npages[3] = 0
+    indptr = np.concatenate([[0], np.cumsum(npages)]).astype(np.int32)
+    last = rng.integers(1, 17, 40).astype(np.int32)
+    assert_bits_equal(oracle.seq_lens(indptr, last, 16), _brute_seq_lens(indptr, last, 16))
+    sl = oracle.seq_lens(indptr, last, 16)
+    newtok = np.minimum(rng.integers(0, 5, 40), sl)
+    qo = np.concatenate([[0], np.cumsum(newtok)]).astype(np.int32)
+    nnz = int(qo[-1]) + 3  # padded tail stays untouched
+    got_b, got_p = oracle.batch_indices_positions(qo, sl, nnz)
+    want_b, want_p = _brute_batch_pos(qo, sl, nnz)
+    assert_bits_equal(got_b, want_b)
+    assert_bits_equal(got_p, want_p)
+    assert (got_b[-3:] == -1).all()
+
+
+def test_workload_positions_match_index_helpers():
+    """The workload builder's positions equal what get_batch_indices_positions derives."""
+    c = wl.cfg5(B=32, V=16)
+    pb = c["batch"]
+    sl = oracle.seq_lens(N(pb.kv_indptr), N(pb.kv_last_page_len), pb.page_size)
+    assert_bits_equal(sl, N(pb.seq_lens))
+    b, p = oracle.batch_indices_positions(N(pb.qo_indptr), sl, int(pb.qo_indptr[-1]))
+    assert_bits_equal(b, N(pb.batch_indices))
+    assert_bits_equal(p, N(pb.positions))
