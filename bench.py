@@ -1,0 +1,260 @@
+"""Benchmark of the per-layer hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only main|ops|copy] [--no-cpu]
+
+One step = one pass of the fused residual-add + RMSNorm [8192, 4096] followed by SiLU-and-mul
+[8192, 2x14336] (configuration 2, Llama-3-8B prefill), inputs resident in HBM. Prints ONE JSON
+line: value = algorithmic HBM GB/s of the step; roofline = the dominant kernel (SiLU-and-mul)
+timed with HIP events on the stream it runs on; cpu_baseline = torch-CPU running the
+reference's own expressions (`residual + x`, F.rms_norm, F.silu(gate) * up) on a bounded
+sample of the same workload; "ops" = every configuration's per-op µs / GB/s (hot and with the
+256 MB last-level cache flushed) and the decode-chain µs (HIP-graph replay).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def _events(fn, iters, flush=None):
+    """Per-launch durations (ms) from HIP events on the current stream."""
+    import torch
+    out = []
+    for _ in range(iters):
+        if flush is not None:
+            flush()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        out.append((a, b))
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in out]
+
+
+def _op_entry(name, nbytes, hot_ms, cold_ms=None):
+    hot = statistics.median(hot_ms)
+    e = {"op": name, "bytes": nbytes, "us_hot": round(hot * 1e3, 2),
+         "gbs_hot": round(nbytes / hot / 1e6, 1), "frac_hot": round(nbytes / hot / 1e6 / HBM_PEAK_GBS, 3)}
+    if cold_ms:
+        cold = statistics.median(cold_ms)
+        e.update({"us_cold": round(cold * 1e3, 2), "gbs_cold": round(nbytes / cold / 1e6, 1),
+                  "frac_cold": round(nbytes / cold / 1e6 / HBM_PEAK_GBS, 3)})
+    return e
+
+
+def cpu_baseline(budget_s: float = 12.0) -> dict:
+    """torch-CPU running the reference's expressions (llama3.py:586 `residual + down`,
+    :555 fun.rms_norm, :569-572 fun.silu(gate) * up) on 256-row slices of configuration 2."""
+    import torch
+    import torch.nn.functional as F
+    from pie_amd import workloads as wl
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    rows = 256
+    c = wl.cfg2(T=rows)
+    I = c["gate_up"].shape[1] // 2
+    nbytes = sum(wl.cfg2_bytes(T=rows))
+
+    def step():
+        s = c["r"] + c["x"]
+        F.rms_norm(s, [s.shape[1]], c["w"], c["eps"])
+        g, u = torch.split(c["gate_up"], [I, I], -1)
+        F.silu(g) * u
+
+    for _ in range(2):
+        step()
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        step()
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(n * nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"{n} x 256-row slices of config 2 (add+rms_norm [256,4096], silu*mul "
+                      f"[256,2x14336]) in torch-CPU bf16, {dt:.1f} s"}
+
+
+def measure_ops(dev, iters=50, cold_iters=20):
+    """Every configuration: per-op hot/cold µs and GB/s; decode-chain µs per graph replay."""
+    import torch
+    from pie_amd import ops
+    from pie_amd import workloads as wl
+    from pie_amd.chain import DecodeChain
+
+    scratch = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+
+    def flush():
+        scratch.fill_(1)  # 1 GiB write evicts the 256 MB last-level cache and L2
+
+    res = []
+    c = wl.cfg1()
+    x, w = c["x"].to(dev), c["w"].to(dev)
+    y = torch.empty_like(x)
+    f = lambda: ops.rmsnorm(x, w, c["eps"], out=y)
+    res.append(_op_entry("cfg1 rmsnorm [2048,2048]", 2 * x.numel() * 2 + w.numel() * 2,
+                         _events(f, iters), _events(f, cold_iters, flush)))
+    del x, y
+
+    c = wl.cfg2()
+    x, r, w, gu = (c[k].to(dev) for k in ("x", "r", "w", "gate_up"))
+    y, s = torch.empty_like(x), torch.empty_like(x)
+    act = torch.empty((gu.shape[0], gu.shape[1] // 2), dtype=gu.dtype, device=dev)
+    b_add, b_silu = wl.cfg2_bytes()
+    f = lambda: ops.add_rms_norm(x, r, w, c["eps"], out=y, residual_out=s)
+    res.append(_op_entry("cfg2a add+rmsnorm [8192,4096]", b_add, _events(f, iters),
+                         _events(f, cold_iters, flush)))
+    f = lambda: ops.silu_and_mul(gu, out=act)
+    res.append(_op_entry("cfg2b silu_and_mul [8192,2x14336]", b_silu, _events(f, iters),
+                         _events(f, cold_iters, flush)))
+    del x, r, gu, y, s, act
+
+    c = wl.cfg3()
+    pb, T = c["batch"], c["qkv"].shape[0]
+    qkv = c["qkv"].to(dev)
+    q, k, v = wl.split_qkv(qkv, 32, 8, 128)
+    cache = wl.sentinel_cache(c["cache_shape"]).to(dev)
+    d = {n: getattr(pb, n).to(dev) for n in ("batch_indices", "positions", "kv_indices",
+                                             "kv_indptr", "kv_last_page_len")}
+    nb = wl.cfg3_bytes(T)
+    f = lambda: ops.apply_llama31_rope_pos_ids_inplace(q, k, d["positions"], **c["rope"])
+    res.append(_op_entry(f"cfg3 llama31 rope T={T}", nb["rope"], _events(f, iters),
+                         _events(f, cold_iters, flush)))
+    f = lambda: ops.append_paged_kv_cache(k, v, d["batch_indices"], d["positions"], cache,
+                                          d["kv_indices"], d["kv_indptr"], d["kv_last_page_len"])
+    res.append(_op_entry(f"cfg3 paged append T={T}", nb["append"], _events(f, iters),
+                         _events(f, cold_iters, flush)))
+    f = lambda: ops.apply_llama31_rope_pos_ids_and_append_paged_kv_cache(
+        q, k, v, d["positions"], d["batch_indices"], d["positions"], cache, d["kv_indices"],
+        d["kv_indptr"], d["kv_last_page_len"], **c["rope"])
+    res.append(_op_entry(f"cfg3 fused rope+append T={T}", nb["fused"], _events(f, iters),
+                         _events(f, cold_iters, flush)))
+    del qkv, q, k, v, cache
+
+    c = wl.cfg4()
+    W, ids = c["W"].to(dev), c["ids"].to(dev)
+    out = torch.empty((ids.numel(), W.shape[1]), dtype=W.dtype, device=dev)
+    f = lambda: ops.embedding(ids, W, out=out)
+    res.append(_op_entry("cfg4 embedding [128256,4096] x16384", wl.cfg4_bytes(), _events(f, iters),
+                         _events(f, cold_iters, flush)))
+    del W, out
+
+    c = wl.cfg5()
+    ch = DecodeChain(c, dev, fused=True)
+    g = ch.capture()
+    chain_bytes = sum(wl.cfg5_bytes().values())
+    ms = _events(g.replay, 200)
+    ms_cold = _events(g.replay, cold_iters, flush)
+    e = _op_entry("cfg5 decode chain (graph, 5 launches)", chain_bytes, ms, ms_cold)
+    e["launches"] = 5
+    res.append(e)
+    ch2 = DecodeChain(c, dev, fused=False)
+    ms_eager = _events(ch2.run, 50)
+    res.append({"op": "cfg5 decode chain (eager, 6 launches)", "us_hot": round(statistics.median(ms_eager) * 1e3, 2)})
+    del scratch
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", choices=["all", "main", "ops", "copy"], default="all")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
+              "ops are independent per token/head and shard without exchange", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from pie_amd import ops
+    from pie_amd import workloads as wl
+    dev = torch.device("cuda:0")
+
+    if args.only == "copy":  # calibration kernel for the FETCH_SIZE / WRITE_SIZE counters
+        a = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(args.steps):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": a.numel(), "bytes_written": b.numel(),
+                          "launches": args.steps}))
+        return
+
+    ops_res = None
+    if args.only in ("all", "ops"):
+        ops_res = measure_ops(dev)
+        if args.only == "ops":
+            print(json.dumps({"ops": ops_res}))
+            return
+
+    c = wl.cfg2()
+    x, r, w, gu = (c[k].to(dev) for k in ("x", "r", "w", "gate_up"))
+    y, s = torch.empty_like(x), torch.empty_like(x)
+    act = torch.empty((gu.shape[0], gu.shape[1] // 2), dtype=gu.dtype, device=dev)
+    b_add, b_silu = wl.cfg2_bytes()
+
+    def step(ev=None):
+        ops.add_rms_norm(x, r, w, c["eps"], out=y, residual_out=s)
+        if ev is not None:
+            ev[0].record()
+        ops.silu_and_mul(gu, out=act)
+        if ev is not None:
+            ev[1].record()
+
+    for _ in range(args.warmup):
+        step()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    silu_ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
+    ms_per_step = dt * 1e3 / args.steps
+    step_bytes = b_add + b_silu
+    achieved = b_silu / (silu_ms * 1e-3) / 1e9
+
+    traffic = None
+    tf = ROOT / "profiles" / "traffic.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get("silu_and_mul_cfg2")
+
+    line = {
+        "metric": "achieved HBM GB/s (% of MI355X peak) per fused op; µs per decode-step layer chain",
+        "value": round(step_bytes * args.steps / dt / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded N(0,1)/N(1,0.1)/N(0,2) as in the configs)",
+        "config": {"workload": "cfg2: fused residual-add+RMSNorm [8192,4096] eps 1e-5 then "
+                               "SiLU-and-mul [8192,2x14336] (Llama-3-8B prefill), bf16",
+                   "bytes_per_step": step_bytes, "parallelism": "single GPU"},
+        "roofline": {"kernel": "silu_and_mul_vec", "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "avg_launch_us": round(silu_ms * 1e3, 2),
+                     "algorithmic_bytes": b_silu},
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(),
+    }
+    if ops_res is not None:
+        line["ops"] = ops_res
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

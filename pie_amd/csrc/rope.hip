@@ -306,6 +306,7 @@ extern "C" int pie_hip_rope_inplace(pie_bf16* q, int64_t q_tok_stride, int64_t q
   if (rc) return rc;
   if (T == 0 || Hq + Hkv == 0 || rotary_dim == 0) return PIE_HIP_OK;
   PIE_REQUIRE(pos && inv_freq && (Hq == 0 || q) && (Hkv == 0 || k), "rope: null pointer");
+  a.pos = pos;
   for (int64_t i = 0; i < rotary_dim / 2; ++i) a.inv_freq[i] = inv_freq[i];
   return launch(a, true, false, interleave ? 1 : 0, (hipStream_t)stream, "rope_inplace");
 }
@@ -349,6 +350,7 @@ extern "C" int pie_hip_rope_append(pie_bf16* q, int64_t q_tok_stride, int64_t q_
   if (rc) return rc;
   if (T == 0 || Hq + Hkv == 0) return PIE_HIP_OK;
   PIE_REQUIRE(pos && inv_freq && (Hq == 0 || q) && (Hkv == 0 || (k && v)), "rope_append: null pointer");
+  a.pos = pos;
   for (int64_t i = 0; i < rotary_dim / 2; ++i) a.inv_freq[i] = inv_freq[i];
   if (rotary_dim == 0) return launch(a, false, true, 0, (hipStream_t)stream, "rope_append");
   return launch(a, true, Hkv > 0, interleave ? 1 : 0, (hipStream_t)stream, "rope_append");

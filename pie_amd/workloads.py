@@ -2,8 +2,8 @@
 
 Each builder returns CPU tensors (bf16 activations, int32 indices) generated in fp32 with
 ``torch.Generator().manual_seed(seed)`` and cast, so the CPU checker, the CPU timing and
-the GPU kernels all see identical bytes. Sizes default to the full configurations; the
-``scale`` arguments shrink them for parity tests.
+the GPU kernels all see identical bytes. Sizes default to the full configurations; keyword
+arguments shrink them for parity tests.
 
   cfg1  RMSNorm [2048, 2048], eps 1e-5                                (Llama-3.2-1B layer)
   cfg2  residual-add + RMSNorm [8192, 4096] eps 1e-5, SiLU-and-mul [8192, 2x14336] (Llama-3-8B)
@@ -135,7 +135,7 @@ def cfg4(V: int = 128256, H: int = 4096, T: int = 16384, repeat_frac: float = 0.
     n_uni = T - n_rep
     g = _gen(13)
     uni = torch.randint(0, V, (n_uni,), generator=g)
-    rep = uni[torch.randint(0, n_uni, (n_rep,), generator=g)]
+    rep = uni[torch.randint(0, max(n_uni, 1), (n_rep,), generator=g)] if n_uni else uni
     ids = torch.cat([uni, rep])[torch.randperm(T, generator=g)].to(torch.int32)
     return {"W": normal((V, H), 12, 0.0, 0.02), "ids": ids}
 

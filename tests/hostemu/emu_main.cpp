@@ -1,0 +1,283 @@
+// Runs every C-ABI entry point of the kernel library, built for the host by the emulator in
+// include/hip/hip_runtime.h, on exact-size heap buffers under AddressSanitizer, and compares
+// the results with the CPU oracle (oracle/oracle.c). TEST INFRASTRUCTURE.
+//
+//   emu_main <case>    case = norm | qk | silu | embed | rope | fused | decode | index | all | big
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <random>
+#include <string>
+#include <vector>
+
+#include "../../include/pie_hip.h"
+
+extern "C" {
+void oracle_rmsnorm(const uint16_t*, int64_t, int64_t, const uint16_t*, uint16_t*, int64_t, int64_t,
+                    int64_t, int64_t, int64_t, double);
+void oracle_add_rmsnorm(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, uint16_t*,
+                        int64_t, int64_t, double);
+void oracle_silu_and_mul(const uint16_t*, int64_t, uint16_t*, int64_t, int64_t, int);
+int64_t oracle_embedding(const int32_t*, int64_t, const uint16_t*, int64_t, int64_t, uint16_t*);
+void oracle_inv_freq_std(double*, int64_t, double, double);
+void oracle_rope(uint16_t*, int64_t, int64_t, uint16_t*, int64_t, int64_t, const int32_t*, int64_t,
+                 int64_t, int64_t, int64_t, int, const double*);
+int64_t oracle_append(const uint16_t*, int64_t, int64_t, const uint16_t*, int64_t, int64_t,
+                      const int32_t*, const int32_t*, const int32_t*, const int32_t*, int64_t,
+                      uint16_t*, uint16_t*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
+                      int64_t, int64_t);
+void oracle_seq_lens(const int32_t*, const int32_t*, int64_t, int64_t, int32_t*);
+void oracle_batch_indices_positions(const int32_t*, const int32_t*, int64_t, int64_t, int32_t*, int32_t*);
+}
+
+static std::mt19937 rng(1234);
+static int failures = 0;
+
+template <typename T>
+struct Buf {  // exact-size heap allocation: any access past the end trips ASan
+  T* p;
+  size_t n;
+  explicit Buf(size_t n_) : p((T*)malloc(n_ ? n_ * sizeof(T) : 1)), n(n_) {}
+  ~Buf() { free(p); }
+  Buf(const Buf&) = delete;
+  T& operator[](size_t i) { return p[i]; }
+};
+
+static uint16_t f2bf(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+static float bf2f(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+static void fill_normal(Buf<uint16_t>& b, float mean = 0.f, float std = 1.f) {
+  std::normal_distribution<float> d(mean, std);
+  for (size_t i = 0; i < b.n; ++i) b[i] = f2bf(d(rng));
+}
+
+static void check_close(const char* what, const uint16_t* got, const uint16_t* want, size_t n) {
+  size_t bad = 0;
+  for (size_t i = 0; i < n; ++i) {
+    float g = bf2f(got[i]), w = bf2f(want[i]);
+    if (!(fabsf(g - w) <= 2e-2f + 1e-2f * fabsf(w))) ++bad;
+  }
+  printf("  %-40s %s (%zu / %zu outside tolerance)\n", what, bad ? "FAIL" : "ok", bad, n);
+  failures += bad != 0;
+}
+template <typename T>
+static void check_equal(const char* what, const T* got, const T* want, size_t n) {
+  size_t bad = 0;
+  for (size_t i = 0; i < n; ++i) bad += got[i] != want[i];
+  printf("  %-40s %s (%zu / %zu differ)\n", what, bad ? "FAIL" : "ok", bad, n);
+  failures += bad != 0;
+}
+static void rc_ok(int rc, const char* what) {
+  if (rc != 0) {
+    printf("  %s returned %d: %s\n", what, rc, pie_hip_last_error());
+    ++failures;
+  }
+}
+
+// ---------------------------------------------------------------------------- norms
+static void case_norm(int64_t T, int64_t H) {
+  printf("norm T=%lld H=%lld\n", (long long)T, (long long)H);
+  Buf<uint16_t> x(T * H), r(T * H), w(H), y(T * H), s(T * H), wy(T * H), ws(T * H);
+  fill_normal(x);
+  fill_normal(r);
+  fill_normal(w, 1.f, 0.1f);
+  rc_ok(pie_hip_rmsnorm(x.p, H, w.p, y.p, H, T, H, 1e-5f, nullptr), "rmsnorm");
+  oracle_rmsnorm(x.p, H, 0, w.p, wy.p, H, 0, T, 1, H, 1e-5);
+  check_close("rmsnorm", y.p, wy.p, T * H);
+  rc_ok(pie_hip_fused_add_rmsnorm(x.p, H, r.p, H, s.p, H, y.p, H, w.p, T, H, 1e-5f, nullptr), "add");
+  oracle_add_rmsnorm(x.p, r.p, w.p, ws.p, wy.p, T, H, 1e-5);
+  check_equal("add_rmsnorm s", s.p, ws.p, T * H);
+  check_close("add_rmsnorm y", y.p, wy.p, T * H);
+}
+
+static void case_qk(int64_t T, int64_t Hq, int64_t Hkv, int64_t D) {
+  printf("qk_rmsnorm T=%lld Hq=%lld Hkv=%lld D=%lld\n", (long long)T, (long long)Hq, (long long)Hkv, (long long)D);
+  const int64_t row = (Hq + 2 * Hkv) * D;
+  Buf<uint16_t> qkv(T * row), qw(D), kw(D), qo(T * Hq * D), ko(T * Hkv * D), wq(T * Hq * D), wk(T * Hkv * D);
+  fill_normal(qkv);
+  fill_normal(qw, 1.f, .1f);
+  fill_normal(kw, 1.f, .1f);
+  rc_ok(pie_hip_qk_rmsnorm(qkv.p, row, D, qo.p, Hq * D, D, qkv.p + Hq * D, row, D, ko.p, Hkv * D, D,
+                           qw.p, kw.p, T, Hq, Hkv, D, 1e-6f, nullptr), "qk_rmsnorm");
+  oracle_rmsnorm(qkv.p, row, D, qw.p, wq.p, Hq * D, D, T, Hq, D, 1e-6);
+  oracle_rmsnorm(qkv.p + Hq * D, row, D, kw.p, wk.p, Hkv * D, D, T, Hkv, D, 1e-6);
+  check_close("q", qo.p, wq.p, T * Hq * D);
+  check_close("k", ko.p, wk.p, T * Hkv * D);
+}
+
+// ---------------------------------------------------------------------------- silu, embed
+static void case_silu(int64_t T, int64_t I) {
+  printf("silu T=%lld I=%lld\n", (long long)T, (long long)I);
+  Buf<uint16_t> gu(T * 2 * I), o(T * I), wo(T * I);
+  fill_normal(gu, 0.f, 1.414f);
+  rc_ok(pie_hip_silu_and_mul(gu.p, 2 * I, o.p, I, T, I, nullptr), "silu");
+  oracle_silu_and_mul(gu.p, 2 * I, wo.p, T, I, 0);
+  check_close("silu_and_mul", o.p, wo.p, T * I);
+}
+
+static void case_embed(int64_t V, int64_t H, int64_t T) {
+  printf("embedding V=%lld H=%lld T=%lld\n", (long long)V, (long long)H, (long long)T);
+  Buf<uint16_t> W(V * H), o(T * H), wo(T * H);
+  Buf<int32_t> ids(T);
+  fill_normal(W);
+  std::uniform_int_distribution<int> d(0, (int)V - 1);
+  for (int64_t t = 0; t < T; ++t) ids[t] = d(rng);
+  if (T > 2) ids[1] = (int32_t)V, ids[2] = -5;
+  rc_ok(pie_hip_embedding(ids.p, T, W.p, V, H, H, o.p, H, nullptr), "embedding");
+  oracle_embedding(ids.p, T, W.p, V, H, wo.p);
+  check_equal("embedding", o.p, wo.p, T * H);
+}
+
+// ---------------------------------------------------------------------------- paged batch
+struct Paged {
+  int64_t B, T, pool, P;
+  std::vector<int32_t> kv_indptr, kv_indices, last, qo, bidx, pos, seq;
+};
+static Paged make_paged(int64_t B, int64_t P, int lo_ctx, int hi_ctx, int lo_new, int hi_new) {
+  Paged p;
+  p.B = B;
+  p.P = P;
+  std::uniform_int_distribution<int> dc(lo_ctx, hi_ctx), dn(lo_new, hi_new);
+  std::vector<int> ctx(B), nw(B);
+  int64_t pages = 0;
+  p.kv_indptr.push_back(0);
+  p.qo.push_back(0);
+  for (int64_t b = 0; b < B; ++b) {
+    ctx[b] = dc(rng);
+    nw[b] = dn(rng);
+    int64_t tot = ctx[b] + nw[b], np = (tot + P - 1) / P;
+    pages += np;
+    p.kv_indptr.push_back((int32_t)pages);
+    p.last.push_back(np ? (int32_t)(tot - P * (np - 1)) : 0);
+    p.qo.push_back(p.qo.back() + nw[b]);
+    p.seq.push_back((int32_t)tot);
+    for (int i = 0; i < nw[b]; ++i) {
+      p.bidx.push_back((int32_t)b);
+      p.pos.push_back(ctx[b] + i);
+    }
+  }
+  p.pool = pages + 3;
+  std::vector<int32_t> perm(p.pool);
+  for (int64_t i = 0; i < p.pool; ++i) perm[i] = (int32_t)i;
+  std::shuffle(perm.begin(), perm.end(), rng);
+  p.kv_indices.assign(perm.begin(), perm.begin() + pages);
+  p.T = p.qo.back();
+  return p;
+}
+
+template <typename T>
+static void copy_in(Buf<T>& b, const std::vector<T>& v) { memcpy(b.p, v.data(), v.size() * sizeof(T)); }
+
+static void case_rope_append(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int lo_ctx, int hi_ctx,
+                             int lo_new, int hi_new, bool fused, int64_t rd = 0, int interleave = 0) {
+  if (rd == 0) rd = D;
+  Paged pg = make_paged(B, 16, lo_ctx, hi_ctx, lo_new, hi_new);
+  const int64_t T = pg.T, row = (Hq + 2 * Hkv) * D, P = pg.P;
+  printf("%s B=%lld T=%lld Hq=%lld Hkv=%lld D=%lld rd=%lld il=%d pool=%lld\n",
+         fused ? "rope+append fused" : "rope, append", (long long)B, (long long)T, (long long)Hq,
+         (long long)Hkv, (long long)D, (long long)rd, interleave, (long long)pg.pool);
+  Buf<uint16_t> qkv(T * row), ref(T * row);
+  fill_normal(qkv);
+  memcpy(ref.p, qkv.p, T * row * 2);
+  const int64_t page_elems = 2 * P * Hkv * D;
+  Buf<uint16_t> cache(pg.pool * page_elems), wcache(pg.pool * page_elems);
+  for (size_t i = 0; i < cache.n; ++i) cache[i] = wcache[i] = 0x7fa5;
+  Buf<int32_t> bidx(T), pos(T), kvi(pg.kv_indices.size()), kvp(B + 1);
+  copy_in(bidx, pg.bidx);
+  copy_in(pos, pg.pos);
+  copy_in(kvi, pg.kv_indices);
+  copy_in(kvp, pg.kv_indptr);
+  float inv[256];
+  double invd[256];
+  rc_ok(pie_hip_rope_inv_freq(inv, rd, 1.f, 1e6f), "inv_freq");
+  oracle_inv_freq_std(invd, rd, 1.0, 1e6);
+  uint16_t* q = qkv.p;
+  uint16_t* k = qkv.p + Hq * D;
+  uint16_t* v = qkv.p + (Hq + Hkv) * D;
+  if (fused) {
+    rc_ok(pie_hip_rope_append(q, row, D, k, row, D, v, row, D, pos.p, T, Hq, Hkv, D, rd, interleave, inv, bidx.p,
+                              pos.p, kvi.p, kvp.p, B, cache.p, cache.p + P * Hkv * D, pg.pool,
+                              page_elems, Hkv * D, D, P, nullptr), "rope_append");
+  } else {
+    rc_ok(pie_hip_rope_inplace(q, row, D, k, row, D, pos.p, T, Hq, Hkv, D, rd, interleave, inv, nullptr), "rope");
+    rc_ok(pie_hip_paged_kv_append(k, row, D, v, row, D, bidx.p, pos.p, kvi.p, kvp.p, B, cache.p,
+                                  cache.p + P * Hkv * D, pg.pool, page_elems, Hkv * D, D, P, T, Hkv, D,
+                                  nullptr), "append");
+  }
+  oracle_rope(ref.p, row, D, ref.p + Hq * D, row, D, pos.p, T, Hq, Hkv, rd, interleave, invd);
+  check_close("q/k rotated (v untouched)", qkv.p, ref.p, T * row);
+  oracle_append(qkv.p + Hq * D, row, D, qkv.p + (Hq + Hkv) * D, row, D, bidx.p, pos.p, kvi.p, kvp.p, B,
+                wcache.p, wcache.p + P * Hkv * D, pg.pool, page_elems, Hkv * D, D, P, T, Hkv, D);
+  check_equal("cache", cache.p, wcache.p, cache.n);
+}
+
+static void case_index(int64_t B) {
+  printf("index helpers B=%lld\n", (long long)B);
+  Paged pg = make_paged(B, 16, 0, 100, 0, 9);
+  Buf<int32_t> kvp(B + 1), last(B), qo(B + 1), sl(B), wsl(B), bi(pg.T), po(pg.T), wbi(pg.T), wpo(pg.T);
+  copy_in(kvp, pg.kv_indptr);
+  copy_in(last, pg.last);
+  copy_in(qo, pg.qo);
+  rc_ok(pie_hip_get_seq_lens(kvp.p, last.p, B, 16, sl.p, nullptr), "seq_lens");
+  oracle_seq_lens(kvp.p, last.p, B, 16, wsl.p);
+  check_equal("seq_lens", sl.p, wsl.p, B);
+  rc_ok(pie_hip_get_batch_indices_positions(qo.p, sl.p, B, pg.T, bi.p, po.p, nullptr), "bip");
+  oracle_batch_indices_positions(qo.p, wsl.p, B, pg.T, wbi.p, wpo.p);
+  check_equal("batch_indices", bi.p, wbi.p, pg.T);
+  check_equal("positions", po.p, wpo.p, pg.T);
+}
+
+int main(int argc, char** argv) {
+  std::string c = argc > 1 ? argv[1] : "all";
+  const bool all = c == "all";
+  if (all || c == "norm") {
+    case_norm(3, 512);
+    case_norm(5, 4096);
+    case_norm(2, 896);
+    case_norm(3, 100);
+    case_norm(4, 128);
+  }
+  if (all || c == "qk") {
+    case_qk(5, 4, 2, 128);
+    case_qk(3, 2, 1, 64);
+    case_qk(2, 2, 1, 96);
+  }
+  if (all || c == "silu") {
+    case_silu(3, 1536);
+    case_silu(2, 13);
+  }
+  if (all || c == "embed") {
+    case_embed(50, 4096, 9);
+    case_embed(20, 100, 5);
+  }
+  if (all || c == "rope") case_rope_append(3, 4, 2, 128, 0, 40, 1, 20, false);
+  if (all || c == "fused") {
+    case_rope_append(3, 4, 2, 128, 0, 40, 1, 20, true);
+    case_rope_append(3, 4, 2, 128, 0, 40, 1, 20, true, 64, 0);   // partial rotary: k tail copied
+    case_rope_append(3, 4, 2, 128, 0, 40, 1, 20, true, 128, 1);  // interleaved pairs
+    case_rope_append(3, 3, 1, 32, 0, 40, 1, 20, true, 24, 0);    // scalar fallback kernels
+    case_rope_append(2, 3, 1, 32, 0, 40, 1, 20, false, 24, 1);
+  }
+  if (c == "big") case_rope_append(4, 2, 1, 64, 0, 100, 600, 700, true);  // T >= 2048: 2 tokens/block
+  if (all || c == "decode") {
+    // Qwen3-8B decode shape (the faulting chain's rope/append and norms), fewer sequences
+    case_rope_append(6, 32, 8, 128, 128, 4096, 1, 1, true);
+    case_rope_append(6, 32, 8, 128, 128, 4096, 1, 1, false);
+    case_qk(6, 32, 8, 128);
+    case_norm(6, 4096);
+  }
+  if (all || c == "index") case_index(40);
+  printf("%s\n", failures ? "FAILURES" : "all ok");
+  return failures ? 1 : 0;
+}

@@ -1,0 +1,78 @@
+"""GPU parity: SiLU-and-mul (tolerance 1e-2 rel / 2e-2 abs of the oracle, which keeps torch's
+double rounding) and the embedding gather (bit-exact)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from pie_amd import ops
+from pie_amd import workloads as wl
+from tests._util import assert_bf16_close, assert_bits_equal, ulp_diff
+
+pytestmark = pytest.mark.gpu
+N = oracle.to_np
+
+
+@pytest.mark.parametrize("T,I", [(1, 8), (17, 512), (64, 14336), (3, 12288), (5, 13), (0, 64)])
+def test_silu_and_mul(dev, T, I):
+    print(f"silu_and_mul T={T} I={I}", flush=True)
+    gu = wl.normal((T, 2 * I), 6, 0.0, 2 ** 0.5)
+    out = ops.silu_and_mul(gu.to(dev))
+    torch.cuda.synchronize()
+    want = oracle.silu_and_mul(N(gu))
+    assert_bf16_close(N(out), want, what=f"silu {T}x{I}")
+    if T:
+        assert ulp_diff(N(out), want).max() <= 2
+
+
+def test_silu_and_mul_strided_input(dev):
+    big = wl.normal((9, 2 * 1024 + 64), 7).to(dev)
+    gu = big[:, 32:32 + 2048]
+    out = ops.silu_and_mul(gu)
+    assert_bf16_close(N(out), oracle.silu_and_mul(N(gu)), what="strided gate_up")
+
+
+def test_silu_and_mul_matches_torch_expression(dev):
+    gu = wl.normal((32, 2 * 4096), 8, 0.0, 2 ** 0.5)
+    g, u = torch.split(gu, [4096, 4096], -1)
+    want = torch.nn.functional.silu(g) * u          # the reference's CPU path
+    got = ops.silu_and_mul(gu.to(dev))
+    assert ulp_diff(N(got), N(want)).max() <= 2
+
+
+def test_silu_and_mul_full_config2(dev):
+    c = wl.cfg2(H=8)
+    out = ops.silu_and_mul(c["gate_up"].to(dev))
+    rows = torch.randperm(8192, generator=torch.Generator().manual_seed(1))[:48]
+    assert_bf16_close(N(out.cpu()[rows]), oracle.silu_and_mul(N(c["gate_up"][rows])),
+                      what="cfg2 silu rows")
+
+
+@pytest.mark.parametrize("V,H,T", [(1000, 64, 300), (50, 4096, 7), (300, 100, 40), (10, 8, 0)])
+def test_embedding(dev, V, H, T):
+    print(f"embedding V={V} H={H} T={T}", flush=True)
+    c = wl.cfg4(V=V, H=H, T=T)
+    out = ops.embedding(c["ids"].to(dev), c["W"].to(dev))
+    want, _ = oracle.embedding(N(c["ids"]), N(c["W"]))
+    assert_bits_equal(N(out).reshape(T, H), want, "embedding")
+
+
+def test_embedding_out_of_range(dev):
+    W = wl.normal((10, 256), 1)
+    ids = torch.tensor([0, 10, -1, 9, 3], dtype=torch.int32)
+    out = ops.embedding(ids.to(dev), W.to(dev))
+    want, bad = oracle.embedding(N(ids), N(W))
+    assert bad == 2
+    assert_bits_equal(N(out), want, "zero rows for bad ids")
+    with pytest.raises(IndexError):
+        ops.embedding(ids.to(dev), W.to(dev), check_ids=True)
+
+
+def test_embedding_full_config4(dev):
+    """Full Llama-3-8B vocab gather: bit-exact against the oracle on every row."""
+    c = wl.cfg4()
+    out = ops.embedding(c["ids"].to(dev), c["W"].to(dev))
+    want, bad = oracle.embedding(N(c["ids"]), N(c["W"]))
+    assert bad == 0
+    assert_bits_equal(N(out), want, "cfg4 embedding")

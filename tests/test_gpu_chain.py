@@ -1,0 +1,76 @@
+"""GPU: the Qwen3-8B decode-step op chain (configuration 5) eagerly vs the oracle, fused vs
+unfused, and HIP-graph replays vs the eager result (every replay checked, with eager work
+and synchronisation between replays)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from pie_amd import workloads as wl
+from pie_amd.chain import DecodeChain
+from tests._util import assert_bf16_close, assert_bits_equal
+
+pytestmark = pytest.mark.gpu
+N = oracle.to_np
+
+
+@pytest.fixture(scope="module")
+def cfg():
+    return wl.cfg5(V=4096)  # full decode shape; a smaller vocabulary keeps the table small
+
+
+def _snap(ch):
+    torch.cuda.synchronize()
+    return {k: N(v) for k, v in ch.outputs().items()}
+
+
+def test_chain_vs_oracle(dev, cfg):
+    ch = DecodeChain(cfg, dev, fused=True)
+    ch.run()
+    got = _snap(ch)
+    hid, _ = oracle.embedding(N(cfg["ids"]), N(cfg["W"]))
+    assert_bits_equal(got["hidden"], hid, "embedding")
+    y, s = oracle.add_rmsnorm(hid, N(cfg["residual"]), N(cfg["w_norm"]), cfg["eps"])
+    assert_bits_equal(got["residual"], s, "residual")
+    assert_bf16_close(got["normed"], y, what="add_rmsnorm")
+    q, k, v = wl.split_qkv(cfg["qkv"], 32, 8, 128)
+    qn = oracle.rmsnorm(N(q), N(cfg["q_norm"]), cfg["eps"])
+    kn = oracle.rmsnorm(N(k), N(cfg["k_norm"]), cfg["eps"])
+    pos = N(cfg["batch"].positions)
+    f = oracle.inv_freq_std(128, 1.0, cfg["theta"])
+    wq, wk = oracle.rope(qn, kn, pos, f)
+    assert_bf16_close(got["q"], wq, what="q norm+rope")
+    assert_bf16_close(got["k"], wk, what="k norm+rope")
+    pb = cfg["batch"]
+    want = N(wl.sentinel_cache(cfg["cache_shape"]))
+    oracle.append(got["k"], N(v), N(pb.batch_indices), N(pb.positions), want, N(pb.kv_indices),
+                  N(pb.kv_indptr))
+    assert_bits_equal(got["cache"], want, "cache")
+    assert_bf16_close(got["act"], oracle.silu_and_mul(N(cfg["gate_up"])), what="silu")
+
+
+def test_chain_fused_equals_unfused(dev, cfg):
+    a, b = DecodeChain(cfg, dev, fused=True), DecodeChain(cfg, dev, fused=False)
+    a.run()
+    b.run()
+    ga, gb = _snap(a), _snap(b)
+    for key in ga:
+        assert_bits_equal(ga[key], gb[key], key)
+
+
+def test_chain_graph_replays(dev, cfg):
+    ch = DecodeChain(cfg, dev, fused=True)
+    ch.reset()
+    ch.run()
+    eager = _snap(ch)
+    g = ch.capture()
+    for i in range(4):
+        ch.reset()
+        junk = torch.randn(1 << 20, device=dev).sum()  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        got = _snap(ch)
+        for key in eager:
+            assert_bits_equal(got[key], eager[key], f"replay {i} {key}")
+        del junk

@@ -1,0 +1,102 @@
+"""CPU: the C-ABI library loads, exports exactly what include/pie_hip.h declares, rejects bad
+arguments before touching a GPU, and the Python wrappers validate inputs and never fall back
+to a CPU path."""
+from __future__ import annotations
+
+import ctypes as C
+import re
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from pie_amd import _lib, ops
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    declared = _lib.header_symbols()
+    assert len(declared) >= 14
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in pie_hip.h but not exported"
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                        text=True, check=True).stdout
+    exported = set(re.findall(r"\b(pie_hip_[a-z0-9_]+)\b", nm))
+    assert exported == set(declared), f"exported but undeclared: {exported - set(declared)}"
+
+
+def test_ctypes_signatures_match_header_arity():
+    text = _lib.HEADER.read_text()
+    for name, argtypes in _lib.SIGNATURES.items():
+        m = re.search(rf"\b{name}\s*\(([^;]*?)\)\s*;", text, re.S)
+        assert m, name
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(argtypes), f"{name}: header {len(params)} vs ctypes {len(argtypes)}"
+
+
+def test_abi_version():
+    assert _lib.load().pie_hip_abi_version() == _lib.ABI_VERSION
+
+
+def _rc(name, *args):
+    lib = _lib.load()
+    return getattr(lib, name)(*args), lib.pie_hip_last_error().decode()
+
+
+def test_bad_arguments_return_einval_without_a_gpu():
+    rc, msg = _rc("pie_hip_rmsnorm", None, 0, None, None, 0, -1, 16, C.c_float(1e-6), None)
+    assert rc == 1 and "bad shape" in msg
+    rc, msg = _rc("pie_hip_rmsnorm", 8, 4, 8, 8, 16, 2, 16, C.c_float(1e-6), None)
+    assert rc == 1 and "stride" in msg
+    rc, msg = _rc("pie_hip_silu_and_mul", 8, 3, 8, 2, 1, 2, None)
+    assert rc == 1 and "stride" in msg
+    rc, msg = _rc("pie_hip_rope_inplace", 16, 0, 0, 16, 0, 0, 16, 4, 1, 1, 128, 130, 0, 16, None)
+    assert rc == 1 and "rotary_dim" in msg
+    rc, msg = _rc("pie_hip_paged_kv_append", 16, 0, 0, 16, 0, 0, 16, 16, 16, 16, 1, 16, 16, 4,
+                  0, 0, 0, 0, 1, 8, 128, None)
+    assert rc == 1 and "page" in msg
+    rc, msg = _rc("pie_hip_llama31_inv_freq", None, 128, C.c_float(8), C.c_float(5e5), C.c_float(4),
+                  C.c_float(1), C.c_float(8192))
+    assert rc == 1
+
+
+def test_empty_inputs_are_noops_without_a_gpu():
+    assert _rc("pie_hip_rmsnorm", None, 0, None, None, 0, 0, 16, C.c_float(1e-6), None)[0] == 0
+    assert _rc("pie_hip_silu_and_mul", None, 0, None, 0, 0, 8, None)[0] == 0
+    assert _rc("pie_hip_embedding", None, 0, None, 10, 8, 8, None, 8, None)[0] == 0
+
+
+def test_inv_freq_tables_match_oracle():
+    import oracle
+    got = (C.c_float * 64)()
+    assert _lib.load().pie_hip_llama31_inv_freq(got, 128, C.c_float(8), C.c_float(5e5),
+                                                C.c_float(1), C.c_float(4), C.c_float(8192)) == 0
+    np.testing.assert_allclose(np.array(got), oracle.inv_freq_llama31(128), rtol=1e-7)
+    assert _lib.load().pie_hip_rope_inv_freq(got, 128, C.c_float(1), C.c_float(1e6)) == 0
+    np.testing.assert_allclose(np.array(got), oracle.inv_freq_std(128, 1.0, 1e6), rtol=1e-7)
+
+
+def test_call_raises_with_library_message():
+    with pytest.raises(ValueError, match="bad shape"):
+        _lib.call("pie_hip_rmsnorm", None, 0, None, None, 0, -1, 16, C.c_float(1e-6), None)
+
+
+def test_wrappers_reject_cpu_tensors_and_wrong_dtypes():
+    x = torch.zeros(4, 128, dtype=torch.bfloat16)
+    w = torch.ones(128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.rmsnorm(x, w)                      # no silent CPU fallback
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.silu_and_mul(torch.zeros(2, 16, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.embedding(torch.zeros(3, dtype=torch.int32), x)
+    with pytest.raises(TypeError):
+        ops.rmsnorm(np.zeros((2, 2)), w)
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(ImportError, match="not built"):
+        _lib.load()
