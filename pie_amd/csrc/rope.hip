@@ -58,6 +58,11 @@ struct RopeAppendArgs {
   float inv_freq[kMaxPairs];
 };
 
+// The rotation with its fused multiply-adds spelled out, so every kernel variant (rope only,
+// fused with the append, scalar fallback) rounds identically: x' = x c - y s, y' = x s + y c.
+__device__ __forceinline__ float rot_x(float x, float y, float2 cs) { return fmaf(x, cs.x, -(y * cs.y)); }
+__device__ __forceinline__ float rot_y(float x, float y, float2 cs) { return fmaf(x, cs.y, y * cs.x); }
+
 // Cache element offset of (token's page, slot), or -1 when the token is skipped.
 __device__ __forceinline__ int64_t slot_offset(const CacheDesc& c, int64_t t) {
   const int b = c.batch_indices[t];
@@ -126,8 +131,8 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float2 cs = tb[c * 8 + e];
-          const float xr = x[e] * cs.x - y[e] * cs.y;
-          const float yr = x[e] * cs.y + y[e] * cs.x;
+          const float xr = rot_x(x[e], y[e], cs);
+          const float yr = rot_y(x[e], y[e], cs);
           x[e] = xr;
           y[e] = yr;
         }
@@ -146,8 +151,8 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           const float2 cs = tb[c * 4 + m];
-          const float xr = f[2 * m] * cs.x - f[2 * m + 1] * cs.y;
-          const float yr = f[2 * m] * cs.y + f[2 * m + 1] * cs.x;
+          const float xr = rot_x(f[2 * m], f[2 * m + 1], cs);
+          const float yr = rot_y(f[2 * m], f[2 * m + 1], cs);
           f[2 * m] = xr;
           f[2 * m + 1] = yr;
         }
@@ -195,8 +200,9 @@ __global__ __launch_bounds__(256) void rope_scalar(RopeAppendArgs a) {
     float sn, cs;
     sincosf((float)a.pos[t] * a.inv_freq[pr], &sn, &cs);
     const float x = bf1(*px), y = bf1(*py);
-    *px = to_bf1(x * cs - y * sn);
-    *py = to_bf1(x * sn + y * cs);
+    const float2 csn = make_float2(cs, sn);
+    *px = to_bf1(rot_x(x, y, csn));
+    *py = to_bf1(rot_y(x, y, csn));
   }
 }
 
