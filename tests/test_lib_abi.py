@@ -100,3 +100,21 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
     with pytest.raises(ImportError, match="not built"):
         _lib.load()
+
+
+def test_integration_installs_flashinfer_namespace():
+    import importlib
+    import sys
+    from pie_amd import integration
+    mod = integration.install()
+    try:
+        fi = importlib.import_module("flashinfer")
+        assert fi is mod
+        for n in integration.HOT_PATH:
+            assert getattr(fi, n) is getattr(ops, n)
+        with pytest.raises(AttributeError):
+            fi.BatchPrefillWithPagedKVCacheWrapper  # not served here, and no real flashinfer
+        assert integration.install() is mod  # idempotent
+    finally:
+        integration.uninstall()
+    assert "flashinfer" not in sys.modules
