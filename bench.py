@@ -92,10 +92,13 @@ def measure_ops(dev, iters=50, cold_iters=20):
     from pie_amd import workloads as wl
     from pie_amd.chain import DecodeChain
 
-    scratch = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    scratch = torch.ones(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+    sink = torch.empty((), dtype=torch.float32, device=dev)
 
     def flush():
-        scratch.fill_(1)  # 1 GiB write evicts the 256 MB last-level cache and L2
+        # Reading 1 GiB evicts the 256 MB last-level cache and L2 with clean lines; a write
+        # would leave dirty lines draining to HBM during the timed kernel.
+        torch.sum(scratch, dim=0, out=sink)
 
     res = []
     c = wl.cfg1()

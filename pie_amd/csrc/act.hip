@@ -7,9 +7,8 @@
 // This kernel keeps both roundings, so it differs from torch only through exp().
 //
 // One pass over HBM: read gate_up [rows, 2I], write out [rows, I] (the reference makes three
-// passes plus a [rows, I] temporary). One 256-thread block per row; each thread issues U
-// independent 16-byte gate loads and U up loads before any math, so every CU keeps
-// > 64 KiB of reads in flight.
+// passes plus a [rows, I] temporary). The grid is flattened over output vectors; each thread
+// issues U independent 16-byte gate loads and U up loads before any math.
 #include "common.h"
 
 namespace pie {
@@ -25,37 +24,38 @@ struct SiluArgs {
   const uint16_t* in;
   uint16_t* out;
   int64_t in_rs, out_rs, rows, I;
+  uint32_t nvec;   // rows * I / 8 (vector path)
+  FastDiv vpr;     // I / 8 vectors per row
 };
 
+// Flattened over all 16-byte output vectors: block b owns vectors [b*256*U, (b+1)*256*U), thread
+// t handles b*256*U + t + 256*i for i < U, so every wave instruction covers 1 KiB contiguous
+// (rows split only at row ends) and small row counts still spread over the whole chip.
 template <int U>
 __global__ __launch_bounds__(256) void silu_and_mul_vec(SiluArgs a) {
-  const int64_t nvec = a.I >> 3;
-  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
-    const uint16_t* g = a.in + row * a.in_rs;
-    const uint16_t* u = g + a.I;
-    uint16_t* o = a.out + row * a.out_rs;
-    for (int64_t base = threadIdx.x; base < nvec; base += 256 * U) {
-      uint4 gv[U], uv[U];
+  const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
+  uint4 gv[U], uv[U];
+  int64_t orow[U];
 #pragma unroll
-      for (int i = 0; i < U; ++i) {
-        const int64_t c = base + 256 * i;
-        if (c < nvec) {
-          gv[i] = ld_stream(g + c * 8);
-          uv[i] = ld_stream(u + c * 8);
-        }
-      }
+  for (int i = 0; i < U; ++i) {
+    const uint32_t v = base + 256u * i;
+    if (v < a.nvec) {
+      const uint32_t row = a.vpr.div(v), c = v - row * a.vpr.d;
+      const uint16_t* g = a.in + (int64_t)row * a.in_rs + (int64_t)c * 8;
+      gv[i] = ld_stream(g);
+      uv[i] = ld_stream(g + a.I);
+      orow[i] = (int64_t)row * a.out_rs + (int64_t)c * 8;
+    }
+  }
 #pragma unroll
-      for (int i = 0; i < U; ++i) {
-        const int64_t c = base + 256 * i;
-        if (c < nvec) {
-          float gf[8], uf[8];
-          unpack8(gv[i], gf);
-          unpack8(uv[i], uf);
+  for (int i = 0; i < U; ++i) {
+    if (base + 256u * i < a.nvec) {
+      float gf[8], uf[8];
+      unpack8(gv[i], gf);
+      unpack8(uv[i], uf);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) gf[e] = silu_bf(gf[e]) * uf[e];
-          st_stream(o + c * 8, pack8(gf));
-        }
-      }
+      for (int e = 0; e < 8; ++e) gf[e] = silu_bf(gf[e]) * uf[e];
+      st_stream(a.out + orow[i], pack8(gf));
     }
   }
 }
@@ -80,12 +80,28 @@ extern "C" int pie_hip_silu_and_mul(const pie_bf16* gate_up, int64_t in_row_stri
   if (rows == 0 || I == 0) return PIE_HIP_OK;
   PIE_REQUIRE(gate_up && out, "silu_and_mul: null pointer");
   PIE_REQUIRE(in_row_stride >= 2 * I && out_row_stride >= I, "silu_and_mul: row stride too small");
-  SiluArgs a{gate_up, out, in_row_stride, out_row_stride, rows, I};
-  const int64_t cap = (int64_t)num_cus() * 64;
-  const dim3 grd((unsigned)(rows < cap ? rows : cap)), blk(256);
+  SiluArgs a{gate_up, out, in_row_stride, out_row_stride, rows, I, 0, FastDiv{}};
+  const dim3 blk(256);
+  const int64_t nvec = rows * (I / 8);
   const bool vec = I % 8 == 0 && in_row_stride % 8 == 0 && out_row_stride % 8 == 0 &&
-                   aligned16(gate_up) && aligned16(out);
-  if (vec) hipLaunchKernelGGL(silu_and_mul_vec<4>, grd, blk, 0, (hipStream_t)stream, a);
-  else hipLaunchKernelGGL(silu_and_mul_scalar, grd, blk, 0, (hipStream_t)stream, a);
+                   aligned16(gate_up) && aligned16(out) && nvec < (1ll << 31);
+  if (vec) {
+    a.nvec = (uint32_t)nvec;
+    a.vpr = FastDiv::make((uint32_t)(I / 8));
+    // Enough blocks to give every CU several waves; more vectors per thread once it is full.
+    const int64_t target = (int64_t)num_cus() * 16;
+    const hipStream_t st = (hipStream_t)stream;
+    if (nvec >= target * 256 * 4) {
+      hipLaunchKernelGGL(silu_and_mul_vec<4>, dim3((unsigned)((nvec + 1023) / 1024)), blk, 0, st, a);
+    } else if (nvec >= target * 256 * 2) {
+      hipLaunchKernelGGL(silu_and_mul_vec<2>, dim3((unsigned)((nvec + 511) / 512)), blk, 0, st, a);
+    } else {
+      hipLaunchKernelGGL(silu_and_mul_vec<1>, dim3((unsigned)((nvec + 255) / 256)), blk, 0, st, a);
+    }
+  } else {
+    const int64_t cap = (int64_t)num_cus() * 64;
+    hipLaunchKernelGGL(silu_and_mul_scalar, dim3((unsigned)(rows < cap ? rows : cap)), blk, 0,
+                       (hipStream_t)stream, a);
+  }
   return check_launch("silu_and_mul");
 }

@@ -89,4 +89,20 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Unsigned 32-bit division by a runtime-constant divisor with a host-computed multiplier
+// (round-up method: q = (mulhi(n, m) + n) >> l with l = ceil(log2 d),
+// m = floor(2^32 (2^l - d) / d) + 1); exact for every 32-bit n.
+struct FastDiv {
+  uint32_t d, m, l;
+  static FastDiv make(uint32_t d) {
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    const uint64_t m = ((((1ull << l) - d) << 32) / d) + 1;
+    return FastDiv{d, (uint32_t)m, l};
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    return (uint32_t)(((uint64_t)__umulhi(n, m) + n) >> l);
+  }
+};
+
 }  // namespace pie

@@ -2,10 +2,10 @@
 // Replaces fun.embedding(token_ids, W) (pie/src/pie_worker/model/llama3.py:471,
 // qwen3.py:468-472; ids are int32 per llama3.py:429-433).
 //
-// One wavefront per token row: the id is read once into a scalar register, then each lane
-// issues U independent 16-byte loads of the table row (1 KiB per wave instruction, fully
-// coalesced) before storing them. Table rows are loaded with the normal cached path so the
-// repeated ids of a batch are served from L2/MALL; the output is written non-temporally.
+// The grid is flattened over 16-byte output vectors (1 KiB of one table row per wave
+// instruction), so a decode batch of a few hundred tokens still spreads over every CU. Table
+// rows are loaded with the normal cached path so the repeated ids of a batch are served from
+// L2/MALL; the output is written non-temporally.
 #include "common.h"
 
 namespace pie {
@@ -16,31 +16,33 @@ struct EmbedArgs {
   const uint16_t* W;
   uint16_t* out;
   int64_t T, V, H, w_rs, out_rs;
+  uint32_t nvec;  // T * H / 8 (vector path)
+  FastDiv vpr;    // H / 8 vectors per row
 };
 
+// Flattened over the 16-byte vectors of the output: thread t of block b copies vectors
+// b*256*U + t + 256*i (i < U). All U table loads are issued before any store. The id of a
+// vector's token is re-read per vector (an L1 hit); ids outside [0, V) give zero rows.
 template <int U>
 __global__ __launch_bounds__(256) void embed_vec(EmbedArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t nwaves = (int64_t)gridDim.x * 4;
-  const int64_t nvec = a.H >> 3;
-  for (int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); t < a.T; t += nwaves) {
-    const int id = uniform(a.ids[t]);
-    uint16_t* o = a.out + t * a.out_rs;
-    if (id < 0 || (int64_t)id >= a.V) {
-      for (int64_t c = lane; c < nvec; c += 64) st_stream(o + c * 8, make_uint4(0, 0, 0, 0));
-      continue;
-    }
-    const uint16_t* src = a.W + (int64_t)id * a.w_rs;
-    for (int64_t base = lane; base < nvec; base += 64 * U) {
-      uint4 v[U];
+  const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
+  uint4 v[U];
+  int64_t dst[U];
 #pragma unroll
-      for (int i = 0; i < U; ++i)
-        if (base + 64 * i < nvec) v[i] = ld16(src + (base + 64 * i) * 8);
-#pragma unroll
-      for (int i = 0; i < U; ++i)
-        if (base + 64 * i < nvec) st_stream(o + (base + 64 * i) * 8, v[i]);
+  for (int i = 0; i < U; ++i) {
+    const uint32_t n = base + 256u * i;
+    dst[i] = -1;
+    if (n < a.nvec) {
+      const uint32_t t = a.vpr.div(n), c = n - t * a.vpr.d;
+      const int id = a.ids[t];
+      dst[i] = (int64_t)t * a.out_rs + (int64_t)c * 8;
+      v[i] = (id >= 0 && (int64_t)id < a.V) ? ld16(a.W + (int64_t)id * a.w_rs + (int64_t)c * 8)
+                                            : make_uint4(0, 0, 0, 0);
     }
   }
+#pragma unroll
+  for (int i = 0; i < U; ++i)
+    if (dst[i] >= 0) st_stream(a.out + dst[i], v[i]);
 }
 
 __global__ __launch_bounds__(256) void embed_scalar(EmbedArgs a) {
@@ -66,12 +68,25 @@ extern "C" int pie_hip_embedding(const int32_t* ids, int64_t T, const pie_bf16* 
   if (T == 0 || H == 0) return PIE_HIP_OK;
   PIE_REQUIRE(ids && out && (W || V == 0), "embedding: null pointer");
   PIE_REQUIRE(w_row_stride >= H && out_row_stride >= H, "embedding: row stride smaller than H");
-  EmbedArgs a{ids, W, out, T, V, H, w_row_stride, out_row_stride};
-  const int64_t blocks = (T + 3) / 4, cap = (int64_t)num_cus() * 64;
-  const dim3 grd((unsigned)(blocks < cap ? blocks : cap)), blk(256);
+  EmbedArgs a{ids, W, out, T, V, H, w_row_stride, out_row_stride, 0, FastDiv{}};
+  const dim3 blk(256);
+  const hipStream_t st = (hipStream_t)stream;
+  const int64_t nvec = T * (H / 8);
   const bool vec = H % 8 == 0 && w_row_stride % 8 == 0 && out_row_stride % 8 == 0 &&
-                   (V == 0 || aligned16(W)) && aligned16(out);
-  if (vec) hipLaunchKernelGGL(embed_vec<8>, grd, blk, 0, (hipStream_t)stream, a);
-  else hipLaunchKernelGGL(embed_scalar, grd, blk, 0, (hipStream_t)stream, a);
+                   (V == 0 || aligned16(W)) && aligned16(out) && nvec < (1ll << 31);
+  if (vec) {
+    a.nvec = (uint32_t)nvec;
+    a.vpr = FastDiv::make((uint32_t)(H / 8));
+    const int64_t target = (int64_t)num_cus() * 16;
+    if (nvec >= target * 256 * 4)
+      hipLaunchKernelGGL(embed_vec<4>, dim3((unsigned)((nvec + 1023) / 1024)), blk, 0, st, a);
+    else if (nvec >= target * 256 * 2)
+      hipLaunchKernelGGL(embed_vec<2>, dim3((unsigned)((nvec + 511) / 512)), blk, 0, st, a);
+    else
+      hipLaunchKernelGGL(embed_vec<1>, dim3((unsigned)((nvec + 255) / 256)), blk, 0, st, a);
+  } else {
+    const int64_t blocks = (T + 3) / 4, cap = (int64_t)num_cus() * 64;
+    hipLaunchKernelGGL(embed_scalar, dim3((unsigned)(blocks < cap ? blocks : cap)), blk, 0, st, a);
+  }
   return check_launch("embedding");
 }

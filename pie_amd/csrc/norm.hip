@@ -52,57 +52,79 @@ __device__ __forceinline__ void row_offsets(const RowSet& s, int64_t r, int64_t&
   oo = t * s.out_ts + h * s.out_hs;
 }
 
-// ---------------------------------------------------------------- one wave per row, NV*512 cols
-template <int NV, bool ADD>
-__global__ __launch_bounds__(256) void rmsnorm_rows_reg(NormArgs a) {
+// ---------------------------------------------------------------- W waves per row, VPL*512*W cols
+// A row is held in registers by a group of W wavefronts (VPL 16-byte vectors per lane); lane l
+// of wave g in the group owns vectors j*64*W + g*64 + l. W = 1 for long row lists (no barrier);
+// W > 1 spreads short lists (decode batches) over the chip, combining the W partial sums of
+// squares through LDS in a fixed order. The weight row stays in registers across rows.
+template <int VPL, bool ADD>
+__global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
+  __shared__ float part[8];
   const RowSet& s = a.set[0];
-  const int lane = threadIdx.x & 63;
-  const int64_t wave0 = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
-  if (wave0 >= s.rows) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = wave / W, gsub = wave - grp * W;
+  const int G = blockDim.x / (64 * W);  // row groups per block
+  const int64_t stride = (int64_t)gridDim.x * G;
+  const int vstep = 64 * W;
+  const int v0 = gsub * 64 + lane;
 
-  uint4 wv[NV];
+  uint4 wv[VPL];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) wv[j] = ld16(s.w + (lane + 64 * j) * 8);
+  for (int j = 0; j < VPL; ++j) wv[j] = ld16(s.w + (int64_t)(v0 + j * vstep) * 8);
 
-  for (int64_t r = wave0; r < s.rows; r += nwaves) {
-    int64_t oi, orr, os, oo;
-    row_offsets(s, r, oi, orr, os, oo);
-    uint4 xv[NV];
+  // block-uniform trip count: every thread reaches every barrier
+  for (int64_t base = (int64_t)blockIdx.x * G; base < s.rows; base += stride) {
+    const int64_t r = base + grp;
+    const bool live = r < s.rows;
+    int64_t oi = 0, orr = 0, os = 0, oo = 0;
+    if (live) row_offsets(s, r, oi, orr, os, oo);
+    uint4 xv[VPL];
+    float ss = 0.f;
+    if (live) {
 #pragma unroll
-    for (int j = 0; j < NV; ++j) xv[j] = ld_stream(s.in + oi + (lane + 64 * j) * 8);
-    if constexpr (ADD) {
-      uint4 rv[NV];
+      for (int j = 0; j < VPL; ++j) xv[j] = ld_stream(s.in + oi + (int64_t)(v0 + j * vstep) * 8);
+      if constexpr (ADD) {
+        uint4 rv[VPL];
 #pragma unroll
-      for (int j = 0; j < NV; ++j) rv[j] = ld_stream(s.res + orr + (lane + 64 * j) * 8);
+        for (int j = 0; j < VPL; ++j) rv[j] = ld_stream(s.res + orr + (int64_t)(v0 + j * vstep) * 8);
 #pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        float xf[8], rf[8];
+        for (int j = 0; j < VPL; ++j) {
+          float xf[8], rf[8];
+          unpack8(xv[j], xf);
+          unpack8(rv[j], rf);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xf[e] = rf[e] + xf[e];
+          xv[j] = pack8(xf);  // s rounded to bf16: the norm below reads the rounded values
+          st_stream(s.sum + os + (int64_t)(v0 + j * vstep) * 8, xv[j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        float xf[8];
         unpack8(xv[j], xf);
-        unpack8(rv[j], rf);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xf[e] = rf[e] + xf[e];
-        xv[j] = pack8(xf);  // s rounded to bf16: the norm below reads the rounded values
-        st_stream(s.sum + os + (lane + 64 * j) * 8, xv[j]);
+        for (int e = 0; e < 8; ++e) ss += xf[e] * xf[e];
       }
     }
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      float xf[8];
-      unpack8(xv[j], xf);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss += xf[e] * xf[e];
+    float tot = wave_sum(ss);
+    if (W > 1) {
+      if (lane == 0) part[wave] = tot;
+      __syncthreads();
+      tot = 0.f;
+      for (int k = 0; k < W; ++k) tot += part[grp * W + k];
+      __syncthreads();
     }
-    const float rstd = rsqrtf(wave_sum(ss) / (float)a.cols + a.eps);
+    if (live) {
+      const float rstd = rsqrtf(tot / (float)a.cols + a.eps);
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      float xf[8], wf[8];
-      unpack8(xv[j], xf);
-      unpack8(wv[j], wf);
+      for (int j = 0; j < VPL; ++j) {
+        float xf[8], wf[8];
+        unpack8(xv[j], xf);
+        unpack8(wv[j], wf);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) xf[e] = (xf[e] * rstd) * wf[e];
-      st_stream(s.out + oo + (lane + 64 * j) * 8, pack8(xf));
+        for (int e = 0; e < 8; ++e) xf[e] = (xf[e] * rstd) * wf[e];
+        st_stream(s.out + oo + (int64_t)(v0 + j * vstep) * 8, pack8(xf));
+      }
     }
   }
 }
@@ -256,16 +278,32 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
   const bool vec = a.cols % 8 == 0 && rowset_vec_ok(a.set[0], ADD) &&
                    (a.set[1].rows == 0 || rowset_vec_ok(a.set[1], ADD));
   const dim3 blk(256);
-  if (vec && a.set[1].rows == 0 && a.cols % 512 == 0 && a.cols <= 16 * 512) {
-    const dim3 grd((unsigned)wave_grid(rows));
-    switch (a.cols / 512) {
-#define PIE_NV(n) \
-  case n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, ADD>), grd, blk, 0, st, a); break;
-      PIE_NV(1) PIE_NV(2) PIE_NV(3) PIE_NV(4) PIE_NV(5) PIE_NV(6) PIE_NV(7) PIE_NV(8)
-      PIE_NV(9) PIE_NV(10) PIE_NV(11) PIE_NV(12) PIE_NV(13) PIE_NV(14) PIE_NV(15) PIE_NV(16)
-#undef PIE_NV
+  if (vec && a.set[1].rows == 0 && a.cols % 512 == 0 && a.cols <= 8 * 16 * 512) {
+    // waves per row: the fewest that give the device ~16 waves per CU (and at most 16
+    // vectors per lane)
+    const int64_t n512 = a.cols / 512, target = (int64_t)num_cus() * 16;
+    int W = 0;
+    for (int w = 1; w <= 8; w *= 2) {
+      if (n512 % w != 0 || n512 / w > 16) continue;
+      W = w;  // the largest valid group if none reaches the target
+      if (rows * w >= target) break;
     }
-    return check_launch(name);
+    if (W > 0) {
+      const int threads = W == 8 ? 512 : 256;
+      const int64_t G = threads / (64 * W);
+      int64_t blocks = (rows + G - 1) / G;
+      const int64_t cap = (int64_t)num_cus() * 64;
+      if (blocks > cap) blocks = cap;
+      const dim3 grd((unsigned)blocks), tb(threads);
+      switch (n512 / W) {
+#define PIE_NV(n) \
+  case n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, ADD>), grd, tb, 0, st, a, W); break;
+        PIE_NV(1) PIE_NV(2) PIE_NV(3) PIE_NV(4) PIE_NV(5) PIE_NV(6) PIE_NV(7) PIE_NV(8)
+        PIE_NV(9) PIE_NV(10) PIE_NV(11) PIE_NV(12) PIE_NV(13) PIE_NV(14) PIE_NV(15) PIE_NV(16)
+#undef PIE_NV
+      }
+      return check_launch(name);
+    }
   }
   if (!ADD && vec && (a.cols == 64 || a.cols == 128 || a.cols == 256)) {
     const int64_t threads = rows * 16;

@@ -102,9 +102,6 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   }
   if (!live) return;
 
-  int64_t kc = -1;
-  if constexpr (APPEND) kc = slot_offset(a.c, t);
-
   const int uph = ROPE ? (INTERLEAVE ? h.rd >> 3 : h.rd >> 4) : 0;  // rope units per head
   const int nq = ROPE ? h.Hq * uph : 0;
   const int nk = ROPE ? h.Hkv * uph : 0;
@@ -112,70 +109,98 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   const int nkt = APPEND ? h.Hkv * tail : 0;
   const int dv = h.D >> 3;
   const int nv = APPEND ? h.Hkv * dv : 0;
-  const int total = nq + nk + nkt + nv;
+  const int nrope = nq + nk;
+  const int total = nrope + nkt + nv;
   const float2* tb = tab[slot];
 
-  for (int u = gt; u < total; u += gsize) {
-    if (ROPE && u < nq + nk) {
-      const bool isq = u < nq;
-      const int uu = isq ? u : u - nq;
-      const int head = uu / uph, c = uu - head * uph;
-      uint16_t* base = isq ? h.q + t * h.q_ts + (int64_t)head * h.q_hs
-                           : h.k + t * h.k_ts + (int64_t)head * h.k_hs;
-      if constexpr (!INTERLEAVE) {
-        uint16_t* px = base + c * 8;
-        uint16_t* py = px + half;
-        float x[8], y[8];
-        unpack8(ld16(px), x);
-        unpack8(ld16(py), y);
+  // The page lookup is a chain of three dependent loads; it is only needed by the stores, so
+  // its loads are issued before the data loads and consumed after them.
+  int64_t kc = -1;
+  if constexpr (APPEND) kc = slot_offset(a.c, t);
+
+  // Batches of UB units per lane: all loads of a batch are issued before any math or store
+  // (a store may alias a later load as far as the compiler knows, so without batching each
+  // lane would have a single 16-byte load in flight).
+  constexpr int UB = 4;
+  for (int u0 = gt; u0 < total; u0 += gsize * UB) {
+    uint4 X[UB], Y[UB];
+    uint16_t* P[UB];  // rope: x chunk (updated in place); copy: source
+    int head[UB], c[UB], kind[UB];  // kind: 0 q rope, 1 k rope, 2 k tail copy, 3 v copy, -1 none
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float2 cs = tb[c * 8 + e];
-          const float xr = rot_x(x[e], y[e], cs);
-          const float yr = rot_y(x[e], y[e], cs);
-          x[e] = xr;
-          y[e] = yr;
+    for (int i = 0; i < UB; ++i) {
+      const int u = u0 + i * gsize;
+      kind[i] = -1;
+      if (u >= total) continue;
+      if (ROPE && u < nrope) {
+        const bool isq = u < nq;
+        const int uu = isq ? u : u - nq;
+        head[i] = uu / uph;
+        c[i] = uu - head[i] * uph;
+        kind[i] = isq ? 0 : 1;
+        P[i] = (isq ? h.q + t * h.q_ts + (int64_t)head[i] * h.q_hs
+                    : h.k + t * h.k_ts + (int64_t)head[i] * h.k_hs) + c[i] * 8;
+        X[i] = ld16(P[i]);
+        if constexpr (!INTERLEAVE) Y[i] = ld16(P[i] + half);
+      } else if (APPEND) {
+        int uu = u - nrope;
+        if (uu < nkt) {
+          head[i] = uu / tail;
+          c[i] = (ROPE ? h.rd : 0) + (uu - head[i] * tail) * 8;  // element offset in the head
+          kind[i] = 2;
+          P[i] = h.k + t * h.k_ts + (int64_t)head[i] * h.k_hs + c[i];
+        } else {
+          uu -= nkt;
+          head[i] = uu / dv;
+          c[i] = (uu - head[i] * dv) * 8;
+          kind[i] = 3;
+          P[i] = const_cast<uint16_t*>(h.v) + t * h.v_ts + (int64_t)head[i] * h.v_hs + c[i];
         }
-        const uint4 xo = pack8(x), yo = pack8(y);
-        st16(px, xo);
-        st16(py, yo);
-        if (APPEND && !isq && kc >= 0) {
-          uint16_t* dst = a.c.k_cache + kc + (int64_t)head * a.c.head_stride + c * 8;
-          st_stream(dst, xo);
-          st_stream(dst + half, yo);
-        }
-      } else {
-        uint16_t* px = base + c * 8;
-        float f[8];
-        unpack8(ld16(px), f);
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const float2 cs = tb[c * 4 + m];
-          const float xr = rot_x(f[2 * m], f[2 * m + 1], cs);
-          const float yr = rot_y(f[2 * m], f[2 * m + 1], cs);
-          f[2 * m] = xr;
-          f[2 * m + 1] = yr;
-        }
-        const uint4 o = pack8(f);
-        st16(px, o);
-        if (APPEND && !isq && kc >= 0)
-          st_stream(a.c.k_cache + kc + (int64_t)head * a.c.head_stride + c * 8, o);
+        X[i] = ld_stream(P[i]);
       }
-      continue;
     }
-    if constexpr (APPEND) {
-      if (kc < 0) break;
-      int uu = u - nq - nk;
-      if (uu < nkt) {
-        const int head = uu / tail, c = uu - head * tail;
-        const int d = (ROPE ? h.rd : 0) + c * 8;
-        const uint4 v = ld_stream(h.k + t * h.k_ts + (int64_t)head * h.k_hs + d);
-        st_stream(a.c.k_cache + kc + (int64_t)head * a.c.head_stride + d, v);
-      } else {
-        uu -= nkt;
-        const int head = uu / dv, c = uu - head * dv;
-        const uint4 v = ld_stream(h.v + t * h.v_ts + (int64_t)head * h.v_hs + c * 8);
-        st_stream(a.c.v_cache + kc + (int64_t)head * a.c.head_stride + c * 8, v);
+#pragma unroll
+    for (int i = 0; i < UB; ++i) {
+      if (kind[i] < 0) continue;
+      if (ROPE && kind[i] <= 1) {
+        if constexpr (!INTERLEAVE) {
+          float x[8], y[8];
+          unpack8(X[i], x);
+          unpack8(Y[i], y);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float2 cs = tb[c[i] * 8 + e];
+            const float xr = rot_x(x[e], y[e], cs);
+            const float yr = rot_y(x[e], y[e], cs);
+            x[e] = xr;
+            y[e] = yr;
+          }
+          const uint4 xo = pack8(x), yo = pack8(y);
+          st16(P[i], xo);
+          st16(P[i] + half, yo);
+          if (APPEND && kind[i] == 1 && kc >= 0) {
+            uint16_t* dst = a.c.k_cache + kc + (int64_t)head[i] * a.c.head_stride + c[i] * 8;
+            st_stream(dst, xo);
+            st_stream(dst + half, yo);
+          }
+        } else {
+          float f[8];
+          unpack8(X[i], f);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            const float2 cs = tb[c[i] * 4 + m];
+            const float xr = rot_x(f[2 * m], f[2 * m + 1], cs);
+            const float yr = rot_y(f[2 * m], f[2 * m + 1], cs);
+            f[2 * m] = xr;
+            f[2 * m + 1] = yr;
+          }
+          const uint4 o = pack8(f);
+          st16(P[i], o);
+          if (APPEND && kind[i] == 1 && kc >= 0)
+            st_stream(a.c.k_cache + kc + (int64_t)head[i] * a.c.head_stride + c[i] * 8, o);
+        }
+      } else if (APPEND && kc >= 0) {
+        uint16_t* cache = kind[i] == 2 ? a.c.k_cache : a.c.v_cache;
+        st_stream(cache + kc + (int64_t)head[i] * a.c.head_stride + c[i], X[i]);
       }
     }
   }

@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "../../include/pie_hip.h"
+#include "../../pie_amd/csrc/common.h"
 
 extern "C" {
 void oracle_rmsnorm(const uint16_t*, int64_t, int64_t, const uint16_t*, uint16_t*, int64_t, int64_t,
@@ -238,15 +239,36 @@ static void case_index(int64_t B) {
   check_equal("positions", po.p, wpo.p, pg.T);
 }
 
+static void case_fastdiv() {
+  printf("fastdiv\n");
+  size_t bad = 0, n = 0;
+  std::uniform_int_distribution<uint32_t> du(0, 0xffffffffu);
+  const uint32_t ds[] = {1, 2, 3, 5, 7, 64, 96, 100, 512, 1536, 1792, 3000, 65535, 65536, 1000003,
+                         0x7fffffffu, 0x80000000u, 0xfffffffbu};
+  for (uint32_t d : ds) {
+    const pie::FastDiv f = pie::FastDiv::make(d);
+    for (int i = 0; i < 20000; ++i, ++n) {
+      const uint32_t x = i < 4 ? (uint32_t[]){0u, d - 1, d, 0xffffffffu}[i] : du(rng);
+      bad += f.div(x) != x / d;
+    }
+  }
+  printf("  %-40s %s (%zu / %zu wrong)\n", "FastDiv vs /", bad ? "FAIL" : "ok", bad, n);
+  failures += bad != 0;
+}
+
 int main(int argc, char** argv) {
   std::string c = argc > 1 ? argv[1] : "all";
   const bool all = c == "all";
+  if (all || c == "fastdiv") case_fastdiv();
   if (all || c == "norm") {
     case_norm(3, 512);
     case_norm(5, 4096);
     case_norm(2, 896);
     case_norm(3, 100);
     case_norm(4, 128);
+    case_norm(3, 5120);   // W = 2 waves per row
+    case_norm(2, 2048);   // W = 4
+    case_norm(40, 1024);  // W = 2, several row groups per block
   }
   if (all || c == "qk") {
     case_qk(5, 4, 2, 128);
@@ -256,10 +278,13 @@ int main(int argc, char** argv) {
   if (all || c == "silu") {
     case_silu(3, 1536);
     case_silu(2, 13);
+    case_silu(8, 2048);   // 2 vectors per thread
+    case_silu(9, 4096);   // 4 vectors per thread
   }
   if (all || c == "embed") {
     case_embed(50, 4096, 9);
     case_embed(20, 100, 5);
+    case_embed(64, 4096, 40);  // 4 vectors per thread
   }
   if (all || c == "rope") case_rope_append(3, 4, 2, 128, 0, 40, 1, 20, false);
   if (all || c == "fused") {

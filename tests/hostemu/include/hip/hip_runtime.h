@@ -36,7 +36,7 @@ inline const char* hipGetErrorString(hipError_t) { return "emulated"; }
 inline hipError_t hipGetDevice(int* d) { *d = 0; return hipSuccess; }
 inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
   const char* e = getenv("EMU_CUS");
-  *v = e ? atoi(e) : 2;  // few "CUs" so grid caps engage and grid-stride loops iterate
+  *v = e ? atoi(e) : 1;  // few "CUs" so grid caps engage and grid-stride loops iterate
   return hipSuccess;
 }
 
@@ -148,3 +148,4 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 
 inline float __uint_as_float(unsigned u) { float f; memcpy(&f, &u, 4); return f; }
 inline float rsqrtf(float x) { return 1.0f / sqrtf(x); }
+inline unsigned __umulhi(unsigned a, unsigned b) { return (unsigned)(((unsigned long long)a * b) >> 32); }
