@@ -39,34 +39,37 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (needs ROCm)")
 
 
-def _compile(hipcc: str, src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(hipcc: str, src: Path, build_dir: Path, defines: tuple[str, ...]) -> Path:
+    obj = build_dir / (src.stem + ".o")
+    cmd = [hipcc, *HIP_FLAGS, *[f"-D{d}" for d in defines], "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every kernel source and link libpie_hip.so; returns the library path."""
+def build(verbose: bool = False, out: Path | None = None, defines: tuple[str, ...] = ()) -> Path:
+    """Compile every kernel source and link libpie_hip.so (or ``out``); returns its path.
+    ``defines`` (e.g. ``("PIE_NT_LOAD=0",)``) produce measurement variants of the library."""
     hipcc = _hipcc()
-    BUILD.mkdir(exist_ok=True)
+    lib = Path(out) if out else LIB
+    build_dir = BUILD if not defines else BUILD / ("v_" + "_".join(defines).replace("=", ""))
+    build_dir.mkdir(parents=True, exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))
     if not srcs:
         raise RuntimeError(f"no kernel sources under {CSRC}")
     jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")), 16)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(hipcc, s), srcs))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda s: _compile(hipcc, s, build_dir, tuple(defines)), srcs))
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
 
 
 if __name__ == "__main__":

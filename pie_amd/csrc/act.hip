@@ -42,8 +42,8 @@ __global__ __launch_bounds__(256) void silu_and_mul_vec(SiluArgs a) {
     if (v < a.nvec) {
       const uint32_t row = a.vpr.div(v), c = v - row * a.vpr.d;
       const uint16_t* g = a.in + (int64_t)row * a.in_rs + (int64_t)c * 8;
-      gv[i] = ld_stream(g);
-      uv[i] = ld_stream(g + a.I);
+      gv[i] = ld_nt(g);
+      uv[i] = ld_nt(g + a.I);
       orow[i] = (int64_t)row * a.out_rs + (int64_t)c * 8;
     }
   }
@@ -55,7 +55,7 @@ __global__ __launch_bounds__(256) void silu_and_mul_vec(SiluArgs a) {
       unpack8(uv[i], uf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) gf[e] = silu_bf(gf[e]) * uf[e];
-      st_stream(a.out + orow[i], pack8(gf));
+      st16(a.out + orow[i], pack8(gf));
     }
   }
 }

@@ -5,7 +5,7 @@
 // The grid is flattened over 16-byte output vectors (1 KiB of one table row per wave
 // instruction), so a decode batch of a few hundred tokens still spreads over every CU. Table
 // rows are loaded with the normal cached path so the repeated ids of a batch are served from
-// L2/MALL; the output is written non-temporally.
+// L2/MALL.
 #include "common.h"
 
 namespace pie {
@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256) void embed_vec(EmbedArgs a) {
   }
 #pragma unroll
   for (int i = 0; i < U; ++i)
-    if (dst[i] >= 0) st_stream(a.out + dst[i], v[i]);
+    if (dst[i] >= 0) st16(a.out + dst[i], v[i]);
 }
 
 __global__ __launch_bounds__(256) void embed_scalar(EmbedArgs a) {

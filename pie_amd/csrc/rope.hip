@@ -58,6 +58,14 @@ struct RopeAppendArgs {
   float inv_freq[kMaxPairs];
 };
 
+// Cache-page stores: non-temporal in the fused RoPE+append kernel, cached in the plain append
+// (measured fastest for each).
+template <bool FUSED>
+__device__ __forceinline__ void st_cache(void* p, const uint4& v) {
+  if constexpr (FUSED) st_nt(p, v);
+  else st16(p, v);
+}
+
 // The rotation with its fused multiply-adds spelled out, so every kernel variant (rope only,
 // fused with the append, scalar fallback) rounds identically: x' = x c - y s, y' = x s + y c.
 __device__ __forceinline__ float rot_x(float x, float y, float2 cs) { return fmaf(x, cs.x, -(y * cs.y)); }
@@ -113,10 +121,10 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   const int total = nrope + nkt + nv;
   const float2* tb = tab[slot];
 
-  // The page lookup is a chain of three dependent loads; it is only needed by the stores, so
-  // its loads are issued before the data loads and consumed after them.
+  // The page lookup is a chain of three dependent loads that only the stores need: it runs
+  // after the first batch's data loads are in flight instead of in front of them.
   int64_t kc = -1;
-  if constexpr (APPEND) kc = slot_offset(a.c, t);
+  bool have_kc = false;
 
   // Batches of UB units per lane: all loads of a batch are issued before any math or store
   // (a store may alias a later load as far as the compiler knows, so without batching each
@@ -155,7 +163,13 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
           kind[i] = 3;
           P[i] = const_cast<uint16_t*>(h.v) + t * h.v_ts + (int64_t)head[i] * h.v_hs + c[i];
         }
-        X[i] = ld_stream(P[i]);
+        X[i] = ld_nt(P[i]);
+      }
+    }
+    if constexpr (APPEND) {
+      if (!have_kc) {
+        kc = slot_offset(a.c, t);
+        have_kc = true;
       }
     }
 #pragma unroll
@@ -179,8 +193,8 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
           st16(P[i] + half, yo);
           if (APPEND && kind[i] == 1 && kc >= 0) {
             uint16_t* dst = a.c.k_cache + kc + (int64_t)head[i] * a.c.head_stride + c[i] * 8;
-            st_stream(dst, xo);
-            st_stream(dst + half, yo);
+            st_cache<ROPE>(dst, xo);
+            st_cache<ROPE>(dst + half, yo);
           }
         } else {
           float f[8];
@@ -196,11 +210,11 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
           const uint4 o = pack8(f);
           st16(P[i], o);
           if (APPEND && kind[i] == 1 && kc >= 0)
-            st_stream(a.c.k_cache + kc + (int64_t)head[i] * a.c.head_stride + c[i] * 8, o);
+            st_cache<ROPE>(a.c.k_cache + kc + (int64_t)head[i] * a.c.head_stride + c[i] * 8, o);
         }
       } else if (APPEND && kc >= 0) {
         uint16_t* cache = kind[i] == 2 ? a.c.k_cache : a.c.v_cache;
-        st_stream(cache + kc + (int64_t)head[i] * a.c.head_stride + c[i], X[i]);
+        st_cache<ROPE>(cache + kc + (int64_t)head[i] * a.c.head_stride + c[i], X[i]);
       }
     }
   }
