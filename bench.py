@@ -1,6 +1,6 @@
 """Benchmark of the per-layer hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only main|ops|copy] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only main|ops|copy|chain] [--no-cpu]
 
 One step = one pass of the fused residual-add + RMSNorm [8192, 4096] followed by SiLU-and-mul
 [8192, 2x14336] (configuration 2, Llama-3-8B prefill), inputs resident in HBM. Prints ONE JSON
@@ -158,12 +158,12 @@ def measure_ops(dev, iters=50, cold_iters=20):
     chain_bytes = sum(wl.cfg5_bytes().values())
     ms = _events(g.replay, 200)
     ms_cold = _events(g.replay, cold_iters, flush)
-    e = _op_entry("cfg5 decode chain (graph, 5 launches)", chain_bytes, ms, ms_cold)
-    e["launches"] = 5
+    e = _op_entry("cfg5 decode chain (graph, 4 launches)", chain_bytes, ms, ms_cold)
+    e["launches"] = 4
     res.append(e)
     ch2 = DecodeChain(c, dev, fused=False)
     ms_eager = _events(ch2.run, 50)
-    res.append({"op": "cfg5 decode chain (eager, 6 launches)", "us_hot": round(statistics.median(ms_eager) * 1e3, 2)})
+    res.append({"op": "cfg5 decode chain (eager, 6 launches: unfused)", "us_hot": round(statistics.median(ms_eager) * 1e3, 2)})
     del scratch
     return res
 
@@ -173,7 +173,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["all", "main", "ops", "copy"], default="all")
+    ap.add_argument("--only", choices=["all", "main", "ops", "copy", "chain"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -194,6 +194,16 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "copy", "bytes_read": a.numel(), "bytes_written": b.numel(),
                           "launches": args.steps}))
+        return
+
+    if args.only == "chain":  # decode chain graph replays alone (for kernel traces)
+        from pie_amd.chain import DecodeChain
+        ch = DecodeChain(wl.cfg5(), dev, fused=True)
+        g = ch.capture()
+        for _ in range(args.warmup):
+            g.replay()
+        ms = _events(g.replay, args.steps)
+        print(json.dumps({"chain_us_median": round(statistics.median(ms) * 1e3, 2), "replays": args.steps}))
         return
 
     ops_res = None

@@ -162,6 +162,29 @@ int pie_hip_rope_append(pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride
                         int64_t page_size, void* stream);
 
 /*
+ * Per-head q/k RMSNorm + standard/any-frequency RoPE + paged append in one pass: the
+ * consecutive calls of pie/src/pie_worker/model/qwen3.py:651-684 (fun.rms_norm on q and k,
+ * flashinfer.apply_rope_pos_ids_inplace, flashinfer.append_paged_kv_cache). Reads q/k/v (views
+ * of the qkv projection), writes normalised+rotated q_out/k_out and the k/v cache rows. Full
+ * rotary dim, half-split pairs. Results equal pie_hip_qk_rmsnorm followed by
+ * pie_hip_rope_append on (q_out, k_out, v) bit for bit (that path is taken for D != 128 or
+ * unaligned tensors).
+ */
+int pie_hip_qk_rmsnorm_rope_append(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                   const pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                                   const pie_bf16* v, int64_t v_tok_stride, int64_t v_head_stride,
+                                   pie_bf16* q_out, int64_t qo_tok_stride, int64_t qo_head_stride,
+                                   pie_bf16* k_out, int64_t ko_tok_stride, int64_t ko_head_stride,
+                                   const pie_bf16* qw, const pie_bf16* kw, float eps,
+                                   const int32_t* pos, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                                   const float* inv_freq, const int32_t* batch_indices,
+                                   const int32_t* positions, const int32_t* kv_indices,
+                                   const int32_t* kv_indptr, int64_t batch_size,
+                                   pie_bf16* k_cache, pie_bf16* v_cache, int64_t num_pages,
+                                   int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                                   int64_t page_size, void* stream);
+
+/*
  * seq_lens[b] = (kv_indptr[b+1]-kv_indptr[b]-1)*page_size + last_page_len[b], or 0 when the
  * request holds no page. Replaces flashinfer.get_seq_lens (llama3.py:745-749;
  * spec pie/src/flashinfer_metal/ops.py:392-407).

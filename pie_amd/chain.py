@@ -6,6 +6,7 @@ out (they are not part of this path):
   (2) residual add + RMSNorm      qwen3.py:571 -> :538
   (3) per-head q/k RMSNorm        qwen3.py:651-662
   (4) RoPE at each sequence's position and (5) paged-KV append   qwen3.py:665-684
+      (fused=True runs (3)-(5) as one kernel, fused=False as three launches)
   (6) SiLU-and-mul                qwen3.py:553-556
 All buffers are preallocated, so ``run()`` launches kernels only and can be captured into a
 HIP graph (``capture()``), as the reference captures its decode layers (llama3.py:315-414).
@@ -57,13 +58,13 @@ class DecodeChain:
         ops.add_rms_norm(self.hidden, self.residual, self.w_norm, self.eps, out=self.normed,
                          residual_out=self.residual)
         q, k, v = wl.split_qkv(self.qkv0, self.Hq, self.Hkv, self.D)
-        ops.qk_rms_norm(q, k, self.q_norm, self.k_norm, self.eps, q_out=self.q_out, k_out=self.k_out)
         if self.fused:
-            ops.apply_rope_pos_ids_and_append_paged_kv_cache(
-                self.q_out, self.k_out, v, b["positions"], b["batch_indices"], b["positions"],
-                self.cache, b["kv_indices"], b["kv_indptr"], b["kv_last_page_len"],
-                rope_theta=self.theta)
+            ops.qk_rms_norm_rope_append(
+                q, k, v, self.q_norm, self.k_norm, self.eps, b["positions"], b["batch_indices"],
+                b["positions"], self.cache, b["kv_indices"], b["kv_indptr"],
+                b["kv_last_page_len"], rope_theta=self.theta, q_out=self.q_out, k_out=self.k_out)
         else:
+            ops.qk_rms_norm(q, k, self.q_norm, self.k_norm, self.eps, q_out=self.q_out, k_out=self.k_out)
             ops.apply_rope_pos_ids_inplace(self.q_out, self.k_out, b["positions"],
                                            rope_theta=self.theta)
             ops.append_paged_kv_cache(self.k_out, v, b["batch_indices"], b["positions"],

@@ -220,6 +220,101 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- q/k RMSNorm + RoPE + append
+// Qwen3's attention prologue (qwen3.py:651-684: per-head q/k RMSNorm, RoPE, paged append) in
+// one pass for D = 128, full rotary dim, half-split pairs. A 16-lane group owns one head row
+// (8 elements per lane): it normalises the row exactly as rmsnorm_heads16 does (same sum
+// order), rounds to bf16, fetches the rotation partner's 8 values from lane l^8 with DPP
+// row_ror:8, rotates exactly as rope_append_vec does, and stores q_out/k_out (and k, v to the
+// cache page). Results are bit-identical to the three separate kernels. Every lane runs the
+// same instruction sequence (stores are predicated), so the DPP exchanges never sit in
+// divergent code.
+struct QkNormArgs {
+  RopeAppendArgs r;  // q/k/v inputs, cache, pos, T, wpt, inv_freq
+  uint16_t* q_out;
+  uint16_t* k_out;
+  int64_t qo_ts, qo_hs, ko_ts, ko_hs;
+  const uint16_t* qw;
+  const uint16_t* kw;
+  float eps;
+};
+
+__device__ __forceinline__ uint32_t dpp_ror8(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
+}
+
+__global__ __launch_bounds__(256) void qk_norm_rope_append_d128(QkNormArgs qa) {
+  const RopeAppendArgs& a = qa.r;
+  __shared__ float2 tab[4][64];
+  const int wpt = a.wpt;
+  const int tpb = 4 / wpt;
+  const int slot = (threadIdx.x >> 6) / wpt;
+  const int gt = threadIdx.x - slot * wpt * 64;
+  const int gsize = wpt * 64;
+  const int64_t t = (int64_t)blockIdx.x * tpb + slot;
+  const bool live = t < a.T;
+  const HeadsDesc& h = a.h;
+  if (live) {
+    const float p = (float)a.pos[t];
+    for (int i = gt; i < 64; i += gsize) {
+      float sn, cs;
+      sincosf(p * a.inv_freq[i], &sn, &cs);
+      tab[slot][i] = make_float2(cs, sn);
+    }
+  }
+  __syncthreads();
+  if (!live) return;  // whole token groups (waves) leave together
+
+  const int sub = gt & 15;            // lane within the head row
+  const int lo = sub & 7;             // pair block: pairs lo*8 .. lo*8+7
+  const bool is_x = sub < 8;          // holds the x half (dims < 64) of its pairs
+  const float2* tb = tab[slot] + lo * 8;
+  const int nrows = h.Hq + 2 * h.Hkv;  // q heads, k heads, v heads
+  const int64_t kc = slot_offset(a.c, t);
+
+  // uniform trip count over the wave: all 64 lanes execute every DPP exchange
+  for (int r0 = (gt >> 4); r0 - (gt >> 4) < nrows; r0 += gsize >> 4) {
+    const int r = r0;
+    const bool on = r < nrows;
+    const int kind = !on ? 3 : (r < h.Hq ? 0 : (r < h.Hq + h.Hkv ? 1 : 2));  // q, k, v, none
+    const int hd = kind == 0 ? r : (kind == 1 ? r - h.Hq : r - h.Hq - h.Hkv);
+    const uint16_t* src = kind == 0 ? h.q + t * h.q_ts + (int64_t)hd * h.q_hs
+                        : kind == 1 ? h.k + t * h.k_ts + (int64_t)hd * h.k_hs
+                                    : h.v + t * h.v_ts + (int64_t)hd * h.v_hs;
+    uint4 xv = make_uint4(0, 0, 0, 0), wv = make_uint4(0, 0, 0, 0);
+    if (on) {
+      xv = kind == 2 ? ld_nt(src + sub * 8) : ld16(src + sub * 8);
+      if (kind < 2) wv = ld16((kind == 0 ? qa.qw : qa.kw) + sub * 8);
+    }
+    float f[8], wf[8];
+    unpack8(xv, f);
+    unpack8(wv, wf);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+    const float rstd = rsqrtf(row16_sum(ss) / 128.0f + qa.eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (f[e] * rstd) * wf[e];
+    const uint4 g = pack8(f);  // normalised row, rounded to bf16 as the separate norm stores it
+    const uint4 pg = make_uint4(dpp_ror8(g.x), dpp_ror8(g.y), dpp_ror8(g.z), dpp_ror8(g.w));
+    float own[8], oth[8];
+    unpack8(g, own);
+    unpack8(pg, oth);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      own[e] = is_x ? rot_x(own[e], oth[e], tb[e]) : rot_y(oth[e], own[e], tb[e]);
+    const uint4 o = pack8(own);
+    if (kind == 0) {
+      st16(qa.q_out + t * qa.qo_ts + (int64_t)hd * qa.qo_hs + sub * 8, o);
+    } else if (kind == 1) {
+      st16(qa.k_out + t * qa.ko_ts + (int64_t)hd * qa.ko_hs + sub * 8, o);
+      if (kc >= 0) st_nt(a.c.k_cache + kc + (int64_t)hd * a.c.head_stride + sub * 8, o);
+    } else if (kind == 2 && kc >= 0) {
+      st_nt(a.c.v_cache + kc + (int64_t)hd * a.c.head_stride + sub * 8, xv);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- scalar fallbacks
 // Any alignment, any D / rd: one thread per (token, head, pair) or (token, head, element).
 __global__ __launch_bounds__(256) void rope_scalar(RopeAppendArgs a) {
@@ -399,4 +494,63 @@ extern "C" int pie_hip_rope_append(pie_bf16* q, int64_t q_tok_stride, int64_t q_
   for (int64_t i = 0; i < rotary_dim / 2; ++i) a.inv_freq[i] = inv_freq[i];
   if (rotary_dim == 0) return launch(a, false, true, 0, (hipStream_t)stream, "rope_append");
   return launch(a, true, Hkv > 0, interleave ? 1 : 0, (hipStream_t)stream, "rope_append");
+}
+
+extern "C" int pie_hip_qk_rmsnorm_rope_append(
+    const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride, const pie_bf16* k,
+    int64_t k_tok_stride, int64_t k_head_stride, const pie_bf16* v, int64_t v_tok_stride,
+    int64_t v_head_stride, pie_bf16* q_out, int64_t qo_tok_stride, int64_t qo_head_stride,
+    pie_bf16* k_out, int64_t ko_tok_stride, int64_t ko_head_stride, const pie_bf16* qw,
+    const pie_bf16* kw, float eps, const int32_t* pos, int64_t T, int64_t Hq, int64_t Hkv,
+    int64_t D, const float* inv_freq, const int32_t* batch_indices, const int32_t* positions,
+    const int32_t* kv_indices, const int32_t* kv_indptr, int64_t batch_size, pie_bf16* k_cache,
+    pie_bf16* v_cache, int64_t num_pages, int64_t page_stride, int64_t slot_stride,
+    int64_t head_stride, int64_t page_size, void* stream) {
+  QkNormArgs qa{};
+  RopeAppendArgs& a = qa.r;
+  int rc = fill_heads(a, const_cast<pie_bf16*>(q), q_tok_stride, q_head_stride,
+                      const_cast<pie_bf16*>(k), k_tok_stride, k_head_stride, v, v_tok_stride,
+                      v_head_stride, T, Hq, Hkv, D, D);
+  if (rc) return rc;
+  rc = fill_cache(a, batch_indices, positions, kv_indices, kv_indptr, batch_size, k_cache, v_cache,
+                  num_pages, page_stride, slot_stride, head_stride, page_size);
+  if (rc) return rc;
+  if (T == 0 || Hq + Hkv == 0) return PIE_HIP_OK;
+  PIE_REQUIRE(pos && inv_freq && (Hq == 0 || (q && q_out && qw)) && (Hkv == 0 || (k && v && k_out && kw)),
+              "qk_rmsnorm_rope_append: null pointer");
+  const bool vec = D == 128 && (Hq == 0 || (heads_vec_ok(q, q_tok_stride, q_head_stride) &&
+                                            heads_vec_ok(q_out, qo_tok_stride, qo_head_stride) &&
+                                            aligned16(qw))) &&
+                   (Hkv == 0 || (heads_vec_ok(k, k_tok_stride, k_head_stride) &&
+                                 heads_vec_ok(v, v_tok_stride, v_head_stride) &&
+                                 heads_vec_ok(k_out, ko_tok_stride, ko_head_stride) && aligned16(kw) &&
+                                 aligned16(k_cache) && aligned16(v_cache) && page_stride % 8 == 0 &&
+                                 slot_stride % 8 == 0 && head_stride % 8 == 0));
+  if (!vec) {  // same results through the separate kernels
+    rc = pie_hip_qk_rmsnorm(q, q_tok_stride, q_head_stride, q_out, qo_tok_stride, qo_head_stride, k,
+                            k_tok_stride, k_head_stride, k_out, ko_tok_stride, ko_head_stride, qw, kw,
+                            T, Hq, Hkv, D, eps, stream);
+    if (rc) return rc;
+    return pie_hip_rope_append(q_out, qo_tok_stride, qo_head_stride, k_out, ko_tok_stride,
+                               ko_head_stride, v, v_tok_stride, v_head_stride, pos, T, Hq, Hkv, D, D,
+                               0, inv_freq, batch_indices, positions, kv_indices, kv_indptr,
+                               batch_size, k_cache, v_cache, num_pages, page_stride, slot_stride,
+                               head_stride, page_size, stream);
+  }
+  a.pos = pos;
+  for (int64_t i = 0; i < D / 2; ++i) a.inv_freq[i] = inv_freq[i];
+  qa.q_out = q_out;
+  qa.k_out = k_out;
+  qa.qo_ts = qo_tok_stride;
+  qa.qo_hs = qo_head_stride;
+  qa.ko_ts = ko_tok_stride;
+  qa.ko_hs = ko_head_stride;
+  qa.qw = qw;
+  qa.kw = kw;
+  qa.eps = eps;
+  a.wpt = pick_wpt(T);
+  const int tpb = 4 / a.wpt;
+  hipLaunchKernelGGL(qk_norm_rope_append_d128, dim3((unsigned)((T + tpb - 1) / tpb)), dim3(256), 0,
+                     (hipStream_t)stream, qa);
+  return check_launch("qk_rmsnorm_rope_append");
 }

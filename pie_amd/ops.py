@@ -16,8 +16,9 @@ replacements for the inline torch expressions:
     silu_and_mul(gate_up)                        fun.silu(gate) * up (llama3.py:569-572)
     embedding(ids, weight)                       fun.embedding      (llama3.py:471)
 
-plus one fused entry with no single reference counterpart:
-    apply_rope_pos_ids_and_append_paged_kv_cache   RoPE + append in one HBM pass.
+plus fused entries with no single reference counterpart:
+    apply_{llama31_,}rope_pos_ids_and_append_paged_kv_cache   RoPE + append in one HBM pass
+    qk_rms_norm_rope_append                      q/k norm + RoPE + append (qwen3.py:651-684)
 
 Every op runs a hand-written gfx950 kernel from libpie_hip.so on the current torch stream.
 Nothing here allocates except the outputs of out-of-place ops (as the reference's torch calls
@@ -39,6 +40,7 @@ __all__ = [
     "append_paged_kv_cache", "apply_rope_pos_ids_and_append_paged_kv_cache",
     "apply_llama31_rope_pos_ids_and_append_paged_kv_cache", "get_seq_lens",
     "get_batch_indices_positions", "rope_inv_freq", "llama31_inv_freq",
+    "qk_rms_norm_rope_append",
 ]
 
 _BF16 = torch.bfloat16
@@ -434,6 +436,38 @@ def apply_llama31_rope_pos_ids_and_append_paged_kv_cache(
                  kv_last_page_len, kv_layout, rotary_dim, interleave,
                  lambda rd: llama31_inv_freq(rd, rope_scale, rope_theta, low_freq_factor,
                                              high_freq_factor, old_context_len))
+
+
+def qk_rms_norm_rope_append(q, k, v, q_weight, k_weight, eps, pos_ids, batch_indices, positions,
+                            paged_kv_cache, kv_indices, kv_indptr, kv_last_page_len,
+                            kv_layout="NHD", rope_scale=1, rope_theta=1e4, q_out=None,
+                            k_out=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Qwen3's attention prologue in one pass (qwen3.py:651-684):
+    q, k = qk_rms_norm(q, k, q_weight, k_weight, eps);
+    apply_rope_pos_ids_inplace(q, k, pos_ids, rope_scale=rope_scale, rope_theta=rope_theta);
+    append_paged_kv_cache(k, v, batch_indices, positions, paged_kv_cache, ...).
+    Returns the normalised, rotated (q, k) (new contiguous tensors unless q_out/k_out given);
+    bit-identical to the three calls."""
+    T, Hq, Hkv, D, rd = _rope_shapes("qk_rms_norm_rope_append", q, k, pos_ids, None)
+    _check("qk_rms_norm_rope_append", _BF16, q_weight=q_weight, k_weight=k_weight)
+    if q_weight.shape != (D,) or k_weight.shape != (D,):
+        raise ValueError("qk_rms_norm_rope_append: weights must be [D]")
+    _append_checks(k, v, batch_indices, positions, kv_indices, kv_indptr, kv_last_page_len)
+    q_out = torch.empty((T, Hq, D), dtype=_BF16, device=q.device) if q_out is None else q_out
+    k_out = torch.empty((T, Hkv, D), dtype=_BF16, device=k.device) if k_out is None else k_out
+    if q_out.shape != q.shape or k_out.shape != k.shape or q_out.stride(2) != 1 or k_out.stride(2) != 1:
+        raise ValueError("qk_rms_norm_rope_append: outputs must match inputs with unit inner stride")
+    kp, vp, npages, ps, ss, hs, P = _cache_desc(paged_kv_cache, kv_layout, Hkv, D)
+    q_weight, k_weight = q_weight.contiguous(), k_weight.contiguous()
+    _lib.call("pie_hip_qk_rmsnorm_rope_append", q.data_ptr(), q.stride(0), q.stride(1),
+              k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+              q_out.data_ptr(), q_out.stride(0), q_out.stride(1), k_out.data_ptr(),
+              k_out.stride(0), k_out.stride(1), q_weight.data_ptr(), k_weight.data_ptr(),
+              C.c_float(_eps(eps)), pos_ids.data_ptr(), T, Hq, Hkv, D,
+              rope_inv_freq(D, rope_scale, rope_theta), batch_indices.data_ptr(),
+              positions.data_ptr(), kv_indices.data_ptr(), kv_indptr.data_ptr(),
+              kv_indptr.numel() - 1, kp, vp, npages, ps, ss, hs, P, _stream(q))
+    return q_out, k_out
 
 
 # ----------------------------------------------------------------------------- index helpers

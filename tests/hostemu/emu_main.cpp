@@ -223,6 +223,40 @@ static void case_rope_append(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int 
   check_equal("cache", cache.p, wcache.p, cache.n);
 }
 
+// q/k RMSNorm + RoPE + append in one kernel vs the three separate entry points (bit-exact).
+static void case_qk_fused(int64_t B, int64_t Hq, int64_t Hkv, int64_t D) {
+  Paged pg = make_paged(B, 16, 100, 3000, 1, 1);
+  const int64_t T = pg.T, row = (Hq + 2 * Hkv) * D, P = pg.P, page_elems = 2 * P * Hkv * D;
+  printf("qk_rmsnorm_rope_append B=%lld Hq=%lld Hkv=%lld D=%lld\n", (long long)B, (long long)Hq,
+         (long long)Hkv, (long long)D);
+  Buf<uint16_t> qkv(T * row), qw(D), kw(D), qa(T * Hq * D), ka(T * Hkv * D), qb(T * Hq * D), kb(T * Hkv * D);
+  Buf<uint16_t> ca(pg.pool * page_elems), cb(pg.pool * page_elems);
+  fill_normal(qkv);
+  fill_normal(qw, 1.f, .1f);
+  fill_normal(kw, 1.f, .1f);
+  for (size_t i = 0; i < ca.n; ++i) ca[i] = cb[i] = 0x7fa5;
+  Buf<int32_t> bidx(T), pos(T), kvi(pg.kv_indices.size()), kvp(B + 1);
+  copy_in(bidx, pg.bidx);
+  copy_in(pos, pg.pos);
+  copy_in(kvi, pg.kv_indices);
+  copy_in(kvp, pg.kv_indptr);
+  float inv[256];
+  rc_ok(pie_hip_rope_inv_freq(inv, D, 1.f, 1e6f), "inv_freq");
+  const uint16_t *q = qkv.p, *k = qkv.p + Hq * D, *v = qkv.p + (Hq + Hkv) * D;
+  rc_ok(pie_hip_qk_rmsnorm_rope_append(q, row, D, k, row, D, v, row, D, qa.p, Hq * D, D, ka.p, Hkv * D, D,
+                                       qw.p, kw.p, 1e-6f, pos.p, T, Hq, Hkv, D, inv, bidx.p, pos.p, kvi.p,
+                                       kvp.p, B, ca.p, ca.p + P * Hkv * D, pg.pool, page_elems, Hkv * D,
+                                       D, P, nullptr), "fused");
+  rc_ok(pie_hip_qk_rmsnorm(q, row, D, qb.p, Hq * D, D, k, row, D, kb.p, Hkv * D, D, qw.p, kw.p, T, Hq,
+                           Hkv, D, 1e-6f, nullptr), "qk_rmsnorm");
+  rc_ok(pie_hip_rope_append(qb.p, Hq * D, D, kb.p, Hkv * D, D, v, row, D, pos.p, T, Hq, Hkv, D, D, 0,
+                            inv, bidx.p, pos.p, kvi.p, kvp.p, B, cb.p, cb.p + P * Hkv * D, pg.pool,
+                            page_elems, Hkv * D, D, P, nullptr), "rope_append");
+  check_equal("q fused == separate", qa.p, qb.p, qa.n);
+  check_equal("k fused == separate", ka.p, kb.p, ka.n);
+  check_equal("cache fused == separate", ca.p, cb.p, ca.n);
+}
+
 static void case_index(int64_t B) {
   printf("index helpers B=%lld\n", (long long)B);
   Paged pg = make_paged(B, 16, 0, 100, 0, 9);
@@ -303,6 +337,11 @@ int main(int argc, char** argv) {
     case_norm(6, 4096);
   }
   if (all || c == "index") case_index(40);
+  if (all || c == "qkfused") {
+    case_qk_fused(5, 4, 2, 128);  // fused kernel
+    case_qk_fused(3, 4, 2, 64);   // D != 128: separate-kernel path
+    case_qk_fused(3, 32, 8, 128);
+  }
   printf("%s\n", failures ? "FAILURES" : "all ok");
   return failures ? 1 : 0;
 }

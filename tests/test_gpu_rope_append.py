@@ -221,3 +221,34 @@ def test_index_helpers_feed_append(dev):
     b, p = ops.get_batch_indices_positions(pb.qo_indptr.to(dev), sl, 64)
     assert_bits_equal(N(b), N(pb.batch_indices))
     assert_bits_equal(N(p), N(pb.positions))
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_qk_norm_rope_append_equals_separate(dev, D):
+    """One-pass q/k norm + RoPE + append (qwen3.py:651-684) == the three calls, bit for bit;
+    and the cache holds the oracle's append of the normalised, rotated k."""
+    print(f"qk_rms_norm_rope_append D={D}", flush=True)
+    pb, qkv, T = _small_batch(seed=9, D=D, ctx_max=300)
+    qkv_d = qkv.to(dev)
+    q, k, v = wl.split_qkv(qkv_d, 4, 2, D)
+    qw, kw = wl.normal((D,), 1, 1.0, 0.1).to(dev), wl.normal((D,), 2, 1.0, 0.1).to(dev)
+    shape = (pb.num_pages, 2, 16, 2, D)
+    d = {n: getattr(pb, n).to(dev) for n in ("batch_indices", "positions", "kv_indices",
+                                             "kv_indptr", "kv_last_page_len")}
+    ca = _cache(shape, "NHD", dev)
+    qa, ka = ops.qk_rms_norm_rope_append(q, k, v, qw, kw, 1e-6, d["positions"], d["batch_indices"],
+                                         d["positions"], ca, d["kv_indices"], d["kv_indptr"],
+                                         d["kv_last_page_len"], rope_theta=1e6)
+    qb, kb = ops.qk_rms_norm(q, k, qw, kw, 1e-6)
+    cb = _cache(shape, "NHD", dev)
+    ops.apply_rope_pos_ids_inplace(qb, kb, d["positions"], rope_theta=1e6)
+    ops.append_paged_kv_cache(kb, v, d["batch_indices"], d["positions"], cb, d["kv_indices"],
+                              d["kv_indptr"], d["kv_last_page_len"])
+    assert_bits_equal(N(qa), N(qb), "q")
+    assert_bits_equal(N(ka), N(kb), "k")
+    assert_bits_equal(N(ca), N(cb), "cache")
+    q0, k0, v0 = wl.split_qkv(qkv, 4, 2, D)
+    wq, wk = oracle.rope(oracle.rmsnorm(N(q0), N(qw), 1e-6), oracle.rmsnorm(N(k0), N(kw), 1e-6),
+                         N(pb.positions), oracle.inv_freq_std(D, 1.0, 1e6))
+    assert_bf16_close(N(qa), wq, what="q vs oracle")
+    assert_bf16_close(N(ka), wk, what="k vs oracle")
