@@ -152,19 +152,52 @@ def measure_ops(dev, iters=50, cold_iters=20):
                          _events(f, cold_iters, flush)))
     del W, out
 
-    c = wl.cfg5()
-    ch = DecodeChain(c, dev, fused=True)
-    g = ch.capture()
-    chain_bytes = sum(wl.cfg5_bytes().values())
-    ms = _events(g.replay, 200)
-    ms_cold = _events(g.replay, cold_iters, flush)
-    e = _op_entry("cfg5 decode chain (graph, 4 launches)", chain_bytes, ms, ms_cold)
-    e["launches"] = 4
-    res.append(e)
-    ch2 = DecodeChain(c, dev, fused=False)
-    ms_eager = _events(ch2.run, 50)
-    res.append({"op": "cfg5 decode chain (eager, 6 launches: unfused)", "us_hot": round(statistics.median(ms_eager) * 1e3, 2)})
+    res.extend(measure_chain(dev, flush, cold_iters))
     del scratch
+    return res
+
+
+def _back_to_back(fn, n, reps=5):
+    """µs per call over n back-to-back calls between two events (median of reps)."""
+    import torch
+    out = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        out.append(a.elapsed_time(b) * 1e3 / n)
+    return statistics.median(out)
+
+
+def measure_chain(dev, flush=None, cold_iters=20):
+    """Configuration 5 (Qwen3-8B decode, 256 sequences): µs per chain.
+    steady: back-to-back HIP-graph replays (host submission overlaps the GPU, as in a serving
+    loop); single: one replay between two events (includes the graph launch latency)."""
+    from pie_amd import workloads as wl
+    from pie_amd.chain import DecodeChain
+    c = wl.cfg5()
+    chain_bytes = sum(wl.cfg5_bytes().values())
+    res = []
+    for fused, launches in ((True, 4), (False, 6)):
+        ch = DecodeChain(c, dev, fused=fused)
+        g = ch.capture()
+        for _ in range(20):
+            g.replay()
+        steady = _back_to_back(g.replay, 100)
+        single = statistics.median(_events(g.replay, 200)) * 1e3
+        e = {"op": f"cfg5 decode chain ({'fused' if fused else 'unfused'}, {launches} launches)",
+             "bytes": chain_bytes, "us_steady": round(steady, 2),
+             "gbs_steady": round(chain_bytes / steady / 1e3, 1),
+             "frac_steady": round(chain_bytes / steady / 1e3 / HBM_PEAK_GBS, 3),
+             "us_single_replay": round(single, 2),
+             "us_eager_steady": round(_back_to_back(ch.run, 50), 2), "launches": launches}
+        if flush is not None and fused:
+            e["us_single_replay_cold"] = round(statistics.median(_events(g.replay, cold_iters, flush)) * 1e3, 2)
+        res.append(e)
+        del ch, g
     return res
 
 
@@ -196,14 +229,8 @@ def main():
                           "launches": args.steps}))
         return
 
-    if args.only == "chain":  # decode chain graph replays alone (for kernel traces)
-        from pie_amd.chain import DecodeChain
-        ch = DecodeChain(wl.cfg5(), dev, fused=True)
-        g = ch.capture()
-        for _ in range(args.warmup):
-            g.replay()
-        ms = _events(g.replay, args.steps)
-        print(json.dumps({"chain_us_median": round(statistics.median(ms) * 1e3, 2), "replays": args.steps}))
+    if args.only == "chain":  # decode chain alone (also for kernel traces)
+        print(json.dumps({"chain": measure_chain(dev)}))
         return
 
     ops_res = None

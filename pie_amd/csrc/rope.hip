@@ -97,19 +97,6 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   const HeadsDesc& h = a.h;
   const int half = h.rd >> 1;
 
-  if constexpr (ROPE) {
-    if (live) {
-      const float p = (float)a.pos[t];
-      for (int i = gt; i < half; i += gsize) {
-        float sn, cs;
-        sincosf(p * a.inv_freq[i], &sn, &cs);
-        tab[slot][i] = make_float2(cs, sn);
-      }
-    }
-    __syncthreads();
-  }
-  if (!live) return;
-
   const int uph = ROPE ? (INTERLEAVE ? h.rd >> 3 : h.rd >> 4) : 0;  // rope units per head
   const int nq = ROPE ? h.Hq * uph : 0;
   const int nk = ROPE ? h.Hkv * uph : 0;
@@ -118,22 +105,16 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   const int dv = h.D >> 3;
   const int nv = APPEND ? h.Hkv * dv : 0;
   const int nrope = nq + nk;
-  const int total = nrope + nkt + nv;
-  const float2* tb = tab[slot];
-
-  // The page lookup is a chain of three dependent loads that only the stores need: it runs
-  // after the first batch's data loads are in flight instead of in front of them.
-  int64_t kc = -1;
-  bool have_kc = false;
+  const int total = live ? nrope + nkt + nv : 0;
 
   // Batches of UB units per lane: all loads of a batch are issued before any math or store
   // (a store may alias a later load as far as the compiler knows, so without batching each
   // lane would have a single 16-byte load in flight).
   constexpr int UB = 4;
-  for (int u0 = gt; u0 < total; u0 += gsize * UB) {
-    uint4 X[UB], Y[UB];
-    uint16_t* P[UB];  // rope: x chunk (updated in place); copy: source
-    int head[UB], c[UB], kind[UB];  // kind: 0 q rope, 1 k rope, 2 k tail copy, 3 v copy, -1 none
+  uint4 X[UB], Y[UB];
+  uint16_t* P[UB];  // rope: x chunk (updated in place); copy: source
+  int head[UB], c[UB], kind[UB];  // kind: 0 q rope, 1 k rope, 2 k tail copy, 3 v copy, -1 none
+  auto load_batch = [&](int u0) {
 #pragma unroll
     for (int i = 0; i < UB; ++i) {
       const int u = u0 + i * gsize;
@@ -166,12 +147,31 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
         X[i] = ld_nt(P[i]);
       }
     }
-    if constexpr (APPEND) {
-      if (!have_kc) {
-        kc = slot_offset(a.c, t);
-        have_kc = true;
+  };
+
+  // Latency order: the position, the first batch of data and the page lookup chain are all
+  // requested before the cos/sin table is computed, so they overlap it.
+  const float p = (ROPE && live) ? (float)a.pos[t] : 0.f;
+  load_batch(gt);
+  int64_t kc = -1;
+  if constexpr (APPEND) {
+    if (live) kc = slot_offset(a.c, t);
+  }
+  if constexpr (ROPE) {
+    if (live) {
+      for (int i = gt; i < half; i += gsize) {
+        float sn, cs;
+        sincosf(p * a.inv_freq[i], &sn, &cs);
+        tab[slot][i] = make_float2(cs, sn);
       }
     }
+    __syncthreads();
+  }
+  if (!live) return;
+  const float2* tb = tab[slot];
+
+  for (int u0 = gt; u0 < total; u0 += gsize * UB) {
+    if (u0 != gt) load_batch(u0);
 #pragma unroll
     for (int i = 0; i < UB; ++i) {
       if (kind[i] < 0) continue;
@@ -254,8 +254,41 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_d128(QkNormArgs qa) {
   const int64_t t = (int64_t)blockIdx.x * tpb + slot;
   const bool live = t < a.T;
   const HeadsDesc& h = a.h;
+
+  const int sub = gt & 15;            // lane within the head row
+  const int lo = sub & 7;             // pair block: pairs lo*8 .. lo*8+7
+  const bool is_x = sub < 8;          // holds the x half (dims < 64) of its pairs
+  const int sg = gt >> 4, nsg = gsize >> 4;
+  const int nrows = h.Hq + 2 * h.Hkv;  // q heads, k heads, v heads
+
+  // Latency order: position and the first batch of rows are requested before the page
+  // lookup chain and the cos/sin table, which then overlap the loads in flight.
+  constexpr int UB = 4;  // head rows per 16-lane group per batch
+  const float p = live ? (float)a.pos[t] : 0.f;
+  uint4 X[UB], Wt[UB];
+  int kind[UB], hd[UB];
+  auto load_batch = [&](int r0) {
+#pragma unroll
+    for (int i = 0; i < UB; ++i) {
+      const int r = r0 + i * nsg;
+      kind[i] = (!live || r >= nrows) ? 3 : (r < h.Hq ? 0 : (r < h.Hq + h.Hkv ? 1 : 2));
+      hd[i] = kind[i] == 0 ? r : (kind[i] == 1 ? r - h.Hq : r - h.Hq - h.Hkv);
+      X[i] = make_uint4(0, 0, 0, 0);
+      Wt[i] = make_uint4(0, 0, 0, 0);
+      if (kind[i] == 0) {
+        X[i] = ld16(h.q + t * h.q_ts + (int64_t)hd[i] * h.q_hs + sub * 8);
+        Wt[i] = ld16(qa.qw + sub * 8);
+      } else if (kind[i] == 1) {
+        X[i] = ld16(h.k + t * h.k_ts + (int64_t)hd[i] * h.k_hs + sub * 8);
+        Wt[i] = ld16(qa.kw + sub * 8);
+      } else if (kind[i] == 2) {
+        X[i] = ld_nt(h.v + t * h.v_ts + (int64_t)hd[i] * h.v_hs + sub * 8);
+      }
+    }
+  };
+  load_batch(sg);
+  const int64_t kc = live ? slot_offset(a.c, t) : -1;
   if (live) {
-    const float p = (float)a.pos[t];
     for (int i = gt; i < 64; i += gsize) {
       float sn, cs;
       sincosf(p * a.inv_freq[i], &sn, &cs);
@@ -264,53 +297,40 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_d128(QkNormArgs qa) {
   }
   __syncthreads();
   if (!live) return;  // whole token groups (waves) leave together
-
-  const int sub = gt & 15;            // lane within the head row
-  const int lo = sub & 7;             // pair block: pairs lo*8 .. lo*8+7
-  const bool is_x = sub < 8;          // holds the x half (dims < 64) of its pairs
   const float2* tb = tab[slot] + lo * 8;
-  const int nrows = h.Hq + 2 * h.Hkv;  // q heads, k heads, v heads
-  const int64_t kc = slot_offset(a.c, t);
 
   // uniform trip count over the wave: all 64 lanes execute every DPP exchange
-  for (int r0 = (gt >> 4); r0 - (gt >> 4) < nrows; r0 += gsize >> 4) {
-    const int r = r0;
-    const bool on = r < nrows;
-    const int kind = !on ? 3 : (r < h.Hq ? 0 : (r < h.Hq + h.Hkv ? 1 : 2));  // q, k, v, none
-    const int hd = kind == 0 ? r : (kind == 1 ? r - h.Hq : r - h.Hq - h.Hkv);
-    const uint16_t* src = kind == 0 ? h.q + t * h.q_ts + (int64_t)hd * h.q_hs
-                        : kind == 1 ? h.k + t * h.k_ts + (int64_t)hd * h.k_hs
-                                    : h.v + t * h.v_ts + (int64_t)hd * h.v_hs;
-    uint4 xv = make_uint4(0, 0, 0, 0), wv = make_uint4(0, 0, 0, 0);
-    if (on) {
-      xv = kind == 2 ? ld_nt(src + sub * 8) : ld16(src + sub * 8);
-      if (kind < 2) wv = ld16((kind == 0 ? qa.qw : qa.kw) + sub * 8);
-    }
-    float f[8], wf[8];
-    unpack8(xv, f);
-    unpack8(wv, wf);
-    float ss = 0.f;
+  const int nbatch = (nrows + nsg * UB - 1) / (nsg * UB);
+  for (int bi = 0; bi < nbatch; ++bi) {
+    if (bi > 0) load_batch(sg + bi * nsg * UB);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
-    const float rstd = rsqrtf(row16_sum(ss) / 128.0f + qa.eps);
+    for (int i = 0; i < UB; ++i) {
+      float f[8], wf[8];
+      unpack8(X[i], f);
+      unpack8(Wt[i], wf);
+      float ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = (f[e] * rstd) * wf[e];
-    const uint4 g = pack8(f);  // normalised row, rounded to bf16 as the separate norm stores it
-    const uint4 pg = make_uint4(dpp_ror8(g.x), dpp_ror8(g.y), dpp_ror8(g.z), dpp_ror8(g.w));
-    float own[8], oth[8];
-    unpack8(g, own);
-    unpack8(pg, oth);
+      for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+      const float rstd = rsqrtf(row16_sum(ss) / 128.0f + qa.eps);
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      own[e] = is_x ? rot_x(own[e], oth[e], tb[e]) : rot_y(oth[e], own[e], tb[e]);
-    const uint4 o = pack8(own);
-    if (kind == 0) {
-      st16(qa.q_out + t * qa.qo_ts + (int64_t)hd * qa.qo_hs + sub * 8, o);
-    } else if (kind == 1) {
-      st16(qa.k_out + t * qa.ko_ts + (int64_t)hd * qa.ko_hs + sub * 8, o);
-      if (kc >= 0) st_nt(a.c.k_cache + kc + (int64_t)hd * a.c.head_stride + sub * 8, o);
-    } else if (kind == 2 && kc >= 0) {
-      st_nt(a.c.v_cache + kc + (int64_t)hd * a.c.head_stride + sub * 8, xv);
+      for (int e = 0; e < 8; ++e) f[e] = (f[e] * rstd) * wf[e];
+      const uint4 g = pack8(f);  // normalised row, rounded to bf16 as the separate norm stores it
+      const uint4 pg = make_uint4(dpp_ror8(g.x), dpp_ror8(g.y), dpp_ror8(g.z), dpp_ror8(g.w));
+      float own[8], oth[8];
+      unpack8(g, own);
+      unpack8(pg, oth);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        own[e] = is_x ? rot_x(own[e], oth[e], tb[e]) : rot_y(oth[e], own[e], tb[e]);
+      const uint4 o = pack8(own);
+      if (kind[i] == 0) {
+        st16(qa.q_out + t * qa.qo_ts + (int64_t)hd[i] * qa.qo_hs + sub * 8, o);
+      } else if (kind[i] == 1) {
+        st16(qa.k_out + t * qa.ko_ts + (int64_t)hd[i] * qa.ko_hs + sub * 8, o);
+        if (kc >= 0) st_nt(a.c.k_cache + kc + (int64_t)hd[i] * a.c.head_stride + sub * 8, o);
+      } else if (kind[i] == 2 && kc >= 0) {
+        st_nt(a.c.v_cache + kc + (int64_t)hd[i] * a.c.head_stride + sub * 8, X[i]);
+      }
     }
   }
 }
