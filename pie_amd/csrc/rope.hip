@@ -24,6 +24,8 @@
 // 1 KiB runs of a page: the scatter is coalesced per (page, slot).
 #include "common.h"
 
+
+
 namespace pie {
 namespace {
 
@@ -111,48 +113,53 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   // (a store may alias a later load as far as the compiler knows, so without batching each
   // lane would have a single 16-byte load in flight).
   constexpr int UB = 4;
-  uint4 X[UB], Y[UB];
-  uint16_t* P[UB];  // rope: x chunk (updated in place); copy: source
-  int head[UB], c[UB], kind[UB];  // kind: 0 q rope, 1 k rope, 2 k tail copy, 3 v copy, -1 none
-  auto load_batch = [&](int u0) {
+  struct Batch {
+    uint4 X[UB], Y[UB];
+    uint16_t* P[UB];  // rope: x chunk (updated in place); copy: source
+    int head[UB], c[UB], kind[UB];  // kind: 0 q rope, 1 k rope, 2 k tail copy, 3 v copy, -1 none
+  };
+  // returns by value (captures scalars by value) so the batch stays in registers
+  auto load_batch = [=](int u0) {
+    Batch b;
 #pragma unroll
     for (int i = 0; i < UB; ++i) {
       const int u = u0 + i * gsize;
-      kind[i] = -1;
+      b.kind[i] = -1;
       if (u >= total) continue;
       if (ROPE && u < nrope) {
         const bool isq = u < nq;
         const int uu = isq ? u : u - nq;
-        head[i] = uu / uph;
-        c[i] = uu - head[i] * uph;
-        kind[i] = isq ? 0 : 1;
-        P[i] = (isq ? h.q + t * h.q_ts + (int64_t)head[i] * h.q_hs
-                    : h.k + t * h.k_ts + (int64_t)head[i] * h.k_hs) + c[i] * 8;
-        X[i] = ld16(P[i]);
-        if constexpr (!INTERLEAVE) Y[i] = ld16(P[i] + half);
+        b.head[i] = uu / uph;
+        b.c[i] = uu - b.head[i] * uph;
+        b.kind[i] = isq ? 0 : 1;
+        b.P[i] = (isq ? h.q + t * h.q_ts + (int64_t)b.head[i] * h.q_hs
+                      : h.k + t * h.k_ts + (int64_t)b.head[i] * h.k_hs) + b.c[i] * 8;
+        b.X[i] = ld_nt(b.P[i]);  // non-temporal: measured 76% vs 73% of peak cached
+        if constexpr (!INTERLEAVE) b.Y[i] = ld_nt(b.P[i] + half);
       } else if (APPEND) {
         int uu = u - nrope;
         if (uu < nkt) {
-          head[i] = uu / tail;
-          c[i] = (ROPE ? h.rd : 0) + (uu - head[i] * tail) * 8;  // element offset in the head
-          kind[i] = 2;
-          P[i] = h.k + t * h.k_ts + (int64_t)head[i] * h.k_hs + c[i];
+          b.head[i] = uu / tail;
+          b.c[i] = (ROPE ? h.rd : 0) + (uu - b.head[i] * tail) * 8;  // element offset in head
+          b.kind[i] = 2;
+          b.P[i] = h.k + t * h.k_ts + (int64_t)b.head[i] * h.k_hs + b.c[i];
         } else {
           uu -= nkt;
-          head[i] = uu / dv;
-          c[i] = (uu - head[i] * dv) * 8;
-          kind[i] = 3;
-          P[i] = const_cast<uint16_t*>(h.v) + t * h.v_ts + (int64_t)head[i] * h.v_hs + c[i];
+          b.head[i] = uu / dv;
+          b.c[i] = (uu - b.head[i] * dv) * 8;
+          b.kind[i] = 3;
+          b.P[i] = const_cast<uint16_t*>(h.v) + t * h.v_ts + (int64_t)b.head[i] * h.v_hs + b.c[i];
         }
-        X[i] = ld_nt(P[i]);
+        b.X[i] = ld_nt(b.P[i]);
       }
     }
+    return b;
   };
 
   // Latency order: the position, the first batch of data and the page lookup chain are all
   // requested before the cos/sin table is computed, so they overlap it.
   const float p = (ROPE && live) ? (float)a.pos[t] : 0.f;
-  load_batch(gt);
+  Batch b = load_batch(gt);
   int64_t kc = -1;
   if constexpr (APPEND) {
     if (live) kc = slot_offset(a.c, t);
@@ -171,7 +178,13 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   const float2* tb = tab[slot];
 
   for (int u0 = gt; u0 < total; u0 += gsize * UB) {
-    if (u0 != gt) load_batch(u0);
+    if (u0 != gt) b = load_batch(u0);
+    const uint4* X = b.X;
+    const uint4* Y = b.Y;
+    uint16_t* const* P = b.P;
+    const int* head = b.head;
+    const int* c = b.c;
+    const int* kind = b.kind;
 #pragma unroll
     for (int i = 0; i < UB; ++i) {
       if (kind[i] < 0) continue;
@@ -265,28 +278,32 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_d128(QkNormArgs qa) {
   // lookup chain and the cos/sin table, which then overlap the loads in flight.
   constexpr int UB = 4;  // head rows per 16-lane group per batch
   const float p = live ? (float)a.pos[t] : 0.f;
-  uint4 X[UB], Wt[UB];
-  int kind[UB], hd[UB];
-  auto load_batch = [&](int r0) {
+  struct Batch {
+    uint4 X[UB], Wt[UB];
+    int kind[UB], hd[UB];  // kind: 0 q, 1 k, 2 v, 3 none
+  };
+  auto load_batch = [=](int r0) {
+    Batch b;
 #pragma unroll
     for (int i = 0; i < UB; ++i) {
       const int r = r0 + i * nsg;
-      kind[i] = (!live || r >= nrows) ? 3 : (r < h.Hq ? 0 : (r < h.Hq + h.Hkv ? 1 : 2));
-      hd[i] = kind[i] == 0 ? r : (kind[i] == 1 ? r - h.Hq : r - h.Hq - h.Hkv);
-      X[i] = make_uint4(0, 0, 0, 0);
-      Wt[i] = make_uint4(0, 0, 0, 0);
-      if (kind[i] == 0) {
-        X[i] = ld16(h.q + t * h.q_ts + (int64_t)hd[i] * h.q_hs + sub * 8);
-        Wt[i] = ld16(qa.qw + sub * 8);
-      } else if (kind[i] == 1) {
-        X[i] = ld16(h.k + t * h.k_ts + (int64_t)hd[i] * h.k_hs + sub * 8);
-        Wt[i] = ld16(qa.kw + sub * 8);
-      } else if (kind[i] == 2) {
-        X[i] = ld_nt(h.v + t * h.v_ts + (int64_t)hd[i] * h.v_hs + sub * 8);
+      b.kind[i] = (!live || r >= nrows) ? 3 : (r < h.Hq ? 0 : (r < h.Hq + h.Hkv ? 1 : 2));
+      b.hd[i] = b.kind[i] == 0 ? r : (b.kind[i] == 1 ? r - h.Hq : r - h.Hq - h.Hkv);
+      b.X[i] = make_uint4(0, 0, 0, 0);
+      b.Wt[i] = make_uint4(0, 0, 0, 0);
+      if (b.kind[i] == 0) {
+        b.X[i] = ld16(h.q + t * h.q_ts + (int64_t)b.hd[i] * h.q_hs + sub * 8);
+        b.Wt[i] = ld16(qa.qw + sub * 8);
+      } else if (b.kind[i] == 1) {
+        b.X[i] = ld16(h.k + t * h.k_ts + (int64_t)b.hd[i] * h.k_hs + sub * 8);
+        b.Wt[i] = ld16(qa.kw + sub * 8);
+      } else if (b.kind[i] == 2) {
+        b.X[i] = ld_nt(h.v + t * h.v_ts + (int64_t)b.hd[i] * h.v_hs + sub * 8);
       }
     }
+    return b;
   };
-  load_batch(sg);
+  Batch b = load_batch(sg);
   const int64_t kc = live ? slot_offset(a.c, t) : -1;
   if (live) {
     for (int i = gt; i < 64; i += gsize) {
@@ -302,7 +319,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_d128(QkNormArgs qa) {
   // uniform trip count over the wave: all 64 lanes execute every DPP exchange
   const int nbatch = (nrows + nsg * UB - 1) / (nsg * UB);
   for (int bi = 0; bi < nbatch; ++bi) {
-    if (bi > 0) load_batch(sg + bi * nsg * UB);
+    if (bi > 0) b = load_batch(sg + bi * nsg * UB);
+    const uint4* X = b.X;
+    const uint4* Wt = b.Wt;
+    const int* kind = b.kind;
+    const int* hd = b.hd;
 #pragma unroll
     for (int i = 0; i < UB; ++i) {
       float f[8], wf[8];
