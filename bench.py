@@ -7,8 +7,9 @@ One step = one pass of the fused residual-add + RMSNorm [8192, 4096] followed by
 line: value = algorithmic HBM GB/s of the step; roofline = the dominant kernel (SiLU-and-mul)
 timed with HIP events on the stream it runs on; cpu_baseline = torch-CPU running the
 reference's own expressions (`residual + x`, F.rms_norm, F.silu(gate) * up) on a bounded
-sample of the same workload; "ops" = every configuration's per-op µs / GB/s (hot and with the
-256 MB last-level cache flushed) and the decode-chain µs (HIP-graph replay).
+sample of the same workload; "ops" = every configuration's per-op µs / GB/s (steady state over
+buffer sets larger than the 256 MB last-level cache, and one launch after a flush) and the
+decode-chain µs (HIP-graph replay).
 """
 from __future__ import annotations
 
@@ -40,17 +41,6 @@ def _events(fn, iters, flush=None):
         out.append((a, b))
     torch.cuda.synchronize()
     return [a.elapsed_time(b) for a, b in out]
-
-
-def _op_entry(name, nbytes, hot_ms, cold_ms=None):
-    hot = statistics.median(hot_ms)
-    e = {"op": name, "bytes": nbytes, "us_hot": round(hot * 1e3, 2),
-         "gbs_hot": round(nbytes / hot / 1e6, 1), "frac_hot": round(nbytes / hot / 1e6 / HBM_PEAK_GBS, 3)}
-    if cold_ms:
-        cold = statistics.median(cold_ms)
-        e.update({"us_cold": round(cold * 1e3, 2), "gbs_cold": round(nbytes / cold / 1e6, 1),
-                  "frac_cold": round(nbytes / cold / 1e6 / HBM_PEAK_GBS, 3)})
-    return e
 
 
 def cpu_baseline(budget_s: float = 12.0) -> dict:
@@ -85,72 +75,119 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
                       f"[256,2x14336]) in torch-CPU bf16, {dt:.1f} s"}
 
 
-def measure_ops(dev, iters=50, cold_iters=20):
-    """Every configuration: per-op hot/cold µs and GB/s; decode-chain µs per graph replay."""
+def _rotating(calls, iters=60, reps=3):
+    """µs per launch over back-to-back launches that rotate through independent buffer sets
+    (together larger than the 256 MB last-level cache), so each launch pays for its own HBM
+    reads and for draining its writes; median over reps."""
+    import torch
+    for c in calls:
+        c()
+    out = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(iters):
+            calls[i % len(calls)]()
+        b.record()
+        torch.cuda.synchronize()
+        out.append(a.elapsed_time(b) * 1e3 / iters)
+    return statistics.median(out)
+
+
+def _copies(footprint_bytes):
+    return max(2, -(-(768 << 20) // footprint_bytes))
+
+
+def _entry(name, nbytes, steady_us, cold_ms):
+    cold = statistics.median(cold_ms) * 1e3
+    return {"op": name, "bytes": nbytes,
+            "us": round(steady_us, 2), "gbs": round(nbytes / steady_us / 1e3, 1),
+            "frac": round(nbytes / steady_us / 1e3 / HBM_PEAK_GBS, 3),
+            "us_cold_single": round(cold, 2), "gbs_cold_single": round(nbytes / cold / 1e3, 1)}
+
+
+def measure_ops(dev, cold_iters=20):
+    """Every configuration's ops. "us"/"gbs"/"frac": back-to-back launches over rotating buffer
+    sets (steady state, writes drained); "*_cold_single": one launch after a cache flush.
+    Decode chain: µs per HIP-graph replay."""
     import torch
     from pie_amd import ops
     from pie_amd import workloads as wl
-    from pie_amd.chain import DecodeChain
 
     scratch = torch.ones(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
     sink = torch.empty((), dtype=torch.float32, device=dev)
 
     def flush():
-        # Reading 1 GiB evicts the 256 MB last-level cache and L2 with clean lines; a write
-        # would leave dirty lines draining to HBM during the timed kernel.
+        # Reading 1 GiB evicts the 256 MB last-level cache and L2 with clean lines.
         torch.sum(scratch, dim=0, out=sink)
+
+    def run(name, nbytes, make):
+        calls = [make() for _ in range(_copies(nbytes))]
+        e = _entry(name, nbytes, _rotating(calls), _events(calls[0], cold_iters, flush))
+        del calls
+        torch.cuda.empty_cache()
+        return e
 
     res = []
     c = wl.cfg1()
-    x, w = c["x"].to(dev), c["w"].to(dev)
-    y = torch.empty_like(x)
-    f = lambda: ops.rmsnorm(x, w, c["eps"], out=y)
-    res.append(_op_entry("cfg1 rmsnorm [2048,2048]", 2 * x.numel() * 2 + w.numel() * 2,
-                         _events(f, iters), _events(f, cold_iters, flush)))
-    del x, y
+    x0, w = c["x"].to(dev), c["w"].to(dev)
+
+    def make_cfg1():
+        x, y = x0.clone(), torch.empty_like(x0)
+        return lambda: ops.rmsnorm(x, w, c["eps"], out=y)
+    res.append(run("cfg1 rmsnorm [2048,2048]", 2 * x0.numel() * 2 + w.numel() * 2, make_cfg1))
 
     c = wl.cfg2()
-    x, r, w, gu = (c[k].to(dev) for k in ("x", "r", "w", "gate_up"))
-    y, s = torch.empty_like(x), torch.empty_like(x)
-    act = torch.empty((gu.shape[0], gu.shape[1] // 2), dtype=gu.dtype, device=dev)
+    x0, r0, w, gu0 = (c[k].to(dev) for k in ("x", "r", "w", "gate_up"))
     b_add, b_silu = wl.cfg2_bytes()
-    f = lambda: ops.add_rms_norm(x, r, w, c["eps"], out=y, residual_out=s)
-    res.append(_op_entry("cfg2a add+rmsnorm [8192,4096]", b_add, _events(f, iters),
-                         _events(f, cold_iters, flush)))
-    f = lambda: ops.silu_and_mul(gu, out=act)
-    res.append(_op_entry("cfg2b silu_and_mul [8192,2x14336]", b_silu, _events(f, iters),
-                         _events(f, cold_iters, flush)))
-    del x, r, gu, y, s, act
+
+    def make_add():
+        x, r = x0.clone(), r0.clone()
+        y, s = torch.empty_like(x), torch.empty_like(x)
+        return lambda: ops.add_rms_norm(x, r, w, c["eps"], out=y, residual_out=s)
+
+    def make_silu():
+        gu = gu0.clone()
+        act = torch.empty((gu.shape[0], gu.shape[1] // 2), dtype=gu.dtype, device=dev)
+        return lambda: ops.silu_and_mul(gu, out=act)
+    res.append(run("cfg2a add+rmsnorm [8192,4096]", b_add, make_add))
+    res.append(run("cfg2b silu_and_mul [8192,2x14336]", b_silu, make_silu))
+    del x0, r0, gu0
 
     c = wl.cfg3()
     pb, T = c["batch"], c["qkv"].shape[0]
-    qkv = c["qkv"].to(dev)
-    q, k, v = wl.split_qkv(qkv, 32, 8, 128)
-    cache = wl.sentinel_cache(c["cache_shape"]).to(dev)
+    qkv0 = c["qkv"].to(dev)
     d = {n: getattr(pb, n).to(dev) for n in ("batch_indices", "positions", "kv_indices",
                                              "kv_indptr", "kv_last_page_len")}
     nb = wl.cfg3_bytes(T)
-    f = lambda: ops.apply_llama31_rope_pos_ids_inplace(q, k, d["positions"], **c["rope"])
-    res.append(_op_entry(f"cfg3 llama31 rope T={T}", nb["rope"], _events(f, iters),
-                         _events(f, cold_iters, flush)))
-    f = lambda: ops.append_paged_kv_cache(k, v, d["batch_indices"], d["positions"], cache,
-                                          d["kv_indices"], d["kv_indptr"], d["kv_last_page_len"])
-    res.append(_op_entry(f"cfg3 paged append T={T}", nb["append"], _events(f, iters),
-                         _events(f, cold_iters, flush)))
-    f = lambda: ops.apply_llama31_rope_pos_ids_and_append_paged_kv_cache(
-        q, k, v, d["positions"], d["batch_indices"], d["positions"], cache, d["kv_indices"],
-        d["kv_indptr"], d["kv_last_page_len"], **c["rope"])
-    res.append(_op_entry(f"cfg3 fused rope+append T={T}", nb["fused"], _events(f, iters),
-                         _events(f, cold_iters, flush)))
-    del qkv, q, k, v, cache
+
+    def make_rope(kind):
+        qkv = qkv0.clone()
+        q, k, v = wl.split_qkv(qkv, 32, 8, 128)
+        cache = wl.sentinel_cache(c["cache_shape"]).to(dev) if kind != "rope" else None
+        if kind == "rope":
+            return lambda: ops.apply_llama31_rope_pos_ids_inplace(q, k, d["positions"], **c["rope"])
+        if kind == "append":
+            return lambda: ops.append_paged_kv_cache(k, v, d["batch_indices"], d["positions"], cache,
+                                                     d["kv_indices"], d["kv_indptr"],
+                                                     d["kv_last_page_len"])
+        return lambda: ops.apply_llama31_rope_pos_ids_and_append_paged_kv_cache(
+            q, k, v, d["positions"], d["batch_indices"], d["positions"], cache, d["kv_indices"],
+            d["kv_indptr"], d["kv_last_page_len"], **c["rope"])
+    res.append(run(f"cfg3 llama31 rope T={T}", nb["rope"], lambda: make_rope("rope")))
+    res.append(run(f"cfg3 paged append T={T}", nb["append"], lambda: make_rope("append")))
+    res.append(run(f"cfg3 fused rope+append T={T}", nb["fused"], lambda: make_rope("fused")))
+    del qkv0
 
     c = wl.cfg4()
-    W, ids = c["W"].to(dev), c["ids"].to(dev)
-    out = torch.empty((ids.numel(), W.shape[1]), dtype=W.dtype, device=dev)
-    f = lambda: ops.embedding(ids, W, out=out)
-    res.append(_op_entry("cfg4 embedding [128256,4096] x16384", wl.cfg4_bytes(), _events(f, iters),
-                         _events(f, cold_iters, flush)))
-    del W, out
+    W0, ids = c["W"].to(dev), c["ids"].to(dev)
+
+    def make_embed():
+        W = W0.clone()
+        out = torch.empty((ids.numel(), W.shape[1]), dtype=W.dtype, device=dev)
+        return lambda: ops.embedding(ids, W, out=out)
+    res.append(run("cfg4 embedding [128256,4096] x16384", wl.cfg4_bytes(), make_embed))
+    del W0
 
     res.extend(measure_chain(dev, flush, cold_iters))
     del scratch
@@ -256,14 +293,20 @@ def main():
 
     for _ in range(args.warmup):
         step()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
+    # Timed region: exactly K steps, synchronised on both sides, nothing else in the stream.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    # Second pass over K steps with HIP events around every SiLU-and-mul launch (on the stream
+    # the kernels run on): the dominant kernel's average launch duration for the roofline.
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
     for i in range(args.steps):
         step(evs[i])
     torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
     silu_ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
     ms_per_step = dt * 1e3 / args.steps
     step_bytes = b_add + b_silu

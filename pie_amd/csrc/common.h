@@ -56,8 +56,10 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 
 // 128-bit accesses. ld_nt/st_nt take the non-temporal path (streamed data that must not
 // evict reused lines); ld16/st16 the ordinary cached path. Each kernel picks per access what
-// measured fastest on MI355X (e.g. SiLU-and-mul: non-temporal loads + cached stores, 82% of
-// peak, against 74% with non-temporal stores).
+// measured fastest on MI355X in steady state (back-to-back launches over buffers larger than
+// the last-level cache, so a kernel pays for draining its own writes): non-temporal stores for
+// every large streamed output (e.g. SiLU-and-mul 6.47 vs 6.13 TB/s, embedding 6.27 vs
+// 5.23 TB/s), cached loads and stores for the RMSNorm rows.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_nt(const void* p) {
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));

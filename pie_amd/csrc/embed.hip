@@ -9,6 +9,8 @@
 #include "common.h"
 
 
+
+
 namespace pie {
 namespace {
 
@@ -43,7 +45,7 @@ __global__ __launch_bounds__(256) void embed_vec(EmbedArgs a) {
   }
 #pragma unroll
   for (int i = 0; i < U; ++i)
-    if (dst[i] >= 0) st16(a.out + dst[i], v[i]);
+    if (dst[i] >= 0) st_nt(a.out + dst[i], v[i]);
 }
 
 __global__ __launch_bounds__(256) void embed_scalar(EmbedArgs a) {
@@ -78,8 +80,8 @@ extern "C" int pie_hip_embedding(const int32_t* ids, int64_t T, const pie_bf16* 
   if (vec) {
     a.nvec = (uint32_t)nvec;
     a.vpr = FastDiv::make((uint32_t)(H / 8));
-    // One 16-byte vector per thread (configuration 4: 75% of peak, against 74% with 2 and
-    // 70% with 4 vectors per thread).
+    // One 16-byte vector per thread (configuration 4 steady state: 6.29 TB/s, against 6.27
+    // with 2 and 5.98 with 4 vectors per thread).
     hipLaunchKernelGGL(embed_vec<1>, dim3((unsigned)((nvec + 255) / 256)), blk, 0, st, a);
   } else {
     const int64_t blocks = (T + 3) / 4, cap = (int64_t)num_cus() * 64;

@@ -16,6 +16,7 @@
 
 #include "common.h"
 
+
 namespace pie {
 namespace {
 

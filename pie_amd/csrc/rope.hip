@@ -26,6 +26,9 @@
 
 
 
+
+
+
 namespace pie {
 namespace {
 
@@ -60,13 +63,6 @@ struct RopeAppendArgs {
   float inv_freq[kMaxPairs];
 };
 
-// Cache-page stores: non-temporal in the fused RoPE+append kernel, cached in the plain append
-// (measured fastest for each).
-template <bool FUSED>
-__device__ __forceinline__ void st_cache(void* p, const uint4& v) {
-  if constexpr (FUSED) st_nt(p, v);
-  else st16(p, v);
-}
 
 // The rotation with its fused multiply-adds spelled out, so every kernel variant (rope only,
 // fused with the append, scalar fallback) rounds identically: x' = x c - y s, y' = x s + y c.
@@ -86,7 +82,7 @@ __device__ __forceinline__ int64_t slot_offset(const CacheDesc& c, int64_t t) {
   return (int64_t)page * c.page_stride + (int64_t)(p % c.page_size) * c.slot_stride;
 }
 
-template <bool ROPE, bool APPEND, bool INTERLEAVE>
+template <bool ROPE, bool APPEND, bool INTERLEAVE, int UB>
 __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   __shared__ float2 tab[4][ROPE ? kMaxPairs : 1];
   const int wpt = a.wpt;
@@ -111,8 +107,8 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
 
   // Batches of UB units per lane: all loads of a batch are issued before any math or store
   // (a store may alias a later load as far as the compiler knows, so without batching each
-  // lane would have a single 16-byte load in flight).
-  constexpr int UB = 4;
+  // lane would have a single 16-byte load in flight). The host sizes UB so that a token's
+  // units fit one batch (up to 8 per lane).
   struct Batch {
     uint4 X[UB], Y[UB];
     uint16_t* P[UB];  // rope: x chunk (updated in place); copy: source
@@ -134,7 +130,7 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
         b.kind[i] = isq ? 0 : 1;
         b.P[i] = (isq ? h.q + t * h.q_ts + (int64_t)b.head[i] * h.q_hs
                       : h.k + t * h.k_ts + (int64_t)b.head[i] * h.k_hs) + b.c[i] * 8;
-        b.X[i] = ld_nt(b.P[i]);  // non-temporal: measured 76% vs 73% of peak cached
+        b.X[i] = ld_nt(b.P[i]);  // non-temporal: 5.33 vs 4.90 TB/s cached (steady state)
         if constexpr (!INTERLEAVE) b.Y[i] = ld_nt(b.P[i] + half);
       } else if (APPEND) {
         int uu = u - nrope;
@@ -202,12 +198,12 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
             y[e] = yr;
           }
           const uint4 xo = pack8(x), yo = pack8(y);
-          st16(P[i], xo);
-          st16(P[i] + half, yo);
+          st_nt(P[i], xo);
+          st_nt(P[i] + half, yo);
           if (APPEND && kind[i] == 1 && kc >= 0) {
             uint16_t* dst = a.c.k_cache + kc + (int64_t)head[i] * a.c.head_stride + c[i] * 8;
-            st_cache<ROPE>(dst, xo);
-            st_cache<ROPE>(dst + half, yo);
+            st_nt(dst, xo);
+            st_nt(dst + half, yo);
           }
         } else {
           float f[8];
@@ -221,13 +217,13 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
             f[2 * m + 1] = yr;
           }
           const uint4 o = pack8(f);
-          st16(P[i], o);
+          st_nt(P[i], o);
           if (APPEND && kind[i] == 1 && kc >= 0)
-            st_cache<ROPE>(a.c.k_cache + kc + (int64_t)head[i] * a.c.head_stride + c[i] * 8, o);
+            st_nt(a.c.k_cache + kc + (int64_t)head[i] * a.c.head_stride + c[i] * 8, o);
         }
       } else if (APPEND && kc >= 0) {
         uint16_t* cache = kind[i] == 2 ? a.c.k_cache : a.c.v_cache;
-        st_cache<ROPE>(cache + kc + (int64_t)head[i] * a.c.head_stride + c[i], X[i]);
+        st_nt(cache + kc + (int64_t)head[i] * a.c.head_stride + c[i], X[i]);
       }
     }
   }
@@ -403,7 +399,13 @@ bool heads_vec_ok(const uint16_t* p, int64_t ts, int64_t hs) {
   return aligned16(p) && ts % 8 == 0 && hs % 8 == 0;
 }
 
-int pick_wpt(int64_t T) { return T >= 8192 ? 1 : (T >= 2048 ? 2 : 4); }
+// Waves per token, measured on configuration 3 (T = 68k, steady state): RoPE alone 6.18 TB/s
+// with 4 (5.96 with 2, 5.46 with 1); append alone 5.33 with 2 (4.70 with 4, 5.15 with 1);
+// fused 5.68 with 2 or 4 (5.46 with 1). Small batches (decode) use 4 to spread over the chip.
+int pick_wpt(int64_t T, bool rope, bool append) {
+  if (T < 2048 || (rope && !append)) return 4;
+  return 2;
+}
 
 int launch(RopeAppendArgs& a, bool rope, bool append, int interleave, hipStream_t st,
            const char* name) {
@@ -417,14 +419,31 @@ int launch(RopeAppendArgs& a, bool rope, bool append, int interleave, hipStream_
           aligned16(a.c.k_cache) && aligned16(a.c.v_cache) && a.c.page_stride % 8 == 0 &&
           a.c.slot_stride % 8 == 0 && a.c.head_stride % 8 == 0;
   if (vec) {
-    a.wpt = pick_wpt(a.T);
+    a.wpt = pick_wpt(a.T, rope, append);
     const int tpb = 4 / a.wpt;
     const dim3 grd((unsigned)((a.T + tpb - 1) / tpb)), blk(256);
-#define PIE_RA(R, A, I) hipLaunchKernelGGL((rope_append_vec<R, A, I>), grd, blk, 0, st, a)
-    if (rope && append) { if (interleave) PIE_RA(true, true, true); else PIE_RA(true, true, false); }
-    else if (rope) { if (interleave) PIE_RA(true, false, true); else PIE_RA(true, false, false); }
-    else PIE_RA(false, true, false);
-#undef PIE_RA
+    // Units per lane for one token: one batch holds them all (capped at 8 per batch).
+    const int uph = rope ? (interleave ? h.rd >> 3 : h.rd >> 4) : 0;
+    const int64_t units = (int64_t)(h.Hq + h.Hkv) * uph +
+                          (append ? (int64_t)h.Hkv * ((h.D - (rope ? h.rd : 0)) / 8 + h.D / 8) : 0);
+    int64_t ub = (units + 64 * a.wpt - 1) / (64 * a.wpt);
+    if (ub < 1) ub = 1;
+    if (ub > 8) ub = 8;
+#define PIE_RA_UB(R, A, I)                                                              \
+  switch (ub) {                                                                           \
+    case 1: hipLaunchKernelGGL((rope_append_vec<R, A, I, 1>), grd, blk, 0, st, a); break; \
+    case 2: hipLaunchKernelGGL((rope_append_vec<R, A, I, 2>), grd, blk, 0, st, a); break; \
+    case 3: hipLaunchKernelGGL((rope_append_vec<R, A, I, 3>), grd, blk, 0, st, a); break; \
+    case 4: hipLaunchKernelGGL((rope_append_vec<R, A, I, 4>), grd, blk, 0, st, a); break; \
+    case 5: hipLaunchKernelGGL((rope_append_vec<R, A, I, 5>), grd, blk, 0, st, a); break; \
+    case 6: hipLaunchKernelGGL((rope_append_vec<R, A, I, 6>), grd, blk, 0, st, a); break; \
+    case 7: hipLaunchKernelGGL((rope_append_vec<R, A, I, 7>), grd, blk, 0, st, a); break; \
+    default: hipLaunchKernelGGL((rope_append_vec<R, A, I, 8>), grd, blk, 0, st, a); break; \
+  }
+    if (rope && append) { if (interleave) PIE_RA_UB(true, true, true) else PIE_RA_UB(true, true, false) }
+    else if (rope) { if (interleave) PIE_RA_UB(true, false, true) else PIE_RA_UB(true, false, false) }
+    else PIE_RA_UB(false, true, false)
+#undef PIE_RA_UB
     return check_launch(name);
   }
   const dim3 blk(256);
@@ -589,7 +608,7 @@ extern "C" int pie_hip_qk_rmsnorm_rope_append(
   qa.qw = qw;
   qa.kw = kw;
   qa.eps = eps;
-  a.wpt = pick_wpt(T);
+  a.wpt = pick_wpt(T, true, true);
   const int tpb = 4 / a.wpt;
   hipLaunchKernelGGL(qk_norm_rope_append_d128, dim3((unsigned)((T + tpb - 1) / tpb)), dim3(256), 0,
                      (hipStream_t)stream, qa);
