@@ -106,13 +106,11 @@ def _entry(name, nbytes, steady_us, cold_ms):
             "us_cold_single": round(cold, 2), "gbs_cold_single": round(nbytes / cold / 1e3, 1)}
 
 
-def measure_ops(dev, cold_iters=20):
+def measure_ops(dev, cold_iters=20, only=None):
     """Every configuration's ops. "us"/"gbs"/"frac": back-to-back launches over rotating buffer
     sets (steady state, writes drained); "*_cold_single": one launch after a cache flush.
     Decode chain: µs per HIP-graph replay."""
     import torch
-    from pie_amd import ops
-    from pie_amd import workloads as wl
 
     scratch = torch.ones(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
     sink = torch.empty((), dtype=torch.float32, device=dev)
@@ -129,14 +127,38 @@ def measure_ops(dev, cold_iters=20):
         return e
 
     res = []
+    want = lambda tag: only is None or only == tag
+    if want("cfg1"):
+        res.extend(_ops_cfg1(dev, run))
+    if want("cfg2"):
+        res.extend(_ops_cfg2(dev, run))
+    if want("cfg3"):
+        res.extend(_ops_cfg3(dev, run))
+    if want("cfg4"):
+        res.extend(_ops_cfg4(dev, run))
+    if want("cfg5"):
+        res.extend(measure_chain(dev, flush, cold_iters))
+    del scratch
+    return res
+
+
+def _ops_cfg1(dev, run):
+    import torch
+    from pie_amd import ops
+    from pie_amd import workloads as wl
     c = wl.cfg1()
     x0, w = c["x"].to(dev), c["w"].to(dev)
 
     def make_cfg1():
         x, y = x0.clone(), torch.empty_like(x0)
         return lambda: ops.rmsnorm(x, w, c["eps"], out=y)
-    res.append(run("cfg1 rmsnorm [2048,2048]", 2 * x0.numel() * 2 + w.numel() * 2, make_cfg1))
+    return [run("cfg1 rmsnorm [2048,2048]", 2 * x0.numel() * 2 + w.numel() * 2, make_cfg1)]
 
+
+def _ops_cfg2(dev, run):
+    import torch
+    from pie_amd import ops
+    from pie_amd import workloads as wl
     c = wl.cfg2()
     x0, r0, w, gu0 = (c[k].to(dev) for k in ("x", "r", "w", "gate_up"))
     b_add, b_silu = wl.cfg2_bytes()
@@ -150,10 +172,13 @@ def measure_ops(dev, cold_iters=20):
         gu = gu0.clone()
         act = torch.empty((gu.shape[0], gu.shape[1] // 2), dtype=gu.dtype, device=dev)
         return lambda: ops.silu_and_mul(gu, out=act)
-    res.append(run("cfg2a add+rmsnorm [8192,4096]", b_add, make_add))
-    res.append(run("cfg2b silu_and_mul [8192,2x14336]", b_silu, make_silu))
-    del x0, r0, gu0
+    return [run("cfg2a add+rmsnorm [8192,4096]", b_add, make_add),
+            run("cfg2b silu_and_mul [8192,2x14336]", b_silu, make_silu)]
 
+
+def _ops_cfg3(dev, run):
+    from pie_amd import ops
+    from pie_amd import workloads as wl
     c = wl.cfg3()
     pb, T = c["batch"], c["qkv"].shape[0]
     qkv0 = c["qkv"].to(dev)
@@ -174,11 +199,15 @@ def measure_ops(dev, cold_iters=20):
         return lambda: ops.apply_llama31_rope_pos_ids_and_append_paged_kv_cache(
             q, k, v, d["positions"], d["batch_indices"], d["positions"], cache, d["kv_indices"],
             d["kv_indptr"], d["kv_last_page_len"], **c["rope"])
-    res.append(run(f"cfg3 llama31 rope T={T}", nb["rope"], lambda: make_rope("rope")))
-    res.append(run(f"cfg3 paged append T={T}", nb["append"], lambda: make_rope("append")))
-    res.append(run(f"cfg3 fused rope+append T={T}", nb["fused"], lambda: make_rope("fused")))
-    del qkv0
+    return [run(f"cfg3 llama31 rope T={T}", nb["rope"], lambda: make_rope("rope")),
+            run(f"cfg3 paged append T={T}", nb["append"], lambda: make_rope("append")),
+            run(f"cfg3 fused rope+append T={T}", nb["fused"], lambda: make_rope("fused"))]
 
+
+def _ops_cfg4(dev, run):
+    import torch
+    from pie_amd import ops
+    from pie_amd import workloads as wl
     c = wl.cfg4()
     W0, ids = c["W"].to(dev), c["ids"].to(dev)
 
@@ -186,12 +215,7 @@ def measure_ops(dev, cold_iters=20):
         W = W0.clone()
         out = torch.empty((ids.numel(), W.shape[1]), dtype=W.dtype, device=dev)
         return lambda: ops.embedding(ids, W, out=out)
-    res.append(run("cfg4 embedding [128256,4096] x16384", wl.cfg4_bytes(), make_embed))
-    del W0
-
-    res.extend(measure_chain(dev, flush, cold_iters))
-    del scratch
-    return res
+    return [run("cfg4 embedding [128256,4096] x16384", wl.cfg4_bytes(), make_embed)]
 
 
 def _back_to_back(fn, n, reps=5):
@@ -245,6 +269,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", choices=["all", "main", "ops", "copy", "chain"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--op", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"], default=None,
+                    help="with --only ops: measure one configuration")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
@@ -272,7 +298,7 @@ def main():
 
     ops_res = None
     if args.only in ("all", "ops"):
-        ops_res = measure_ops(dev)
+        ops_res = measure_ops(dev, only=args.op)
         if args.only == "ops":
             print(json.dumps({"ops": ops_res}))
             return

@@ -105,60 +105,58 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   const int nrope = nq + nk;
   const int total = live ? nrope + nkt + nv : 0;
 
-  // Batches of UB units per lane: all loads of a batch are issued before any math or store
-  // (a store may alias a later load as far as the compiler knows, so without batching each
-  // lane would have a single 16-byte load in flight). The host sizes UB so that a token's
-  // units fit one batch (up to 8 per lane).
+  // Wave-uniform token index (clamped for the padding slot of the last block): position and
+  // page lookup become scalar loads that do not wait behind the vector data loads.
+  const int64_t tq = uniform((int)(live ? t : 0));
+  const uint16_t* qrow = h.q + tq * h.q_ts;
+  const uint16_t* krow = h.k + tq * h.k_ts;
+  const uint16_t* vrow = h.v + tq * h.v_ts;
+  const uint16_t* safe = h.Hq > 0 ? qrow : krow;  // a valid 16-byte chunk of this token
+
+  // Batches of UB units per lane: all loads of a batch are issued before any math or store,
+  // and unconditionally (pointers chosen by selects; units past the end re-read `safe` and are
+  // discarded): loads inside divergent branches would each be followed by a wait. The host
+  // sizes UB so that a token's units fit one batch (up to 8 per lane).
   struct Batch {
     uint4 X[UB], Y[UB];
-    uint16_t* P[UB];  // rope: x chunk (updated in place); copy: source
-    int head[UB], c[UB], kind[UB];  // kind: 0 q rope, 1 k rope, 2 k tail copy, 3 v copy, -1 none
+    const uint16_t* P[UB];  // rope: x chunk (updated in place); copy: source
+    int head[UB], e0[UB], kind[UB];  // kind: 0 q rope, 1 k rope, 2 k tail copy, 3 v copy, -1 none
   };
-  // returns by value (captures scalars by value) so the batch stays in registers
   auto load_batch = [=](int u0) {
     Batch b;
 #pragma unroll
     for (int i = 0; i < UB; ++i) {
       const int u = u0 + i * gsize;
-      b.kind[i] = -1;
-      if (u >= total) continue;
-      if (ROPE && u < nrope) {
-        const bool isq = u < nq;
-        const int uu = isq ? u : u - nq;
-        b.head[i] = uu / uph;
-        b.c[i] = uu - b.head[i] * uph;
-        b.kind[i] = isq ? 0 : 1;
-        b.P[i] = (isq ? h.q + t * h.q_ts + (int64_t)b.head[i] * h.q_hs
-                      : h.k + t * h.k_ts + (int64_t)b.head[i] * h.k_hs) + b.c[i] * 8;
-        b.X[i] = ld_nt(b.P[i]);  // non-temporal: 5.33 vs 4.90 TB/s cached (steady state)
-        if constexpr (!INTERLEAVE) b.Y[i] = ld_nt(b.P[i] + half);
-      } else if (APPEND) {
-        int uu = u - nrope;
-        if (uu < nkt) {
-          b.head[i] = uu / tail;
-          b.c[i] = (ROPE ? h.rd : 0) + (uu - b.head[i] * tail) * 8;  // element offset in head
-          b.kind[i] = 2;
-          b.P[i] = h.k + t * h.k_ts + (int64_t)b.head[i] * h.k_hs + b.c[i];
-        } else {
-          uu -= nkt;
-          b.head[i] = uu / dv;
-          b.c[i] = (uu - b.head[i] * dv) * 8;
-          b.kind[i] = 3;
-          b.P[i] = const_cast<uint16_t*>(h.v) + t * h.v_ts + (int64_t)b.head[i] * h.v_hs + b.c[i];
-        }
-        b.X[i] = ld_nt(b.P[i]);
-      }
+      const bool valid = u < total;
+      const bool isq = ROPE && u < nq;
+      const bool isrope = ROPE && u < nrope;
+      const bool istail = APPEND && !isrope && u - nrope < nkt;
+      const int base = isq ? 0 : (isrope ? nq : (istail ? nrope : nrope + nkt));
+      const int div = isrope ? uph : (istail ? tail : dv);
+      const int uu = valid ? u - base : 0;
+      const int hd = uu / (div > 0 ? div : 1);
+      const int e0 = (istail ? (ROPE ? h.rd : 0) : 0) + (uu - hd * div) * 8;
+      const uint16_t* src = isq ? qrow + (int64_t)hd * h.q_hs
+                          : (isrope || istail) ? krow + (int64_t)hd * h.k_hs
+                                               : vrow + (int64_t)hd * h.v_hs;
+      src = valid ? src + e0 : safe;
+      b.P[i] = src;
+      b.head[i] = hd;
+      b.e0[i] = e0;
+      b.kind[i] = !valid ? -1 : (isq ? 0 : (isrope ? 1 : (istail ? 2 : 3)));
+      b.X[i] = ld_nt(src);  // non-temporal: 5.33 vs 4.90 TB/s cached (steady state)
+      if constexpr (ROPE && !INTERLEAVE) b.Y[i] = ld_nt(isrope ? src + half : src);
     }
     return b;
   };
 
   // Latency order: the position, the first batch of data and the page lookup chain are all
   // requested before the cos/sin table is computed, so they overlap it.
-  const float p = (ROPE && live) ? (float)a.pos[t] : 0.f;
+  const float p = ROPE ? (float)a.pos[tq] : 0.f;
   Batch b = load_batch(gt);
   int64_t kc = -1;
   if constexpr (APPEND) {
-    if (live) kc = slot_offset(a.c, t);
+    if (live) kc = slot_offset(a.c, tq);
   }
   if constexpr (ROPE) {
     if (live) {
@@ -175,55 +173,49 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
 
   for (int u0 = gt; u0 < total; u0 += gsize * UB) {
     if (u0 != gt) b = load_batch(u0);
-    const uint4* X = b.X;
-    const uint4* Y = b.Y;
-    uint16_t* const* P = b.P;
-    const int* head = b.head;
-    const int* c = b.c;
-    const int* kind = b.kind;
 #pragma unroll
     for (int i = 0; i < UB; ++i) {
-      if (kind[i] < 0) continue;
-      if (ROPE && kind[i] <= 1) {
+      const int kind = b.kind[i];
+      if (kind < 0) continue;
+      uint16_t* P = const_cast<uint16_t*>(b.P[i]);
+      const int64_t hoff = (int64_t)b.head[i] * a.c.head_stride + b.e0[i];
+      if (ROPE && kind <= 1) {
         if constexpr (!INTERLEAVE) {
           float x[8], y[8];
-          unpack8(X[i], x);
-          unpack8(Y[i], y);
+          unpack8(b.X[i], x);
+          unpack8(b.Y[i], y);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float2 cs = tb[c[i] * 8 + e];
+            const float2 cs = tb[b.e0[i] + e];
             const float xr = rot_x(x[e], y[e], cs);
             const float yr = rot_y(x[e], y[e], cs);
             x[e] = xr;
             y[e] = yr;
           }
           const uint4 xo = pack8(x), yo = pack8(y);
-          st_nt(P[i], xo);
-          st_nt(P[i] + half, yo);
-          if (APPEND && kind[i] == 1 && kc >= 0) {
-            uint16_t* dst = a.c.k_cache + kc + (int64_t)head[i] * a.c.head_stride + c[i] * 8;
-            st_nt(dst, xo);
-            st_nt(dst + half, yo);
+          st_nt(P, xo);
+          st_nt(P + half, yo);
+          if (APPEND && kind == 1 && kc >= 0) {
+            st_nt(a.c.k_cache + kc + hoff, xo);
+            st_nt(a.c.k_cache + kc + hoff + half, yo);
           }
         } else {
           float f[8];
-          unpack8(X[i], f);
+          unpack8(b.X[i], f);
 #pragma unroll
           for (int m = 0; m < 4; ++m) {
-            const float2 cs = tb[c[i] * 4 + m];
+            const float2 cs = tb[(b.e0[i] >> 1) + m];
             const float xr = rot_x(f[2 * m], f[2 * m + 1], cs);
             const float yr = rot_y(f[2 * m], f[2 * m + 1], cs);
             f[2 * m] = xr;
             f[2 * m + 1] = yr;
           }
           const uint4 o = pack8(f);
-          st_nt(P[i], o);
-          if (APPEND && kind[i] == 1 && kc >= 0)
-            st_nt(a.c.k_cache + kc + (int64_t)head[i] * a.c.head_stride + c[i] * 8, o);
+          st_nt(P, o);
+          if (APPEND && kind == 1 && kc >= 0) st_nt(a.c.k_cache + kc + hoff, o);
         }
       } else if (APPEND && kc >= 0) {
-        uint16_t* cache = kind[i] == 2 ? a.c.k_cache : a.c.v_cache;
-        st_nt(cache + kc + (int64_t)head[i] * a.c.head_stride + c[i], X[i]);
+        st_nt((kind == 2 ? a.c.k_cache : a.c.v_cache) + kc + hoff, b.X[i]);
       }
     }
   }
@@ -269,38 +261,45 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_d128(QkNormArgs qa) {
   const bool is_x = sub < 8;          // holds the x half (dims < 64) of its pairs
   const int sg = gt >> 4, nsg = gsize >> 4;
   const int nrows = h.Hq + 2 * h.Hkv;  // q heads, k heads, v heads
+  // Wave-uniform token index (clamped for the padding slot of the last block): the per-token
+  // position and page lookup become scalar loads, which complete on their own counter instead
+  // of behind the vector data loads.
+  const int64_t tq = uniform((int)(live ? t : 0));
 
   // Latency order: position and the first batch of rows are requested before the page
   // lookup chain and the cos/sin table, which then overlap the loads in flight.
   constexpr int UB = 4;  // head rows per 16-lane group per batch
-  const float p = live ? (float)a.pos[t] : 0.f;
+  const float p = (float)a.pos[tq];
   struct Batch {
     uint4 X[UB], Wt[UB];
     int kind[UB], hd[UB];  // kind: 0 q, 1 k, 2 v, 3 none
   };
+  // Branch-free loads (pointer chosen by selects, every load issued unconditionally): loads in
+  // divergent branches would each be followed by a wait, serialising the batch. Rows past the
+  // end re-read the token's first q row and are discarded.
+  const uint16_t* qrow = h.q + tq * h.q_ts;
+  const uint16_t* krow = h.k + tq * h.k_ts;
+  const uint16_t* vrow = h.v + tq * h.v_ts;
   auto load_batch = [=](int r0) {
     Batch b;
 #pragma unroll
     for (int i = 0; i < UB; ++i) {
       const int r = r0 + i * nsg;
-      b.kind[i] = (!live || r >= nrows) ? 3 : (r < h.Hq ? 0 : (r < h.Hq + h.Hkv ? 1 : 2));
-      b.hd[i] = b.kind[i] == 0 ? r : (b.kind[i] == 1 ? r - h.Hq : r - h.Hq - h.Hkv);
-      b.X[i] = make_uint4(0, 0, 0, 0);
-      b.Wt[i] = make_uint4(0, 0, 0, 0);
-      if (b.kind[i] == 0) {
-        b.X[i] = ld16(h.q + t * h.q_ts + (int64_t)b.hd[i] * h.q_hs + sub * 8);
-        b.Wt[i] = ld16(qa.qw + sub * 8);
-      } else if (b.kind[i] == 1) {
-        b.X[i] = ld16(h.k + t * h.k_ts + (int64_t)b.hd[i] * h.k_hs + sub * 8);
-        b.Wt[i] = ld16(qa.kw + sub * 8);
-      } else if (b.kind[i] == 2) {
-        b.X[i] = ld_nt(h.v + t * h.v_ts + (int64_t)b.hd[i] * h.v_hs + sub * 8);
-      }
+      const int kd = r >= nrows ? 3 : (r < h.Hq ? 0 : (r < h.Hq + h.Hkv ? 1 : 2));
+      const int hh = kd == 0 ? r : (kd == 1 ? r - h.Hq : (kd == 2 ? r - h.Hq - h.Hkv : 0));
+      const uint16_t* src = kd == 1 ? krow + (int64_t)hh * h.k_hs
+                          : kd == 2 ? vrow + (int64_t)hh * h.v_hs
+                          : kd == 0 ? qrow + (int64_t)hh * h.q_hs
+                                    : (h.Hq > 0 ? qrow : krow);
+      b.kind[i] = live ? kd : 3;
+      b.hd[i] = hh;
+      b.X[i] = ld_nt(src + sub * 8);
+      b.Wt[i] = ld16((kd == 1 || h.Hq == 0 ? qa.kw : qa.qw) + sub * 8);
     }
     return b;
   };
   Batch b = load_batch(sg);
-  const int64_t kc = live ? slot_offset(a.c, t) : -1;
+  const int64_t kc = live ? slot_offset(a.c, tq) : -1;
   if (live) {
     for (int i = gt; i < 64; i += gsize) {
       float sn, cs;
@@ -341,9 +340,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_d128(QkNormArgs qa) {
         own[e] = is_x ? rot_x(own[e], oth[e], tb[e]) : rot_y(oth[e], own[e], tb[e]);
       const uint4 o = pack8(own);
       if (kind[i] == 0) {
-        st16(qa.q_out + t * qa.qo_ts + (int64_t)hd[i] * qa.qo_hs + sub * 8, o);
+        st16(qa.q_out + tq * qa.qo_ts + (int64_t)hd[i] * qa.qo_hs + sub * 8, o);
       } else if (kind[i] == 1) {
-        st16(qa.k_out + t * qa.ko_ts + (int64_t)hd[i] * qa.ko_hs + sub * 8, o);
+        st16(qa.k_out + tq * qa.ko_ts + (int64_t)hd[i] * qa.ko_hs + sub * 8, o);
         if (kc >= 0) st_nt(a.c.k_cache + kc + (int64_t)hd[i] * a.c.head_stride + sub * 8, o);
       } else if (kind[i] == 2 && kc >= 0) {
         st_nt(a.c.v_cache + kc + (int64_t)hd[i] * a.c.head_stride + sub * 8, X[i]);
