@@ -281,21 +281,21 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
   const bool vec = a.cols % 8 == 0 && rowset_vec_ok(a.set[0], ADD) &&
                    (a.set[1].rows == 0 || rowset_vec_ok(a.set[1], ADD));
   const dim3 blk(256);
-  if (vec && a.set[1].rows == 0 && a.cols % 512 == 0 && a.cols <= 8 * 16 * 512) {
+  if (vec && a.set[1].rows == 0 && a.cols % 512 == 0 && a.cols <= 8 * 12 * 512) {
     const int64_t n512 = a.cols / 512, target = (int64_t)num_cus() * 16;
     // As many waves per row as divide it (up to 8): one or two 16-byte vectors per lane keeps
     // VGPR use low, so more rows are in flight per CU and the last wave of rows is shorter
     // (measured on configuration 2: 8 waves 46.0 us, 1 wave 50.4 us).
     int W = 0;
     for (int w = 8; w >= 1; w /= 2)
-      if (n512 % w == 0 && n512 / w <= 16) { W = w; break; }
+      if (n512 % w == 0 && n512 / w <= 12) { W = w; break; }
     (void)target;
     static const int forced = [] {  // tuning override: PIE_HIP_NORM_WAVES=1|2|4|8
       const char* e = getenv("PIE_HIP_NORM_WAVES");
       return e ? atoi(e) : 0;
     }();
     if (forced == 1 || forced == 2 || forced == 4 || forced == 8)
-      if (n512 % forced == 0 && n512 / forced <= 16) W = forced;
+      if (n512 % forced == 0 && n512 / forced <= 12) W = forced;
     if (W > 0) {
       const int threads = W == 8 ? 512 : 256;
       const int64_t G = threads / (64 * W);
@@ -307,7 +307,7 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
 #define PIE_NV(n) \
   case n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, ADD>), grd, tb, 0, st, a, W); break;
         PIE_NV(1) PIE_NV(2) PIE_NV(3) PIE_NV(4) PIE_NV(5) PIE_NV(6) PIE_NV(7) PIE_NV(8)
-        PIE_NV(9) PIE_NV(10) PIE_NV(11) PIE_NV(12) PIE_NV(13) PIE_NV(14) PIE_NV(15) PIE_NV(16)
+        PIE_NV(9) PIE_NV(10) PIE_NV(11) PIE_NV(12)
 #undef PIE_NV
       }
       return check_launch(name);

@@ -82,6 +82,49 @@ __device__ __forceinline__ int64_t slot_offset(const CacheDesc& c, int64_t t) {
   return (int64_t)page * c.page_stride + (int64_t)(p % c.page_size) * c.slot_stride;
 }
 
+// Per-token unit layout of rope_append_vec: [q rope | k rope | k tail copy | v copy].
+struct UnitGeom {
+  int gsize, total, nq, nrope, nkt, uph, tail, dv, half, rd_off;
+  int64_t q_hs, k_hs, v_hs;
+  const uint16_t *qrow, *krow, *vrow, *safe;
+};
+template <int UB>
+struct UnitBatch {
+  uint4 X[UB], Y[UB];
+  const uint16_t* P[UB];  // rope: x chunk (updated in place); copy: source
+  int head[UB], e0[UB], kind[UB];  // kind: 0 q rope, 1 k rope, 2 k tail copy, 3 v copy, -1 none
+};
+
+// Loads the UB units u0, u0+gsize, ... of one token. All loads are issued unconditionally,
+// with pointers chosen by selects (units past the end re-read `safe` and are discarded):
+// loads inside divergent branches would each be followed by a wait, serialising the batch.
+template <bool ROPE, bool APPEND, bool INTERLEAVE, int UB>
+__device__ __forceinline__ void load_units(UnitBatch<UB>& b, const UnitGeom g, int u0) {
+#pragma unroll
+  for (int i = 0; i < UB; ++i) {
+    const int u = u0 + i * g.gsize;
+    const bool valid = u < g.total;
+    const bool isq = ROPE && u < g.nq;
+    const bool isrope = ROPE && u < g.nrope;
+    const bool istail = APPEND && !isrope && u - g.nrope < g.nkt;
+    const int base = isq ? 0 : (isrope ? g.nq : (istail ? g.nrope : g.nrope + g.nkt));
+    const int div = isrope ? g.uph : (istail ? g.tail : g.dv);
+    const int uu = valid ? u - base : 0;
+    const int hd = uu / (div > 0 ? div : 1);
+    const int e0 = (istail ? g.rd_off : 0) + (uu - hd * div) * 8;
+    const uint16_t* src = isq ? g.qrow + (int64_t)hd * g.q_hs
+                        : (isrope || istail) ? g.krow + (int64_t)hd * g.k_hs
+                                             : g.vrow + (int64_t)hd * g.v_hs;
+    src = valid ? src + e0 : g.safe;
+    b.P[i] = src;
+    b.head[i] = hd;
+    b.e0[i] = e0;
+    b.kind[i] = !valid ? -1 : (isq ? 0 : (isrope ? 1 : (istail ? 2 : 3)));
+    b.X[i] = ld_nt(src);  // non-temporal: 5.33 vs 4.90 TB/s cached (steady state)
+    if constexpr (ROPE && !INTERLEAVE) b.Y[i] = ld_nt(isrope ? src + g.half : src);
+  }
+}
+
 template <bool ROPE, bool APPEND, bool INTERLEAVE, int UB>
 __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   __shared__ float2 tab[4][ROPE ? kMaxPairs : 1];
@@ -92,7 +135,8 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   const int gsize = wpt * 64;
   const int64_t t = (int64_t)blockIdx.x * tpb + slot;
   const bool live = t < a.T;
-  const HeadsDesc& h = a.h;
+  const HeadsDesc h = a.h;
+  const CacheDesc cd = a.c;  // by value: no reference into the kernel-argument block
   const int half = h.rd >> 1;
 
   const int uph = ROPE ? (INTERLEAVE ? h.rd >> 3 : h.rd >> 4) : 0;  // rope units per head
@@ -113,50 +157,17 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   const uint16_t* vrow = h.v + tq * h.v_ts;
   const uint16_t* safe = h.Hq > 0 ? qrow : krow;  // a valid 16-byte chunk of this token
 
-  // Batches of UB units per lane: all loads of a batch are issued before any math or store,
-  // and unconditionally (pointers chosen by selects; units past the end re-read `safe` and are
-  // discarded): loads inside divergent branches would each be followed by a wait. The host
-  // sizes UB so that a token's units fit one batch (up to 8 per lane).
-  struct Batch {
-    uint4 X[UB], Y[UB];
-    const uint16_t* P[UB];  // rope: x chunk (updated in place); copy: source
-    int head[UB], e0[UB], kind[UB];  // kind: 0 q rope, 1 k rope, 2 k tail copy, 3 v copy, -1 none
-  };
-  auto load_batch = [=](int u0) {
-    Batch b;
-#pragma unroll
-    for (int i = 0; i < UB; ++i) {
-      const int u = u0 + i * gsize;
-      const bool valid = u < total;
-      const bool isq = ROPE && u < nq;
-      const bool isrope = ROPE && u < nrope;
-      const bool istail = APPEND && !isrope && u - nrope < nkt;
-      const int base = isq ? 0 : (isrope ? nq : (istail ? nrope : nrope + nkt));
-      const int div = isrope ? uph : (istail ? tail : dv);
-      const int uu = valid ? u - base : 0;
-      const int hd = uu / (div > 0 ? div : 1);
-      const int e0 = (istail ? (ROPE ? h.rd : 0) : 0) + (uu - hd * div) * 8;
-      const uint16_t* src = isq ? qrow + (int64_t)hd * h.q_hs
-                          : (isrope || istail) ? krow + (int64_t)hd * h.k_hs
-                                               : vrow + (int64_t)hd * h.v_hs;
-      src = valid ? src + e0 : safe;
-      b.P[i] = src;
-      b.head[i] = hd;
-      b.e0[i] = e0;
-      b.kind[i] = !valid ? -1 : (isq ? 0 : (isrope ? 1 : (istail ? 2 : 3)));
-      b.X[i] = ld_nt(src);  // non-temporal: 5.33 vs 4.90 TB/s cached (steady state)
-      if constexpr (ROPE && !INTERLEAVE) b.Y[i] = ld_nt(isrope ? src + half : src);
-    }
-    return b;
-  };
-
+  // Batches of UB units per lane, loaded by load_units (below).
+  const UnitGeom g{gsize, total, nq, nrope, nkt, uph, tail, dv, half, ROPE ? h.rd : 0,
+                   h.q_hs, h.k_hs, h.v_hs, qrow, krow, vrow, safe};
+  UnitBatch<UB> b;
   // Latency order: the position, the first batch of data and the page lookup chain are all
   // requested before the cos/sin table is computed, so they overlap it.
   const float p = ROPE ? (float)a.pos[tq] : 0.f;
-  Batch b = load_batch(gt);
+  load_units<ROPE, APPEND, INTERLEAVE, UB>(b, g, gt);
   int64_t kc = -1;
   if constexpr (APPEND) {
-    if (live) kc = slot_offset(a.c, tq);
+    if (live) kc = slot_offset(cd, tq);
   }
   if constexpr (ROPE) {
     if (live) {
@@ -172,13 +183,13 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   const float2* tb = tab[slot];
 
   for (int u0 = gt; u0 < total; u0 += gsize * UB) {
-    if (u0 != gt) b = load_batch(u0);
+    if (u0 != gt) load_units<ROPE, APPEND, INTERLEAVE, UB>(b, g, u0);
 #pragma unroll
     for (int i = 0; i < UB; ++i) {
       const int kind = b.kind[i];
       if (kind < 0) continue;
       uint16_t* P = const_cast<uint16_t*>(b.P[i]);
-      const int64_t hoff = (int64_t)b.head[i] * a.c.head_stride + b.e0[i];
+      const int64_t hoff = (int64_t)b.head[i] * cd.head_stride + b.e0[i];
       if (ROPE && kind <= 1) {
         if constexpr (!INTERLEAVE) {
           float x[8], y[8];
@@ -196,8 +207,8 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
           st_nt(P, xo);
           st_nt(P + half, yo);
           if (APPEND && kind == 1 && kc >= 0) {
-            st_nt(a.c.k_cache + kc + hoff, xo);
-            st_nt(a.c.k_cache + kc + hoff + half, yo);
+            st_nt(cd.k_cache + kc + hoff, xo);
+            st_nt(cd.k_cache + kc + hoff + half, yo);
           }
         } else {
           float f[8];
@@ -212,10 +223,10 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
           }
           const uint4 o = pack8(f);
           st_nt(P, o);
-          if (APPEND && kind == 1 && kc >= 0) st_nt(a.c.k_cache + kc + hoff, o);
+          if (APPEND && kind == 1 && kc >= 0) st_nt(cd.k_cache + kc + hoff, o);
         }
       } else if (APPEND && kc >= 0) {
-        st_nt((kind == 2 ? a.c.k_cache : a.c.v_cache) + kc + hoff, b.X[i]);
+        st_nt((kind == 2 ? cd.k_cache : cd.v_cache) + kc + hoff, b.X[i]);
       }
     }
   }
