@@ -78,19 +78,32 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
 def _rotating(calls, iters=60, reps=3):
     """µs per launch over back-to-back launches that rotate through independent buffer sets
     (together larger than the 256 MB last-level cache), so each launch pays for its own HBM
-    reads and for draining its writes; median over reps."""
+    reads and for draining its writes. The launches are recorded into one HIP graph and
+    replayed, so host-side launch cost (Python, ctypes) does not limit small ops; median over
+    reps."""
     import torch
-    for c in calls:
-        c()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for c in calls:
+            c()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(iters):
+            calls[i % len(calls)]()
+    g.replay()
+    torch.cuda.synchronize()
     out = []
     for _ in range(reps):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        for i in range(iters):
-            calls[i % len(calls)]()
+        g.replay()
         b.record()
         torch.cuda.synchronize()
         out.append(a.elapsed_time(b) * 1e3 / iters)
+    del g
     return statistics.median(out)
 
 

@@ -17,6 +17,7 @@
 #include "common.h"
 
 
+
 namespace pie {
 namespace {
 
@@ -55,19 +56,23 @@ __device__ __forceinline__ void row_offsets(const RowSet& s, int64_t r, int64_t&
   oo = t * s.out_ts + h * s.out_hs;
 }
 
+// Rows per wave group in flight at once. 1 measured best on configuration 2 (steady state:
+// 2 rows equal, 4 rows 6% slower: the extra registers cost more occupancy than they gain).
+constexpr int kRowsPerGroup = 1;
+
 // ---------------------------------------------------------------- W waves per row, VPL*512*W cols
 // A row is held in registers by a group of W wavefronts (VPL 16-byte vectors per lane); lane l
 // of wave g in the group owns vectors j*64*W + g*64 + l. W = 1 for long row lists (no barrier);
 // W > 1 spreads short lists (decode batches) over the chip, combining the W partial sums of
 // squares through LDS in a fixed order. The weight row stays in registers across rows.
-template <int VPL, bool ADD>
+template <int VPL, int RPG, bool ADD>
 __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
-  __shared__ float part[8];
+  __shared__ float part[RPG][8];
   const RowSet& s = a.set[0];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = wave / W, gsub = wave - grp * W;
   const int G = blockDim.x / (64 * W);  // row groups per block
-  const int64_t stride = (int64_t)gridDim.x * G;
+  const int64_t stride = (int64_t)gridDim.x * G * RPG;
   const int vstep = 64 * W;
   const int v0 = gsub * 64 + lane;
 
@@ -75,58 +80,77 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
 #pragma unroll
   for (int j = 0; j < VPL; ++j) wv[j] = ld16(s.w + (int64_t)(v0 + j * vstep) * 8);
 
-  // block-uniform trip count: every thread reaches every barrier
-  for (int64_t base = (int64_t)blockIdx.x * G; base < s.rows; base += stride) {
-    const int64_t r = base + grp;
-    const bool live = r < s.rows;
-    int64_t oi = 0, orr = 0, os = 0, oo = 0;
-    if (live) row_offsets(s, r, oi, orr, os, oo);
-    uint4 xv[VPL];
-    float ss = 0.f;
-    if (live) {
+  // A group handles RPG rows at once (rows base+grp, base+grp+G, ...): all their loads are in
+  // flight before the first reduction. Block-uniform trip count: every thread reaches every
+  // barrier.
+  for (int64_t base = (int64_t)blockIdx.x * G * RPG; base < s.rows; base += stride) {
+    int64_t oo[RPG];
+    bool live[RPG];
+    uint4 xv[RPG][VPL];
+    float ss[RPG];
 #pragma unroll
-      for (int j = 0; j < VPL; ++j) xv[j] = ld16(s.in + oi + (int64_t)(v0 + j * vstep) * 8);
-      if constexpr (ADD) {
-        uint4 rv[VPL];
+    for (int k = 0; k < RPG; ++k) {
+      const int64_t r = base + grp + (int64_t)k * G;
+      live[k] = r < s.rows;
+      int64_t oi = 0, orr = 0, os = 0;
+      oo[k] = 0;
+      if (live[k]) row_offsets(s, r, oi, orr, os, oo[k]);
+      ss[k] = 0.f;
+      if (live[k]) {
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) rv[j] = ld16(s.res + orr + (int64_t)(v0 + j * vstep) * 8);
+        for (int j = 0; j < VPL; ++j) xv[k][j] = ld16(s.in + oi + (int64_t)(v0 + j * vstep) * 8);
+        if constexpr (ADD) {
+          uint4 rv[VPL];
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) rv[j] = ld16(s.res + orr + (int64_t)(v0 + j * vstep) * 8);
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) {
+            float xf[8], rf[8];
+            unpack8(xv[k][j], xf);
+            unpack8(rv[j], rf);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xf[e] = rf[e] + xf[e];
+            xv[k][j] = pack8(xf);  // s rounded to bf16: the norm below reads the rounded values
+            st16(s.sum + os + (int64_t)(v0 + j * vstep) * 8, xv[k][j]);
+          }
+        }
 #pragma unroll
         for (int j = 0; j < VPL; ++j) {
-          float xf[8], rf[8];
-          unpack8(xv[j], xf);
-          unpack8(rv[j], rf);
+          float xf[8];
+          unpack8(xv[k][j], xf);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) xf[e] = rf[e] + xf[e];
-          xv[j] = pack8(xf);  // s rounded to bf16: the norm below reads the rounded values
-          st16(s.sum + os + (int64_t)(v0 + j * vstep) * 8, xv[j]);
+          for (int e = 0; e < 8; ++e) ss[k] += xf[e] * xf[e];
         }
       }
-#pragma unroll
-      for (int j = 0; j < VPL; ++j) {
-        float xf[8];
-        unpack8(xv[j], xf);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += xf[e] * xf[e];
-      }
     }
-    float tot = wave_sum(ss);
+    float tot[RPG];
+#pragma unroll
+    for (int k = 0; k < RPG; ++k) tot[k] = wave_sum(ss[k]);
     if (W > 1) {
-      if (lane == 0) part[wave] = tot;
+      if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < RPG; ++k) part[k][wave] = tot[k];
+      }
       __syncthreads();
-      tot = 0.f;
-      for (int k = 0; k < W; ++k) tot += part[grp * W + k];
+#pragma unroll
+      for (int k = 0; k < RPG; ++k) {
+        tot[k] = 0.f;
+        for (int q = 0; q < W; ++q) tot[k] += part[k][grp * W + q];
+      }
       __syncthreads();
     }
-    if (live) {
-      const float rstd = rsqrtf(tot / (float)a.cols + a.eps);
+#pragma unroll
+    for (int k = 0; k < RPG; ++k) {
+      if (!live[k]) continue;
+      const float rstd = rsqrtf(tot[k] / (float)a.cols + a.eps);
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
         float xf[8], wf[8];
-        unpack8(xv[j], xf);
+        unpack8(xv[k][j], xf);
         unpack8(wv[j], wf);
 #pragma unroll
         for (int e = 0; e < 8; ++e) xf[e] = (xf[e] * rstd) * wf[e];
-        st16(s.out + oo + (int64_t)(v0 + j * vstep) * 8, pack8(xf));
+        st16(s.out + oo[k] + (int64_t)(v0 + j * vstep) * 8, pack8(xf));
       }
     }
   }
@@ -299,13 +323,13 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
     if (W > 0) {
       const int threads = W == 8 ? 512 : 256;
       const int64_t G = threads / (64 * W);
-      int64_t blocks = (rows + G - 1) / G;
+      int64_t blocks = (rows + G * kRowsPerGroup - 1) / (G * kRowsPerGroup);
       const int64_t cap = (int64_t)num_cus() * 64;
       if (blocks > cap) blocks = cap;
       const dim3 grd((unsigned)blocks), tb(threads);
       switch (n512 / W) {
 #define PIE_NV(n) \
-  case n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, ADD>), grd, tb, 0, st, a, W); break;
+  case n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, kRowsPerGroup, ADD>), grd, tb, 0, st, a, W); break;
         PIE_NV(1) PIE_NV(2) PIE_NV(3) PIE_NV(4) PIE_NV(5) PIE_NV(6) PIE_NV(7) PIE_NV(8)
         PIE_NV(9) PIE_NV(10) PIE_NV(11) PIE_NV(12)
 #undef PIE_NV
