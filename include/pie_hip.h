@@ -49,6 +49,28 @@ int pie_hip_rmsnorm(const pie_bf16* x, int64_t x_row_stride,
                     int64_t rows, int64_t cols, float eps, void* stream);
 
 /*
+ * Gemma RMSNorm: the expression of pie/src/pie_worker/model/gemma2.py:514-526 and
+ * gemma3.py:491-510 (and their q/k norm, gemma3.py:499-510),
+ *   variance = x.pow(2).mean(-1); x * rsqrt(variance + eps) * (1.0 + weight)
+ * evaluated as separate bf16 torch ops: every intermediate is rounded to bf16. Same arguments
+ * as pie_hip_rmsnorm / pie_hip_fused_add_rmsnorm / pie_hip_qk_rmsnorm (the add variant sums
+ * first, as `residual + down` (gemma3.py:585) feeding the next layer's norm).
+ */
+int pie_hip_gemma_rmsnorm(const pie_bf16* x, int64_t x_row_stride, const pie_bf16* w,
+                          pie_bf16* y, int64_t y_row_stride, int64_t rows, int64_t cols, float eps,
+                          void* stream);
+int pie_hip_gemma_fused_add_rmsnorm(const pie_bf16* x, int64_t x_row_stride, const pie_bf16* r,
+                                    int64_t r_row_stride, pie_bf16* s, int64_t s_row_stride,
+                                    pie_bf16* y, int64_t y_row_stride, const pie_bf16* w,
+                                    int64_t rows, int64_t cols, float eps, void* stream);
+int pie_hip_gemma_qk_rmsnorm(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                             pie_bf16* q_out, int64_t qo_tok_stride, int64_t qo_head_stride,
+                             const pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                             pie_bf16* k_out, int64_t ko_tok_stride, int64_t ko_head_stride,
+                             const pie_bf16* qw, const pie_bf16* kw, int64_t T, int64_t Hq,
+                             int64_t Hkv, int64_t D, float eps, void* stream);
+
+/*
  * Residual add followed by RMSNorm of the sum:
  *   s = bf16(f32(r) + f32(x));  y = rmsnorm(s)
  * Replaces `residual + down` / `residual + attn_proj` (llama3.py:586, :710; qwen3.py:571, :710)
@@ -86,6 +108,16 @@ int pie_hip_silu_and_mul(const pie_bf16* gate_up, int64_t in_row_stride,
                          int64_t rows, int64_t I, void* stream);
 
 /*
+ * GELU(tanh)-and-mul: out = bf16( f32(bf16(gelu_tanh(f32(gate)))) * f32(up) ), the
+ * `_gelu_pytorch_tanh(gate) * up` of pie/src/pie_worker/model/gemma2.py:224-226, :608 and
+ * gemma3.py:246-248, :566 (torch gelu with approximate="tanh"). Same layout as
+ * pie_hip_silu_and_mul.
+ */
+int pie_hip_gelu_tanh_and_mul(const pie_bf16* gate_up, int64_t in_row_stride,
+                              pie_bf16* out, int64_t out_row_stride,
+                              int64_t rows, int64_t I, void* stream);
+
+/*
  * Token-embedding gather: out[t,:] = W[ids[t],:] (bit copy).
  * Replaces fun.embedding(token_ids, W) at llama3.py:471 and qwen3.py:468-472.
  * Ids outside [0, V) produce a zero row (torch raises instead; a graph-capturable kernel
@@ -94,6 +126,15 @@ int pie_hip_silu_and_mul(const pie_bf16* gate_up, int64_t in_row_stride,
 int pie_hip_embedding(const int32_t* ids, int64_t T,
                       const pie_bf16* W, int64_t V, int64_t H, int64_t w_row_stride,
                       pie_bf16* out, int64_t out_row_stride, void* stream);
+
+/*
+ * Scaled embedding: out[t,:] = bf16(f32(W[ids[t],:]) * scale), the
+ * `fun.embedding(ids, W) * self.embed_normalizer` of pie/src/pie_worker/model/gemma3.py:476-489
+ * and gemma2.py (scale = fp32(sqrt(hidden))). Out-of-range ids give zero rows.
+ */
+int pie_hip_embedding_scaled(const int32_t* ids, int64_t T,
+                             const pie_bf16* W, int64_t V, int64_t H, int64_t w_row_stride,
+                             pie_bf16* out, int64_t out_row_stride, float scale, void* stream);
 
 /*
  * Rotary embedding applied in place to q [T,Hq,D] and k [T,Hkv,D] at positions pos[T].
@@ -110,6 +151,20 @@ int pie_hip_rope_inplace(pie_bf16* q, int64_t q_tok_stride, int64_t q_head_strid
                          const int32_t* pos, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
                          int64_t rotary_dim, int interleave, const float* inv_freq,
                          void* stream);
+
+/*
+ * RoPE in place from a precomputed fp32 table: row pos[t] of cos_sin_cache holds cos at
+ * [0, rotary_dim/2) and sin at [rotary_dim/2, rotary_dim) (row stride cache_ld elements).
+ * interleave=0 is is_neox=True. Positions outside [0, cache_rows) leave the token unchanged.
+ * Replaces flashinfer.apply_rope_with_cos_sin_cache_inplace (gpt_oss.py:671-678,
+ * olmo3.py:797-804; YaRN tables built at gpt_oss.py:520-547, olmo3.py:447-525).
+ */
+int pie_hip_rope_cos_sin_cache_inplace(pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                       pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                                       const int32_t* pos, int64_t T, int64_t Hq, int64_t Hkv,
+                                       int64_t D, int interleave, const float* cos_sin_cache,
+                                       int64_t cache_rows, int64_t rotary_dim, int64_t cache_ld,
+                                       void* stream);
 
 /*
  * Host helpers: fill inv_freq[rotary_dim/2] (computed in float64, rounded to fp32).

@@ -37,6 +37,7 @@ _lib = None
 _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 i64 = C.c_int64
 
 
@@ -67,6 +68,12 @@ def _load():
                                 C.c_void_p, C.c_void_p, i64, i64, i64, i64, i64, i64, i64, i64]),
         "oracle_seq_lens": (None, [_i32p, _i32p, i64, i64, _i32p]),
         "oracle_batch_indices_positions": (None, [_i32p, _i32p, i64, i64, _i32p, _i32p]),
+        "oracle_gemma_rmsnorm": (None, [_u16p, i64, i64, _u16p, _u16p, i64, i64, i64, i64, i64, C.c_double]),
+        "oracle_gemma_add_rmsnorm": (None, [_u16p, _u16p, _u16p, _u16p, _u16p, i64, i64, C.c_double]),
+        "oracle_gelu_tanh_and_mul": (None, [_u16p, i64, _u16p, i64, i64]),
+        "oracle_embedding_scaled": (i64, [_i32p, i64, _u16p, i64, i64, C.c_float, _u16p]),
+        "oracle_rope_cs": (None, [_u16p, i64, i64, _u16p, i64, i64, _i32p, i64, i64, i64, i64,
+                                  C.c_int, _f32p, i64, i64]),
         "oracle_f32_to_bf16": (C.c_uint16, [C.c_float]),
         "oracle_f64_to_bf16": (C.c_uint16, [C.c_double]),
     }
@@ -140,6 +147,55 @@ def silu_and_mul(gu: np.ndarray, mode: int = 0) -> np.ndarray:
     out = np.empty((*gu.shape[:-1], I), dtype=np.uint16)
     _load().oracle_silu_and_mul(gu, 2 * I, out, rows, I, mode)
     return out
+
+
+def gemma_rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """Gemma RMSNorm with bf16 rounding after every torch op (gemma2.py:514-526)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    H = x.shape[-1]
+    y = np.empty_like(x)
+    _load().oracle_gemma_rmsnorm(x, H, 0, np.ascontiguousarray(w, np.uint16), y, H, 0,
+                                 x.size // H if H else 0, 1, H, eps)
+    return y
+
+
+def gemma_add_rmsnorm(x: np.ndarray, r: np.ndarray, w: np.ndarray, eps: float):
+    """Returns (y, s): s = bf16(r + x), y = gemma_rmsnorm(s)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    r = np.ascontiguousarray(r, dtype=np.uint16)
+    H = x.shape[-1]
+    s, y = np.empty_like(x), np.empty_like(x)
+    _load().oracle_gemma_add_rmsnorm(x, r, np.ascontiguousarray(w, np.uint16), s, y, x.size // H, H, eps)
+    return y, s
+
+
+def gelu_tanh_and_mul(gu: np.ndarray) -> np.ndarray:
+    gu = np.ascontiguousarray(gu, dtype=np.uint16)
+    I = gu.shape[-1] // 2
+    out = np.empty((*gu.shape[:-1], I), dtype=np.uint16)
+    _load().oracle_gelu_tanh_and_mul(gu, 2 * I, out, gu.size // (2 * I) if I else 0, I)
+    return out
+
+
+def embedding_scaled(ids: np.ndarray, W: np.ndarray, scale: float):
+    ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
+    W = np.ascontiguousarray(W, dtype=np.uint16)
+    V, H = W.shape
+    out = np.empty((ids.size, H), dtype=np.uint16)
+    bad = _load().oracle_embedding_scaled(ids, ids.size, W, V, H, float(np.float32(scale)), out)
+    return out, int(bad)
+
+
+def rope_cos_sin(q: np.ndarray, k: np.ndarray, pos, cos_sin: np.ndarray, interleave=False):
+    """Rotated copies of q [T,Hq,D], k [T,Hkv,D] with cos/sin from a [rows, rd] fp32 table."""
+    q = np.array(q, dtype=np.uint16, order="C", copy=True)
+    k = np.array(k, dtype=np.uint16, order="C", copy=True)
+    cs = np.ascontiguousarray(cos_sin, dtype=np.float32)
+    T, Hq, D = q.shape
+    _load().oracle_rope_cs(q, Hq * D, D, k, k.shape[1] * D, D, np.ascontiguousarray(pos, np.int32),
+                           T, Hq, k.shape[1], cs.shape[1], 1 if interleave else 0, cs,
+                           cs.shape[0], cs.shape[1])
+    return q, k
 
 
 def embedding(ids: np.ndarray, W: np.ndarray):

@@ -13,6 +13,10 @@
  *   add_rmsnorm        `residual + down` (llama3.py:586) then the next rms_norm (llama3.py:555)
  *   silu_and_mul       `fun.silu(gate) * up` after torch.split (llama3.py:569-572)
  *   embedding          fun.embedding(ids, W) (llama3.py:471)
+ *   gemma_rmsnorm      pie/src/pie_worker/model/gemma2.py:514-526, gemma3.py:491-510
+ *   gelu_tanh_and_mul  gemma2.py:224-226, :608
+ *   embedding_scaled   gemma3.py:476-489
+ *   rope_cs            flashinfer.apply_rope_with_cos_sin_cache_inplace (gpt_oss.py:671-678)
  *   rope               pie/src/flashinfer_metal/kernels/metal_rope.metal:26-107
  *   inv_freq_llama31   metal_rope.metal:63-89
  *   append             pie/src/flashinfer_metal/kernels/metal_append_paged_kv_cache.metal:23-107
@@ -92,6 +96,42 @@ void oracle_add_rmsnorm(const uint16_t* x, const uint16_t* r, const uint16_t* w,
   }
 }
 
+/* Gemma RMSNorm, pie/src/pie_worker/model/gemma2.py:514-526 / gemma3.py:491-510:
+ *   variance = x.pow(2).mean(-1); x * rsqrt(variance + eps) * (1.0 + weight)
+ * as separate bf16 torch ops: each step's result is rounded to bf16 (the mean's sum itself is
+ * exact here, torch accumulates it in fp32). */
+static void gemma_row(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t cols, double eps) {
+  double ss = 0.0;
+  for (int64_t j = 0; j < cols; ++j) {
+    float v = bf2f(x[j]);
+    ss += bf2f(f2bf(v * v));
+  }
+  float var = bf2f(d2bf(ss / (double)cols));
+  float t = bf2f(f2bf(var + (float)eps));
+  float r = bf2f(d2bf(1.0 / sqrt((double)t)));
+  for (int64_t j = 0; j < cols; ++j) {
+    float xn = bf2f(d2bf((double)bf2f(x[j]) * r));
+    float w1 = bf2f(f2bf(1.0f + bf2f(w[j])));
+    y[j] = d2bf((double)xn * w1);
+  }
+}
+
+void oracle_gemma_rmsnorm(const uint16_t* x, int64_t x_ts, int64_t x_hs, const uint16_t* w,
+                          uint16_t* y, int64_t y_ts, int64_t y_hs, int64_t T, int64_t heads,
+                          int64_t cols, double eps) {
+  for (int64_t t = 0; t < T; ++t)
+    for (int64_t h = 0; h < heads; ++h)
+      gemma_row(x + t * x_ts + h * x_hs, w, y + t * y_ts + h * y_hs, cols, eps);
+}
+
+void oracle_gemma_add_rmsnorm(const uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* s,
+                              uint16_t* y, int64_t rows, int64_t cols, double eps) {
+  for (int64_t i = 0; i < rows; ++i) {
+    for (int64_t j = 0; j < cols; ++j) s[i * cols + j] = f2bf(bf2f(r[i * cols + j]) + bf2f(x[i * cols + j]));
+    gemma_row(s + i * cols, w, y + i * cols, cols, eps);
+  }
+}
+
 /* ------------------------------------------------------------------ SiLU-and-mul */
 /* mode 0: torch's rounding, bf16(bf16(silu(g)) * up); mode 1: single rounding of silu(g)*up. */
 void oracle_silu_and_mul(const uint16_t* gu, int64_t in_rs, uint16_t* out, int64_t rows,
@@ -103,6 +143,20 @@ void oracle_silu_and_mul(const uint16_t* gu, int64_t in_rs, uint16_t* out, int64
       double s = g / (1.0 + exp(-g));
       if (mode == 0) out[i * I + j] = d2bf((double)bf2f(d2bf(s)) * u);
       else out[i * I + j] = d2bf(s * u);
+    }
+}
+
+/* GELU(tanh)-and-mul, `_gelu_pytorch_tanh(gate) * up` (gemma2.py:224-226, :608):
+ * torch gelu(approximate="tanh") rounded to bf16, times up, rounded again. */
+void oracle_gelu_tanh_and_mul(const uint16_t* gu, int64_t in_rs, uint16_t* out, int64_t rows,
+                              int64_t I) {
+  const double k0 = sqrt(2.0 / M_PI);
+  for (int64_t i = 0; i < rows; ++i)
+    for (int64_t j = 0; j < I; ++j) {
+      double g = bf2f(gu[i * in_rs + j]);
+      double u = bf2f(gu[i * in_rs + I + j]);
+      double gl = 0.5 * g * (1.0 + tanh(k0 * (g + 0.044715 * g * g * g)));
+      out[i * I + j] = d2bf((double)bf2f(d2bf(gl)) * u);
     }
 }
 
@@ -118,6 +172,22 @@ int64_t oracle_embedding(const int32_t* ids, int64_t T, const uint16_t* W, int64
     } else {
       memcpy(out + t * H, W + (int64_t)ids[t] * H, (size_t)H * 2);
     }
+  }
+  return bad;
+}
+
+/* `fun.embedding(ids, W) * self.embed_normalizer` (gemma3.py:476-489): torch multiplies the bf16
+ * rows by the scalar in fp32 and rounds once. Out-of-range ids give zero rows. */
+int64_t oracle_embedding_scaled(const int32_t* ids, int64_t T, const uint16_t* W, int64_t V,
+                                int64_t H, float scale, uint16_t* out) {
+  int64_t bad = 0;
+  for (int64_t t = 0; t < T; ++t) {
+    if (ids[t] < 0 || ids[t] >= V) {
+      memset(out + t * H, 0, (size_t)H * 2);
+      ++bad;
+      continue;
+    }
+    for (int64_t j = 0; j < H; ++j) out[t * H + j] = f2bf(bf2f(W[(int64_t)ids[t] * H + j]) * scale);
   }
   return bad;
 }
@@ -159,6 +229,30 @@ void oracle_rope(uint16_t* q, int64_t q_ts, int64_t q_hs, uint16_t* k, int64_t k
     double p = (double)pos[t];
     for (int64_t h = 0; h < Hq; ++h) rope_head(q + t * q_ts + h * q_hs, rd, interleave, p, inv_freq);
     for (int64_t h = 0; h < Hkv; ++h) rope_head(k + t * k_ts + h * k_hs, rd, interleave, p, inv_freq);
+  }
+}
+
+/* RoPE from a cos/sin table (flashinfer.apply_rope_with_cos_sin_cache_inplace, gpt_oss.py:671):
+ * row pos of `cs` (stride ld) holds cos at [0, rd/2) and sin at [rd/2, rd); positions outside
+ * [0, rows) leave the token unchanged. */
+static void rope_head_cs(uint16_t* v, int64_t rd, int interleave, const float* row) {
+  for (int64_t i = 0; i < rd / 2; ++i) {
+    int64_t ix = interleave ? 2 * i : i, iy = interleave ? 2 * i + 1 : i + rd / 2;
+    double c = row[i], s = row[rd / 2 + i];
+    double x = bf2f(v[ix]), y = bf2f(v[iy]);
+    v[ix] = d2bf(x * c - y * s);
+    v[iy] = d2bf(x * s + y * c);
+  }
+}
+
+void oracle_rope_cs(uint16_t* q, int64_t q_ts, int64_t q_hs, uint16_t* k, int64_t k_ts, int64_t k_hs,
+                    const int32_t* pos, int64_t T, int64_t Hq, int64_t Hkv, int64_t rd,
+                    int interleave, const float* cs, int64_t rows, int64_t ld) {
+  for (int64_t t = 0; t < T; ++t) {
+    if (pos[t] < 0 || pos[t] >= rows) continue;
+    const float* row = cs + (int64_t)pos[t] * ld;
+    for (int64_t h = 0; h < Hq; ++h) rope_head_cs(q + t * q_ts + h * q_hs, rd, interleave, row);
+    for (int64_t h = 0; h < Hkv; ++h) rope_head_cs(k + t * k_ts + h * k_hs, rd, interleave, row);
   }
 }
 

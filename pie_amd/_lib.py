@@ -21,6 +21,14 @@ SIGNATURES: dict[str, list] = {
     "pie_hip_abi_version": [],
     "pie_hip_rmsnorm": [vp, i64, vp, vp, i64, i64, i64, f32, vp],
     "pie_hip_fused_add_rmsnorm": [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, i64, f32, vp],
+    "pie_hip_gemma_rmsnorm": [vp, i64, vp, vp, i64, i64, i64, f32, vp],
+    "pie_hip_gemma_fused_add_rmsnorm": [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, i64, f32, vp],
+    "pie_hip_gemma_qk_rmsnorm": [vp, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64, i64, vp, vp,
+                                 i64, i64, i64, i64, f32, vp],
+    "pie_hip_gelu_tanh_and_mul": [vp, i64, vp, i64, i64, i64, vp],
+    "pie_hip_embedding_scaled": [vp, i64, vp, i64, i64, i64, vp, i64, f32, vp],
+    "pie_hip_rope_cos_sin_cache_inplace": [vp, i64, i64, vp, i64, i64, vp, i64, i64, i64, i64, i32,
+                                           vp, i64, i64, i64, vp],
     "pie_hip_qk_rmsnorm": [vp, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64, i64, vp, vp,
                            i64, i64, i64, i64, f32, vp],
     "pie_hip_silu_and_mul": [vp, i64, vp, i64, i64, i64, vp],

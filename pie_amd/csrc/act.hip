@@ -17,6 +17,19 @@
 namespace pie {
 namespace {
 
+enum { kSilu = 0, kGeluTanh = 1 };
+
+// GELU with the tanh approximation (torch.nn.functional.gelu(x, approximate="tanh"), used by
+// gemma2.py:224-226 / gemma3.py:246-248): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))),
+// tanh(u) = 1 - 2 / (1 + e^{2u}) with the hardware exp2 and reciprocal; rounded to bf16 like
+// torch's bf16 gelu output before the multiply.
+__device__ __forceinline__ float gelu_tanh_bf(float x) {
+  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  const float e = __builtin_amdgcn_exp2f(2.0f * 1.44269504088896341f * u);
+  const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+  return round_bf(0.5f * x * (1.0f + th));
+}
+
 __device__ __forceinline__ float silu_bf(float g) {
   // exp(-g) via the hardware base-2 exponential; 1/(1+e) via the hardware reciprocal.
   const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
@@ -34,7 +47,7 @@ struct SiluArgs {
 // Flattened over all 16-byte output vectors: block b owns vectors [b*256*U, (b+1)*256*U), thread
 // t handles b*256*U + t + 256*i for i < U, so every wave instruction covers 1 KiB contiguous
 // (rows split only at row ends) and small row counts still spread over the whole chip.
-template <int U>
+template <int U, int ACT>
 __global__ __launch_bounds__(256) void silu_and_mul_vec(SiluArgs a) {
   const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
   uint4 gv[U], uv[U];
@@ -57,18 +70,19 @@ __global__ __launch_bounds__(256) void silu_and_mul_vec(SiluArgs a) {
       unpack8(gv[i], gf);
       unpack8(uv[i], uf);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) gf[e] = silu_bf(gf[e]) * uf[e];
+      for (int e = 0; e < 8; ++e) gf[e] = (ACT == kSilu ? silu_bf(gf[e]) : gelu_tanh_bf(gf[e])) * uf[e];
       st_nt(a.out + orow[i], pack8(gf));
     }
   }
 }
 
+template <int ACT>
 __global__ __launch_bounds__(256) void silu_and_mul_scalar(SiluArgs a) {
   for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
     const uint16_t* g = a.in + row * a.in_rs;
     uint16_t* o = a.out + row * a.out_rs;
     for (int64_t c = threadIdx.x; c < a.I; c += 256)
-      o[c] = to_bf1(silu_bf(bf1(g[c])) * bf1(g[a.I + c]));
+      o[c] = to_bf1((ACT == kSilu ? silu_bf(bf1(g[c])) : gelu_tanh_bf(bf1(g[c]))) * bf1(g[a.I + c]));
   }
 }
 
@@ -77,9 +91,11 @@ __global__ __launch_bounds__(256) void silu_and_mul_scalar(SiluArgs a) {
 
 using namespace pie;
 
-extern "C" int pie_hip_silu_and_mul(const pie_bf16* gate_up, int64_t in_row_stride, pie_bf16* out,
-                                    int64_t out_row_stride, int64_t rows, int64_t I, void* stream) {
-  PIE_REQUIRE(rows >= 0 && I >= 0, "silu_and_mul: bad shape rows=%lld I=%lld", (long long)rows, (long long)I);
+namespace {
+template <int ACT>
+int act_and_mul(const pie_bf16* gate_up, int64_t in_row_stride, pie_bf16* out,
+                int64_t out_row_stride, int64_t rows, int64_t I, void* stream) {
+  PIE_REQUIRE(rows >= 0 && I >= 0, "act_and_mul: bad shape rows=%lld I=%lld", (long long)rows, (long long)I);
   if (rows == 0 || I == 0) return PIE_HIP_OK;
   PIE_REQUIRE(gate_up && out, "silu_and_mul: null pointer");
   PIE_REQUIRE(in_row_stride >= 2 * I && out_row_stride >= I, "silu_and_mul: row stride too small");
@@ -93,12 +109,24 @@ extern "C" int pie_hip_silu_and_mul(const pie_bf16* gate_up, int64_t in_row_stri
     a.vpr = FastDiv::make((uint32_t)(I / 8));
     // One 16-byte vector per thread over a grid of nvec/256 blocks: measured fastest on MI355X
     // (configuration 2 steady state: 6.46 TB/s, against 6.25 with 2 and 5.99 with 4 vectors).
-    hipLaunchKernelGGL(silu_and_mul_vec<1>, dim3((unsigned)((nvec + 255) / 256)), blk, 0,
+    hipLaunchKernelGGL((silu_and_mul_vec<1, ACT>), dim3((unsigned)((nvec + 255) / 256)), blk, 0,
                        (hipStream_t)stream, a);
   } else {
     const int64_t cap = (int64_t)num_cus() * 64;
-    hipLaunchKernelGGL(silu_and_mul_scalar, dim3((unsigned)(rows < cap ? rows : cap)), blk, 0,
+    hipLaunchKernelGGL(silu_and_mul_scalar<ACT>, dim3((unsigned)(rows < cap ? rows : cap)), blk, 0,
                        (hipStream_t)stream, a);
   }
-  return check_launch("silu_and_mul");
+  return check_launch(ACT == kSilu ? "silu_and_mul" : "gelu_tanh_and_mul");
+}
+}  // namespace
+
+extern "C" int pie_hip_silu_and_mul(const pie_bf16* gate_up, int64_t in_row_stride, pie_bf16* out,
+                                    int64_t out_row_stride, int64_t rows, int64_t I, void* stream) {
+  return act_and_mul<kSilu>(gate_up, in_row_stride, out, out_row_stride, rows, I, stream);
+}
+
+extern "C" int pie_hip_gelu_tanh_and_mul(const pie_bf16* gate_up, int64_t in_row_stride,
+                                         pie_bf16* out, int64_t out_row_stride, int64_t rows,
+                                         int64_t I, void* stream) {
+  return act_and_mul<kGeluTanh>(gate_up, in_row_stride, out, out_row_stride, rows, I, stream);
 }

@@ -21,12 +21,13 @@ struct EmbedArgs {
   int64_t T, V, H, w_rs, out_rs;
   uint32_t nvec;  // T * H / 8 (vector path)
   FastDiv vpr;    // H / 8 vectors per row
+  float scale;    // SCALE: out = bf16(f32(W[id]) * scale)
 };
 
 // Flattened over the 16-byte vectors of the output: thread t of block b copies vectors
 // b*256*U + t + 256*i (i < U). All U table loads are issued before any store. The id of a
 // vector's token is re-read per vector (an L1 hit); ids outside [0, V) give zero rows.
-template <int U>
+template <int U, bool SCALE>
 __global__ __launch_bounds__(256) void embed_vec(EmbedArgs a) {
   const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
   uint4 v[U];
@@ -44,10 +45,20 @@ __global__ __launch_bounds__(256) void embed_vec(EmbedArgs a) {
     }
   }
 #pragma unroll
-  for (int i = 0; i < U; ++i)
-    if (dst[i] >= 0) st_nt(a.out + dst[i], v[i]);
+  for (int i = 0; i < U; ++i) {
+    if (dst[i] < 0) continue;
+    if constexpr (SCALE) {
+      float f[8];
+      unpack8(v[i], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] *= a.scale;
+      v[i] = pack8(f);
+    }
+    st_nt(a.out + dst[i], v[i]);
+  }
 }
 
+template <bool SCALE>
 __global__ __launch_bounds__(256) void embed_scalar(EmbedArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
@@ -55,7 +66,10 @@ __global__ __launch_bounds__(256) void embed_scalar(EmbedArgs a) {
     const int id = a.ids[t];
     uint16_t* o = a.out + t * a.out_rs;
     const bool ok = id >= 0 && (int64_t)id < a.V;
-    for (int64_t c = lane; c < a.H; c += 64) o[c] = ok ? a.W[(int64_t)id * a.w_rs + c] : 0;
+    for (int64_t c = lane; c < a.H; c += 64) {
+      const uint16_t v = ok ? a.W[(int64_t)id * a.w_rs + c] : 0;
+      o[c] = SCALE ? to_bf1(bf1(v) * a.scale) : v;
+    }
   }
 }
 
@@ -64,14 +78,16 @@ __global__ __launch_bounds__(256) void embed_scalar(EmbedArgs a) {
 
 using namespace pie;
 
-extern "C" int pie_hip_embedding(const int32_t* ids, int64_t T, const pie_bf16* W, int64_t V,
-                                 int64_t H, int64_t w_row_stride, pie_bf16* out,
-                                 int64_t out_row_stride, void* stream) {
+namespace {
+template <bool SCALE>
+int embedding_impl(const int32_t* ids, int64_t T, const pie_bf16* W, int64_t V, int64_t H,
+                   int64_t w_row_stride, pie_bf16* out, int64_t out_row_stride, float scale,
+                   void* stream) {
   PIE_REQUIRE(T >= 0 && V >= 0 && H >= 0, "embedding: bad shape");
   if (T == 0 || H == 0) return PIE_HIP_OK;
   PIE_REQUIRE(ids && out && (W || V == 0), "embedding: null pointer");
   PIE_REQUIRE(w_row_stride >= H && out_row_stride >= H, "embedding: row stride smaller than H");
-  EmbedArgs a{ids, W, out, T, V, H, w_row_stride, out_row_stride, 0, FastDiv{}};
+  EmbedArgs a{ids, W, out, T, V, H, w_row_stride, out_row_stride, 0, FastDiv{}, scale};
   const dim3 blk(256);
   const hipStream_t st = (hipStream_t)stream;
   const int64_t nvec = T * (H / 8);
@@ -82,10 +98,23 @@ extern "C" int pie_hip_embedding(const int32_t* ids, int64_t T, const pie_bf16* 
     a.vpr = FastDiv::make((uint32_t)(H / 8));
     // One 16-byte vector per thread (configuration 4 steady state: 6.29 TB/s, against 6.27
     // with 2 and 5.98 with 4 vectors per thread).
-    hipLaunchKernelGGL(embed_vec<1>, dim3((unsigned)((nvec + 255) / 256)), blk, 0, st, a);
+    hipLaunchKernelGGL((embed_vec<1, SCALE>), dim3((unsigned)((nvec + 255) / 256)), blk, 0, st, a);
   } else {
     const int64_t blocks = (T + 3) / 4, cap = (int64_t)num_cus() * 64;
-    hipLaunchKernelGGL(embed_scalar, dim3((unsigned)(blocks < cap ? blocks : cap)), blk, 0, st, a);
+    hipLaunchKernelGGL(embed_scalar<SCALE>, dim3((unsigned)(blocks < cap ? blocks : cap)), blk, 0, st, a);
   }
-  return check_launch("embedding");
+  return check_launch(SCALE ? "embedding_scaled" : "embedding");
+}
+}  // namespace
+
+extern "C" int pie_hip_embedding(const int32_t* ids, int64_t T, const pie_bf16* W, int64_t V,
+                                 int64_t H, int64_t w_row_stride, pie_bf16* out,
+                                 int64_t out_row_stride, void* stream) {
+  return embedding_impl<false>(ids, T, W, V, H, w_row_stride, out, out_row_stride, 1.0f, stream);
+}
+
+extern "C" int pie_hip_embedding_scaled(const int32_t* ids, int64_t T, const pie_bf16* W, int64_t V,
+                                        int64_t H, int64_t w_row_stride, pie_bf16* out,
+                                        int64_t out_row_stride, float scale, void* stream) {
+  return embedding_impl<true>(ids, T, W, V, H, w_row_stride, out, out_row_stride, scale, stream);
 }

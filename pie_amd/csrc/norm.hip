@@ -39,6 +39,24 @@ struct NormArgs {
   float eps;
 };
 
+// Normalisation rules. Standard: torch's rms_norm (one rounding at the end):
+//   y = bf16((x * rsqrt(mean(x^2) + eps)) * w)
+// Gemma (pie/src/pie_worker/model/gemma2.py:514-526, gemma3.py:491-510): the expression
+//   variance = x.pow(2).mean(-1); x * rsqrt(variance + eps) * (1.0 + weight)
+// evaluated as separate bf16 torch ops, i.e. rounded to bf16 after every step.
+template <bool GEMMA>
+__device__ __forceinline__ float nsq(float x) { return GEMMA ? round_bf(x * x) : x * x; }
+template <bool GEMMA>
+__device__ __forceinline__ float nscale(float tot, float cols, float eps) {
+  if constexpr (GEMMA) return round_bf(rsqrtf(round_bf(round_bf(tot / cols) + eps)));
+  return rsqrtf(tot / cols + eps);
+}
+template <bool GEMMA>
+__device__ __forceinline__ float napply(float x, float r, float w) {
+  if constexpr (GEMMA) return round_bf(x * r) * round_bf(1.0f + w);
+  return (x * r) * w;
+}
+
 __device__ __forceinline__ void row_offsets(const RowSet& s, int64_t r, int64_t& oi, int64_t& orr,
                                             int64_t& os, int64_t& oo) {
   int64_t t = r, h = 0;
@@ -65,7 +83,7 @@ constexpr int kRowsPerGroup = 1;
 // of wave g in the group owns vectors j*64*W + g*64 + l. W = 1 for long row lists (no barrier);
 // W > 1 spreads short lists (decode batches) over the chip, combining the W partial sums of
 // squares through LDS in a fixed order. The weight row stays in registers across rows.
-template <int VPL, int RPG, bool ADD>
+template <int VPL, int RPG, bool ADD, bool GEMMA>
 __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
   __shared__ float part[RPG][8];
   const RowSet& s = a.set[0];
@@ -119,7 +137,7 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
           float xf[8];
           unpack8(xv[k][j], xf);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) ss[k] += xf[e] * xf[e];
+          for (int e = 0; e < 8; ++e) ss[k] += nsq<GEMMA>(xf[e]);
         }
       }
     }
@@ -142,14 +160,14 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
 #pragma unroll
     for (int k = 0; k < RPG; ++k) {
       if (!live[k]) continue;
-      const float rstd = rsqrtf(tot[k] / (float)a.cols + a.eps);
+      const float rstd = nscale<GEMMA>(tot[k], (float)a.cols, a.eps);
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
         float xf[8], wf[8];
         unpack8(xv[k][j], xf);
         unpack8(wv[j], wf);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xf[e] = (xf[e] * rstd) * wf[e];
+        for (int e = 0; e < 8; ++e) xf[e] = napply<GEMMA>(xf[e], rstd, wf[e]);
         st16(s.out + oo[k] + (int64_t)(v0 + j * vstep) * 8, pack8(xf));
       }
     }
@@ -185,7 +203,7 @@ struct Chunk<16> {
   __device__ void set(const float* f) { v0 = pack8(f); v1 = pack8(f + 8); }
 };
 
-template <int EPL>
+template <int EPL, bool GEMMA>
 __global__ __launch_bounds__(256) void rmsnorm_heads16(NormArgs a) {
   const int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;  // 16-lane group
   const int sub = threadIdx.x & 15;
@@ -211,10 +229,10 @@ __global__ __launch_bounds__(256) void rmsnorm_heads16(NormArgs a) {
   }
   float ss = 0.f;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) ss += f[e] * f[e];
-  const float rstd = rsqrtf(row16_sum(ss) / (float)a.cols + a.eps);
+  for (int e = 0; e < EPL; ++e) ss += nsq<GEMMA>(f[e]);
+  const float rstd = nscale<GEMMA>(row16_sum(ss), (float)a.cols, a.eps);
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) f[e] = (f[e] * rstd) * wf[e];
+  for (int e = 0; e < EPL; ++e) f[e] = napply<GEMMA>(f[e], rstd, wf[e]);
   if (live) {
     c.set(f);
     c.store(s.out + oo + sub * EPL);
@@ -224,7 +242,7 @@ __global__ __launch_bounds__(256) void rmsnorm_heads16(NormArgs a) {
 // ---------------------------------------------------------------- generic: one wave per row
 // VEC = 8: 16-byte accesses (cols % 8 == 0, all rows 16-byte aligned); VEC = 1: scalar.
 // Pass 1 reads the row (and writes s), pass 2 re-reads it from cache and writes y.
-template <int VEC, bool ADD>
+template <int VEC, bool ADD, bool GEMMA>
 __global__ __launch_bounds__(256) void rmsnorm_rows_generic(NormArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t wave0 = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -262,19 +280,19 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_generic(NormArgs a) {
         }
       }
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) ss += f[e] * f[e];
+      for (int e = 0; e < VEC; ++e) ss += nsq<GEMMA>(f[e]);
     }
-    const float rstd = rsqrtf(wave_sum(ss) / (float)a.cols + a.eps);
+    const float rstd = nscale<GEMMA>(wave_sum(ss), (float)a.cols, a.eps);
     for (int64_t j = lane; j < nv; j += 64) {
       if constexpr (VEC == 8) {
         float f[8], wf[8];
         unpack8(ld16(src + j * 8), f);
         unpack8(ld16(s.w + j * 8), wf);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = (f[e] * rstd) * wf[e];
+        for (int e = 0; e < 8; ++e) f[e] = napply<GEMMA>(f[e], rstd, wf[e]);
         st16(s.out + oo + j * 8, pack8(f));
       } else {
-        s.out[oo + j] = to_bf1((bf1(src[j]) * rstd) * bf1(s.w[j]));
+        s.out[oo + j] = to_bf1(napply<GEMMA>(bf1(src[j]), rstd, bf1(s.w[j])));
       }
     }
   }
@@ -298,7 +316,7 @@ bool rowset_vec_ok(const RowSet& s, bool add) {
   return ok;
 }
 
-template <bool ADD>
+template <bool ADD, bool GEMMA>
 int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
   const int64_t rows = a.set[0].rows + a.set[1].rows;
   if (rows == 0) return PIE_HIP_OK;
@@ -329,7 +347,7 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
       const dim3 grd((unsigned)blocks), tb(threads);
       switch (n512 / W) {
 #define PIE_NV(n) \
-  case n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, kRowsPerGroup, ADD>), grd, tb, 0, st, a, W); break;
+  case n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, kRowsPerGroup, ADD, GEMMA>), grd, tb, 0, st, a, W); break;
         PIE_NV(1) PIE_NV(2) PIE_NV(3) PIE_NV(4) PIE_NV(5) PIE_NV(6) PIE_NV(7) PIE_NV(8)
         PIE_NV(9) PIE_NV(10) PIE_NV(11) PIE_NV(12)
 #undef PIE_NV
@@ -340,14 +358,14 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
   if (!ADD && vec && (a.cols == 64 || a.cols == 128 || a.cols == 256)) {
     const int64_t threads = rows * 16;
     const dim3 grd((unsigned)((threads + 255) / 256));
-    if (a.cols == 64) hipLaunchKernelGGL(rmsnorm_heads16<4>, grd, blk, 0, st, a);
-    else if (a.cols == 128) hipLaunchKernelGGL(rmsnorm_heads16<8>, grd, blk, 0, st, a);
-    else hipLaunchKernelGGL(rmsnorm_heads16<16>, grd, blk, 0, st, a);
+    if (a.cols == 64) hipLaunchKernelGGL((rmsnorm_heads16<4, GEMMA>), grd, blk, 0, st, a);
+    else if (a.cols == 128) hipLaunchKernelGGL((rmsnorm_heads16<8, GEMMA>), grd, blk, 0, st, a);
+    else hipLaunchKernelGGL((rmsnorm_heads16<16, GEMMA>), grd, blk, 0, st, a);
     return check_launch(name);
   }
   const dim3 grd((unsigned)wave_grid(rows));
-  if (vec) hipLaunchKernelGGL((rmsnorm_rows_generic<8, ADD>), grd, blk, 0, st, a);
-  else hipLaunchKernelGGL((rmsnorm_rows_generic<1, ADD>), grd, blk, 0, st, a);
+  if (vec) hipLaunchKernelGGL((rmsnorm_rows_generic<8, ADD, GEMMA>), grd, blk, 0, st, a);
+  else hipLaunchKernelGGL((rmsnorm_rows_generic<1, ADD, GEMMA>), grd, blk, 0, st, a);
   return check_launch(name);
 }
 
@@ -356,9 +374,10 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
 
 using namespace pie;
 
-extern "C" int pie_hip_rmsnorm(const pie_bf16* x, int64_t x_row_stride, const pie_bf16* w,
-                               pie_bf16* y, int64_t y_row_stride, int64_t rows, int64_t cols,
-                               float eps, void* stream) {
+namespace {
+template <bool GEMMA>
+int rmsnorm_impl(const pie_bf16* x, int64_t x_row_stride, const pie_bf16* w, pie_bf16* y,
+                 int64_t y_row_stride, int64_t rows, int64_t cols, float eps, void* stream) {
   PIE_REQUIRE(rows >= 0 && cols > 0, "rmsnorm: bad shape rows=%lld cols=%lld", (long long)rows, (long long)cols);
   if (rows == 0) return PIE_HIP_OK;
   PIE_REQUIRE(x && w && y, "rmsnorm: null pointer");
@@ -367,15 +386,14 @@ extern "C" int pie_hip_rmsnorm(const pie_bf16* x, int64_t x_row_stride, const pi
   a.set[0] = RowSet{x, nullptr, nullptr, y, w, x_row_stride, 0, 0, 0, 0, 0, y_row_stride, 0, 1, rows};
   a.cols = cols;
   a.eps = eps;
-  return launch_rows<false>(a, (hipStream_t)stream, "rmsnorm");
+  return launch_rows<false, GEMMA>(a, (hipStream_t)stream, GEMMA ? "gemma_rmsnorm" : "rmsnorm");
 }
 
-extern "C" int pie_hip_fused_add_rmsnorm(const pie_bf16* x, int64_t x_row_stride,
-                                         const pie_bf16* r, int64_t r_row_stride,
-                                         pie_bf16* s, int64_t s_row_stride,
-                                         pie_bf16* y, int64_t y_row_stride,
-                                         const pie_bf16* w, int64_t rows, int64_t cols,
-                                         float eps, void* stream) {
+template <bool GEMMA>
+int add_rmsnorm_impl(const pie_bf16* x, int64_t x_row_stride, const pie_bf16* r,
+                     int64_t r_row_stride, pie_bf16* s, int64_t s_row_stride, pie_bf16* y,
+                     int64_t y_row_stride, const pie_bf16* w, int64_t rows, int64_t cols, float eps,
+                     void* stream) {
   PIE_REQUIRE(rows >= 0 && cols > 0, "fused_add_rmsnorm: bad shape rows=%lld cols=%lld", (long long)rows, (long long)cols);
   if (rows == 0) return PIE_HIP_OK;
   PIE_REQUIRE(x && r && s && y && w, "fused_add_rmsnorm: null pointer");
@@ -385,15 +403,16 @@ extern "C" int pie_hip_fused_add_rmsnorm(const pie_bf16* x, int64_t x_row_stride
   a.set[0] = RowSet{x, r, s, y, w, x_row_stride, 0, r_row_stride, 0, s_row_stride, 0, y_row_stride, 0, 1, rows};
   a.cols = cols;
   a.eps = eps;
-  return launch_rows<true>(a, (hipStream_t)stream, "fused_add_rmsnorm");
+  return launch_rows<true, GEMMA>(a, (hipStream_t)stream, GEMMA ? "gemma_fused_add_rmsnorm" : "fused_add_rmsnorm");
 }
 
-extern "C" int pie_hip_qk_rmsnorm(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
-                                  pie_bf16* q_out, int64_t qo_tok_stride, int64_t qo_head_stride,
-                                  const pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
-                                  pie_bf16* k_out, int64_t ko_tok_stride, int64_t ko_head_stride,
-                                  const pie_bf16* qw, const pie_bf16* kw, int64_t T, int64_t Hq,
-                                  int64_t Hkv, int64_t D, float eps, void* stream) {
+template <bool GEMMA>
+int qk_rmsnorm_impl(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride, pie_bf16* q_out,
+                    int64_t qo_tok_stride, int64_t qo_head_stride, const pie_bf16* k,
+                    int64_t k_tok_stride, int64_t k_head_stride, pie_bf16* k_out,
+                    int64_t ko_tok_stride, int64_t ko_head_stride, const pie_bf16* qw,
+                    const pie_bf16* kw, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, float eps,
+                    void* stream) {
   PIE_REQUIRE(T >= 0 && Hq >= 0 && Hkv >= 0 && D > 0, "qk_rmsnorm: bad shape");
   if (T == 0 || Hq + Hkv == 0) return PIE_HIP_OK;
   PIE_REQUIRE(Hq == 0 || (q && q_out && qw), "qk_rmsnorm: null q pointer");
@@ -406,5 +425,58 @@ extern "C" int pie_hip_qk_rmsnorm(const pie_bf16* q, int64_t q_tok_stride, int64
   if (Hq == 0) { a.set[0] = a.set[1]; a.set[1] = RowSet{}; }
   a.cols = D;
   a.eps = eps;
-  return launch_rows<false>(a, (hipStream_t)stream, "qk_rmsnorm");
+  return launch_rows<false, GEMMA>(a, (hipStream_t)stream, GEMMA ? "gemma_qk_rmsnorm" : "qk_rmsnorm");
 }
+}  // namespace
+
+#define PIE_NORM_ARGS x, x_row_stride, w, y, y_row_stride, rows, cols, eps, stream
+extern "C" int pie_hip_rmsnorm(const pie_bf16* x, int64_t x_row_stride, const pie_bf16* w,
+                               pie_bf16* y, int64_t y_row_stride, int64_t rows, int64_t cols,
+                               float eps, void* stream) {
+  return rmsnorm_impl<false>(PIE_NORM_ARGS);
+}
+extern "C" int pie_hip_gemma_rmsnorm(const pie_bf16* x, int64_t x_row_stride, const pie_bf16* w,
+                                     pie_bf16* y, int64_t y_row_stride, int64_t rows, int64_t cols,
+                                     float eps, void* stream) {
+  return rmsnorm_impl<true>(PIE_NORM_ARGS);
+}
+#undef PIE_NORM_ARGS
+
+#define PIE_ADD_ARGS x, x_row_stride, r, r_row_stride, s, s_row_stride, y, y_row_stride, w, rows, cols, eps, stream
+extern "C" int pie_hip_fused_add_rmsnorm(const pie_bf16* x, int64_t x_row_stride,
+                                         const pie_bf16* r, int64_t r_row_stride,
+                                         pie_bf16* s, int64_t s_row_stride,
+                                         pie_bf16* y, int64_t y_row_stride,
+                                         const pie_bf16* w, int64_t rows, int64_t cols,
+                                         float eps, void* stream) {
+  return add_rmsnorm_impl<false>(PIE_ADD_ARGS);
+}
+extern "C" int pie_hip_gemma_fused_add_rmsnorm(const pie_bf16* x, int64_t x_row_stride,
+                                               const pie_bf16* r, int64_t r_row_stride,
+                                               pie_bf16* s, int64_t s_row_stride,
+                                               pie_bf16* y, int64_t y_row_stride,
+                                               const pie_bf16* w, int64_t rows, int64_t cols,
+                                               float eps, void* stream) {
+  return add_rmsnorm_impl<true>(PIE_ADD_ARGS);
+}
+#undef PIE_ADD_ARGS
+
+#define PIE_QK_ARGS q, q_tok_stride, q_head_stride, q_out, qo_tok_stride, qo_head_stride, k, \
+    k_tok_stride, k_head_stride, k_out, ko_tok_stride, ko_head_stride, qw, kw, T, Hq, Hkv, D, eps, stream
+extern "C" int pie_hip_qk_rmsnorm(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                  pie_bf16* q_out, int64_t qo_tok_stride, int64_t qo_head_stride,
+                                  const pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                                  pie_bf16* k_out, int64_t ko_tok_stride, int64_t ko_head_stride,
+                                  const pie_bf16* qw, const pie_bf16* kw, int64_t T, int64_t Hq,
+                                  int64_t Hkv, int64_t D, float eps, void* stream) {
+  return qk_rmsnorm_impl<false>(PIE_QK_ARGS);
+}
+extern "C" int pie_hip_gemma_qk_rmsnorm(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                        pie_bf16* q_out, int64_t qo_tok_stride, int64_t qo_head_stride,
+                                        const pie_bf16* k, int64_t k_tok_stride, int64_t k_head_stride,
+                                        pie_bf16* k_out, int64_t ko_tok_stride, int64_t ko_head_stride,
+                                        const pie_bf16* qw, const pie_bf16* kw, int64_t T, int64_t Hq,
+                                        int64_t Hkv, int64_t D, float eps, void* stream) {
+  return qk_rmsnorm_impl<true>(PIE_QK_ARGS);
+}
+#undef PIE_QK_ARGS

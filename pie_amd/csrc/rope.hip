@@ -62,7 +62,24 @@ struct RopeAppendArgs {
   int32_t wpt;         // waves per token (vector kernel)
   int32_t interleave;  // pair layout (scalar kernel)
   float inv_freq[kMaxPairs];
+  // Precomputed table instead of inv_freq (flashinfer's apply_rope_with_cos_sin_cache_inplace):
+  // row p holds cos(angle_i) at [i] and sin(angle_i) at [rd/2 + i]; positions outside
+  // [0, cs_rows) rotate by the identity.
+  const float* cs;
+  int64_t cs_rows, cs_ld;
 };
+
+// cos/sin of pair i at position p: from the table when one is given, else from inv_freq.
+__device__ __forceinline__ float2 rope_cs(const RopeAppendArgs& a, int p, int i, int half) {
+  if (a.cs) {
+    if (p < 0 || (int64_t)p >= a.cs_rows) return make_float2(1.f, 0.f);
+    const float* row = a.cs + (int64_t)p * a.cs_ld;
+    return make_float2(row[i], row[half + i]);
+  }
+  float sn, cs;
+  sincosf((float)p * a.inv_freq[i], &sn, &cs);
+  return make_float2(cs, sn);
+}
 
 
 // The rotation with its fused multiply-adds spelled out, so every kernel variant (rope only,
@@ -164,20 +181,15 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   UnitBatch<UB> b;
   // Latency order: the position, the first batch of data and the page lookup chain are all
   // requested before the cos/sin table is computed, so they overlap it.
-  const float p = ROPE ? (float)a.pos[tq] : 0.f;
+  const int p = ROPE ? a.pos[tq] : 0;
   load_units<ROPE, APPEND, INTERLEAVE, UB>(b, g, gt);
   int64_t kc = -1;
   if constexpr (APPEND) {
     if (live) kc = slot_offset(cd, tq);
   }
   if constexpr (ROPE) {
-    if (live) {
-      for (int i = gt; i < half; i += gsize) {
-        float sn, cs;
-        sincosf(p * a.inv_freq[i], &sn, &cs);
-        tab[slot][i] = make_float2(cs, sn);
-      }
-    }
+    if (live)
+      for (int i = gt; i < half; i += gsize) tab[slot][i] = rope_cs(a, p, i, half);
     __syncthreads();
   }
   if (!live) return;
@@ -408,10 +420,8 @@ __global__ __launch_bounds__(256) void rope_scalar(RopeAppendArgs a) {
                                  : h.k + t * h.k_ts + (int64_t)(head - h.Hq) * h.k_hs;
     uint16_t* px = base + (a.interleave ? 2 * pr : pr);
     uint16_t* py = base + (a.interleave ? 2 * pr + 1 : pr + half);
-    float sn, cs;
-    sincosf((float)a.pos[t] * a.inv_freq[pr], &sn, &cs);
+    const float2 csn = rope_cs(a, a.pos[t], pr, half);
     const float x = bf1(*px), y = bf1(*py);
-    const float2 csn = make_float2(cs, sn);
     *px = to_bf1(rot_x(x, y, csn));
     *py = to_bf1(rot_y(x, y, csn));
   }
@@ -663,4 +673,26 @@ extern "C" int pie_hip_qk_rmsnorm_rope_append(
   hipLaunchKernelGGL(qk_norm_rope_append_d128, dim3((unsigned)((T + tpb - 1) / tpb)), dim3(threads), 0,
                      (hipStream_t)stream, qa);
   return check_launch("qk_rmsnorm_rope_append");
+}
+
+extern "C" int pie_hip_rope_cos_sin_cache_inplace(pie_bf16* q, int64_t q_tok_stride,
+                                                  int64_t q_head_stride, pie_bf16* k,
+                                                  int64_t k_tok_stride, int64_t k_head_stride,
+                                                  const int32_t* pos, int64_t T, int64_t Hq,
+                                                  int64_t Hkv, int64_t D, int interleave,
+                                                  const float* cos_sin_cache, int64_t cache_rows,
+                                                  int64_t rotary_dim, int64_t cache_ld,
+                                                  void* stream) {
+  RopeAppendArgs a{};
+  int rc = fill_heads(a, q, q_tok_stride, q_head_stride, k, k_tok_stride, k_head_stride, nullptr,
+                      0, 0, T, Hq, Hkv, D, rotary_dim);
+  if (rc) return rc;
+  if (T == 0 || Hq + Hkv == 0 || rotary_dim == 0) return PIE_HIP_OK;
+  PIE_REQUIRE(pos && cos_sin_cache && (Hq == 0 || q) && (Hkv == 0 || k), "rope_cos_sin_cache: null pointer");
+  PIE_REQUIRE(cache_rows >= 0 && cache_ld >= rotary_dim, "rope_cos_sin_cache: bad cache shape");
+  a.pos = pos;
+  a.cs = cos_sin_cache;
+  a.cs_rows = cache_rows;
+  a.cs_ld = cache_ld;
+  return launch(a, true, false, interleave ? 1 : 0, (hipStream_t)stream, "rope_cos_sin_cache");
 }

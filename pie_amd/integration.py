@@ -19,7 +19,8 @@ import types
 
 from . import ops
 
-# flashinfer names this package serves (the calls at llama3.py:660-755, qwen3.py:665-684).
+# flashinfer names this package serves (the calls at llama3.py:660-755, qwen3.py:665-684,
+# gemma2.py:608, gpt_oss.py:671-678).
 HOT_PATH = (
     "apply_rope_pos_ids_inplace",
     "apply_llama31_rope_pos_ids_inplace",
@@ -29,6 +30,8 @@ HOT_PATH = (
     "rmsnorm",
     "fused_add_rmsnorm",
     "silu_and_mul",
+    "gelu_tanh_and_mul",
+    "apply_rope_with_cos_sin_cache_inplace",
 )
 
 

@@ -20,6 +20,10 @@ plus fused entries with no single reference counterpart:
     apply_{llama31_,}rope_pos_ids_and_append_paged_kv_cache   RoPE + append in one HBM pass
     qk_rms_norm_rope_append                      q/k norm + RoPE + append (qwen3.py:651-684)
 
+variant ops of the other model families (gemma2/3, gpt-oss, olmo3):
+    gemma_rms_norm, gemma_add_rms_norm, gemma_qk_rms_norm, gelu_tanh_and_mul,
+    embedding(..., scale=), apply_rope_with_cos_sin_cache_inplace
+
 Every op runs a hand-written gfx950 kernel from libpie_hip.so on the current torch stream.
 Nothing here allocates except the outputs of out-of-place ops (as the reference's torch calls
 do), nothing synchronises the host, and so every op can be captured into a HIP graph. There is
@@ -40,7 +44,8 @@ __all__ = [
     "append_paged_kv_cache", "apply_rope_pos_ids_and_append_paged_kv_cache",
     "apply_llama31_rope_pos_ids_and_append_paged_kv_cache", "get_seq_lens",
     "get_batch_indices_positions", "rope_inv_freq", "llama31_inv_freq",
-    "qk_rms_norm_rope_append",
+    "qk_rms_norm_rope_append", "gemma_rms_norm", "gemma_add_rms_norm", "gemma_qk_rms_norm",
+    "gelu_tanh_and_mul", "apply_rope_with_cos_sin_cache_inplace",
 ]
 
 _BF16 = torch.bfloat16
@@ -93,21 +98,34 @@ def rmsnorm(input: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
     Numerics follow torch's rms_norm (torch/_decomp/decompositions.py:1760-1810), the op the
     reference calls at pie/src/pie_worker/model/llama3.py:555-560.
     """
-    _check("rmsnorm", _BF16, input=input, weight=weight)
+    return _rmsnorm("rmsnorm", input, weight, eps, out, False)
+
+
+def gemma_rms_norm(input: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Gemma RMSNorm, ``x * rsqrt(x.pow(2).mean(-1) + eps) * (1.0 + weight)`` evaluated as bf16
+    torch ops (every step rounded to bf16): pie/src/pie_worker/model/gemma2.py:514-526,
+    gemma3.py:491-510 (a [T, H, D] input is normalised per head, as gemma3's _qk_norm)."""
+    return _rmsnorm("gemma_rms_norm", input, weight, eps, out, True)
+
+
+def _rmsnorm(name, input, weight, eps, out, gemma):
+    _check(name, _BF16, input=input, weight=weight)
     H = input.shape[-1]
     if weight.shape != (H,):
         raise ValueError(f"rmsnorm: weight shape {tuple(weight.shape)} != ({H},)")
     weight = weight.contiguous()
     if input.dim() == 3 and H in (64, 128, 256) and input.stride(-1) == 1:
-        return _per_head_norm(input, weight, eps, out)
-    x2 = _rows("rmsnorm", input, H)
+        return _per_head_norm(input, weight, eps, out, gemma)
+    x2 = _rows(name, input, H)
     if out is None:
         out = torch.empty(input.shape, dtype=_BF16, device=input.device)
-    y2 = _rows("rmsnorm", out, H)
+    y2 = _rows(name, out, H)
     if y2.data_ptr() != out.data_ptr():
-        raise ValueError("rmsnorm: out must be viewable as [rows, H] with unit inner stride")
-    _lib.call("pie_hip_rmsnorm", x2.data_ptr(), x2.stride(0), weight.data_ptr(), y2.data_ptr(),
-              y2.stride(0), x2.shape[0], H, C.c_float(float(eps)), _stream(input))
+        raise ValueError(f"{name}: out must be viewable as [rows, H] with unit inner stride")
+    _lib.call("pie_hip_gemma_rmsnorm" if gemma else "pie_hip_rmsnorm", x2.data_ptr(),
+              x2.stride(0), weight.data_ptr(), y2.data_ptr(), y2.stride(0), x2.shape[0], H,
+              C.c_float(float(eps)), _stream(input))
     return out
 
 
@@ -123,21 +141,28 @@ def rms_norm(input: torch.Tensor, normalized_shape: Union[int, Sequence[int]],
 
 
 def _per_head_norm(x: torch.Tensor, w: torch.Tensor, eps: float,
-                   out: Optional[torch.Tensor]) -> torch.Tensor:
+                   out: Optional[torch.Tensor], gemma: bool = False) -> torch.Tensor:
     T, H, D = x.shape
     if out is None:
         out = torch.empty((T, H, D), dtype=_BF16, device=x.device)
     if out.shape != x.shape or out.stride(-1) != 1:
         raise ValueError("rmsnorm: out must match input shape with unit inner stride")
-    _lib.call("pie_hip_qk_rmsnorm", x.data_ptr(), x.stride(0), x.stride(1), out.data_ptr(),
-              out.stride(0), out.stride(1), None, 0, 0, None, 0, 0, w.data_ptr(), None,
-              T, H, 0, D, C.c_float(float(eps)), _stream(x))
+    _lib.call("pie_hip_gemma_qk_rmsnorm" if gemma else "pie_hip_qk_rmsnorm", x.data_ptr(),
+              x.stride(0), x.stride(1), out.data_ptr(), out.stride(0), out.stride(1), None, 0, 0,
+              None, 0, 0, w.data_ptr(), None, T, H, 0, D, C.c_float(float(eps)), _stream(x))
     return out
+
+
+def gemma_qk_rms_norm(q, k, q_weight, k_weight, eps=None, q_out=None, k_out=None):
+    """Gemma3's per-head q/k norm with (1 + weight) and bf16 step rounding (gemma3.py:499-510,
+    :653-654), q and k in one launch."""
+    return qk_rms_norm(q, k, q_weight, k_weight, eps, q_out, k_out, _gemma=True)
 
 
 def qk_rms_norm(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
                 eps: Optional[float] = None, q_out: Optional[torch.Tensor] = None,
-                k_out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                k_out: Optional[torch.Tensor] = None,
+                _gemma: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """Per-head RMSNorm of q [T,Hq,D] and k [T,Hkv,D] in one launch.
 
     Replaces ``q = fun.rms_norm(q, [D], q_norm, eps); k = fun.rms_norm(k, [D], k_norm, eps)``
@@ -159,16 +184,24 @@ def qk_rms_norm(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_weig
     if q_out.shape != q.shape or k_out.shape != k.shape or q_out.stride(2) != 1 or k_out.stride(2) != 1:
         raise ValueError("qk_rms_norm: outputs must match inputs with unit inner stride")
     q_weight, k_weight = q_weight.contiguous(), k_weight.contiguous()
-    _lib.call("pie_hip_qk_rmsnorm", q.data_ptr(), q.stride(0), q.stride(1), q_out.data_ptr(),
+    _lib.call("pie_hip_gemma_qk_rmsnorm" if _gemma else "pie_hip_qk_rmsnorm", q.data_ptr(),
+              q.stride(0), q.stride(1), q_out.data_ptr(),
               q_out.stride(0), q_out.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
               k_out.data_ptr(), k_out.stride(0), k_out.stride(1), q_weight.data_ptr(),
               k_weight.data_ptr(), T, Hq, Hkv, D, C.c_float(_eps(eps)), _stream(q))
     return q_out, k_out
 
 
+def gemma_add_rms_norm(input, residual, weight, eps=None, out=None, residual_out=None):
+    """``residual + input`` then Gemma RMSNorm of the sum (gemma3.py:585 / :705 feeding the next
+    layer's _gemma_rms_norm); returns (normed, new_residual)."""
+    return add_rms_norm(input, residual, weight, eps, out, residual_out, _gemma=True)
+
+
 def add_rms_norm(input: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
                  eps: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                 residual_out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                 residual_out: Optional[torch.Tensor] = None,
+                 _gemma: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """Residual add + RMSNorm of the sum; returns (normed, new_residual).
 
     new_residual = bf16(residual + input)  -- `residual + down` at llama3.py:586 / :710
@@ -189,7 +222,8 @@ def add_rms_norm(input: torch.Tensor, residual: torch.Tensor, weight: torch.Tens
     if y2.data_ptr() != out.data_ptr() or s2.data_ptr() != residual_out.data_ptr():
         raise ValueError("add_rms_norm: outputs must be viewable as [rows, H]")
     weight = weight.contiguous()
-    _lib.call("pie_hip_fused_add_rmsnorm", x2.data_ptr(), x2.stride(0), r2.data_ptr(), r2.stride(0),
+    _lib.call("pie_hip_gemma_fused_add_rmsnorm" if _gemma else "pie_hip_fused_add_rmsnorm",
+              x2.data_ptr(), x2.stride(0), r2.data_ptr(), r2.stride(0),
               s2.data_ptr(), s2.stride(0), y2.data_ptr(), y2.stride(0), weight.data_ptr(),
               x2.shape[0], H, C.c_float(_eps(eps)), _stream(input))
     return out, residual_out
@@ -211,25 +245,38 @@ def silu_and_mul(input: torch.Tensor, out: Optional[torch.Tensor] = None) -> tor
     (pie/src/pie_worker/model/llama3.py:569-572), including torch's rounding of silu to bf16
     before the multiply.
     """
-    _check("silu_and_mul", _BF16, input=input)
+    return _act_and_mul("silu_and_mul", "pie_hip_silu_and_mul", input, out)
+
+
+def gelu_tanh_and_mul(input: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """flashinfer.activation.gelu_tanh_and_mul: ``fun.gelu(gate, approximate="tanh") * up``
+    (gemma2.py:224-226, :608; gemma3.py:246-248, :566), gelu rounded to bf16 before the
+    multiply as torch does."""
+    return _act_and_mul("gelu_tanh_and_mul", "pie_hip_gelu_tanh_and_mul", input, out)
+
+
+def _act_and_mul(name, sym, input, out):
+    _check(name, _BF16, input=input)
     if input.shape[-1] % 2:
-        raise ValueError(f"silu_and_mul: last dim {input.shape[-1]} must be even")
+        raise ValueError(f"{name}: last dim {input.shape[-1]} must be even")
     I = input.shape[-1] // 2
-    x2 = _rows("silu_and_mul", input, 2 * I)
+    x2 = _rows(name, input, 2 * I)
     if out is None:
         out = torch.empty((*input.shape[:-1], I), dtype=_BF16, device=input.device)
-    y2 = _rows("silu_and_mul", out, I)
+    y2 = _rows(name, out, I)
     if y2.data_ptr() != out.data_ptr():
-        raise ValueError("silu_and_mul: out must be viewable as [rows, I]")
-    _lib.call("pie_hip_silu_and_mul", x2.data_ptr(), x2.stride(0), y2.data_ptr(), y2.stride(0),
-              x2.shape[0], I, _stream(input))
+        raise ValueError(f"{name}: out must be viewable as [rows, I]")
+    _lib.call(sym, x2.data_ptr(), x2.stride(0), y2.data_ptr(), y2.stride(0), x2.shape[0], I,
+              _stream(input))
     return out
 
 
 # ----------------------------------------------------------------------------- embedding
 def embedding(input: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Tensor] = None,
-              check_ids: bool = False) -> torch.Tensor:
+              check_ids: bool = False, scale: Optional[float] = None) -> torch.Tensor:
     """fun.embedding(ids, W) for int32 ids and a bf16 table (llama3.py:471): a bit copy.
+    With ``scale``: ``fun.embedding(ids, W) * scale`` rounded once to bf16, as gemma's
+    ``embeddings * self.embed_normalizer`` (gemma3.py:476-489; torch multiplies in fp32).
 
     The kernel writes a zero row for an id outside [0, V) (it cannot raise without a host
     sync); check_ids=True validates on the host first and raises IndexError as torch does.
@@ -248,8 +295,13 @@ def embedding(input: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Ten
     y2 = _rows("embedding", out, H)
     if y2.data_ptr() != out.data_ptr() or y2.shape[0] != T:
         raise ValueError("embedding: out must be viewable as [T, H]")
-    _lib.call("pie_hip_embedding", ids.data_ptr(), T, weight.data_ptr(), V, H, weight.stride(0),
-              y2.data_ptr(), y2.stride(0), _stream(weight))
+    if scale is None:
+        _lib.call("pie_hip_embedding", ids.data_ptr(), T, weight.data_ptr(), V, H,
+                  weight.stride(0), y2.data_ptr(), y2.stride(0), _stream(weight))
+    else:
+        _lib.call("pie_hip_embedding_scaled", ids.data_ptr(), T, weight.data_ptr(), V, H,
+                  weight.stride(0), y2.data_ptr(), y2.stride(0), C.c_float(float(scale)),
+                  _stream(weight))
     return out
 
 
@@ -329,6 +381,30 @@ def apply_llama31_rope_pos_ids_inplace(q: torch.Tensor, k: torch.Tensor, pos_ids
     _rope("apply_llama31_rope_pos_ids_inplace", q, k, pos_ids, rotary_dim, interleave,
           lambda rd: llama31_inv_freq(rd, rope_scale, rope_theta, low_freq_factor,
                                       high_freq_factor, old_context_len))
+
+
+def apply_rope_with_cos_sin_cache_inplace(positions: torch.Tensor, query: torch.Tensor,
+                                          key: torch.Tensor, head_size: int,
+                                          cos_sin_cache: torch.Tensor, is_neox: bool = True) -> None:
+    """flashinfer.apply_rope_with_cos_sin_cache_inplace (gpt_oss.py:671-678, olmo3.py:797-804):
+    query [nnz, Hq*head_size] (or [nnz, Hq, head_size]) and key likewise, rotated in place with
+    cos/sin read from ``cos_sin_cache`` [max_pos, rotary_dim] fp32 (cos in the first half, sin in
+    the second). is_neox=True pairs (i, i + rotary_dim/2), else (2i, 2i+1). Positions outside
+    the table leave their token unchanged."""
+    _check("apply_rope_with_cos_sin_cache_inplace", _BF16, query=query, key=key)
+    _check("apply_rope_with_cos_sin_cache_inplace", torch.int32, positions=positions)
+    _check("apply_rope_with_cos_sin_cache_inplace", torch.float32, cos_sin_cache=cos_sin_cache)
+    D = int(head_size)
+    q = query.view(query.shape[0], -1, D) if query.dim() == 2 else query
+    k = key.view(key.shape[0], -1, D) if key.dim() == 2 else key
+    if cos_sin_cache.dim() != 2 or cos_sin_cache.stride(1) != 1:
+        raise ValueError("apply_rope_with_cos_sin_cache_inplace: cos_sin_cache must be [max_pos, rotary_dim]")
+    rd = cos_sin_cache.shape[1]
+    T, Hq, Hkv, D, rd = _rope_shapes("apply_rope_with_cos_sin_cache_inplace", q, k, positions, rd)
+    _lib.call("pie_hip_rope_cos_sin_cache_inplace", q.data_ptr(), q.stride(0), q.stride(1),
+              k.data_ptr(), k.stride(0), k.stride(1), positions.data_ptr(), T, Hq, Hkv, D,
+              0 if is_neox else 1, cos_sin_cache.data_ptr(), cos_sin_cache.shape[0], rd,
+              cos_sin_cache.stride(0), _stream(q))
 
 
 # ----------------------------------------------------------------------------- paged KV append

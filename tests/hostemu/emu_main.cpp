@@ -2,7 +2,8 @@
 // include/hip/hip_runtime.h, on exact-size heap buffers under AddressSanitizer, and compares
 // the results with the CPU oracle (oracle/oracle.c). TEST INFRASTRUCTURE.
 //
-//   emu_main <case>    case = norm | qk | silu | embed | rope | fused | decode | index | all | big
+//   emu_main <case>    case = norm | qk | silu | embed | rope | fused | decode | index | qkfused |
+//                      variants | fastdiv | all | big
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -29,6 +30,15 @@ int64_t oracle_append(const uint16_t*, int64_t, int64_t, const uint16_t*, int64_
                       const int32_t*, const int32_t*, const int32_t*, const int32_t*, int64_t,
                       uint16_t*, uint16_t*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
                       int64_t, int64_t);
+void oracle_gemma_rmsnorm(const uint16_t*, int64_t, int64_t, const uint16_t*, uint16_t*, int64_t,
+                          int64_t, int64_t, int64_t, int64_t, double);
+void oracle_gemma_add_rmsnorm(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, uint16_t*,
+                              int64_t, int64_t, double);
+void oracle_gelu_tanh_and_mul(const uint16_t*, int64_t, uint16_t*, int64_t, int64_t);
+int64_t oracle_embedding_scaled(const int32_t*, int64_t, const uint16_t*, int64_t, int64_t, float,
+                                uint16_t*);
+void oracle_rope_cs(uint16_t*, int64_t, int64_t, uint16_t*, int64_t, int64_t, const int32_t*, int64_t,
+                    int64_t, int64_t, int64_t, int, const float*, int64_t, int64_t);
 void oracle_seq_lens(const int32_t*, const int32_t*, int64_t, int64_t, int32_t*);
 void oracle_batch_indices_positions(const int32_t*, const int32_t*, int64_t, int64_t, int32_t*, int32_t*);
 }
@@ -257,6 +267,82 @@ static void case_qk_fused(int64_t B, int64_t Hq, int64_t Hkv, int64_t D) {
   check_equal("cache fused == separate", ca.p, cb.p, ca.n);
 }
 
+// Gemma norms, GELU-tanh-and-mul, scaled embedding, RoPE from a cos/sin table.
+static void case_variants(int64_t T, int64_t H, int64_t Hq, int64_t Hkv, int64_t D, int64_t I) {
+  printf("variants T=%lld H=%lld Hq=%lld Hkv=%lld D=%lld I=%lld\n", (long long)T, (long long)H,
+         (long long)Hq, (long long)Hkv, (long long)D, (long long)I);
+  {
+    Buf<uint16_t> x(T * H), r(T * H), w(H), y(T * H), s(T * H), wy(T * H), ws(T * H);
+    fill_normal(x);
+    fill_normal(r);
+    fill_normal(w, 0.f, .5f);
+    rc_ok(pie_hip_gemma_rmsnorm(x.p, H, w.p, y.p, H, T, H, 1e-6f, nullptr), "gemma_rmsnorm");
+    oracle_gemma_rmsnorm(x.p, H, 0, w.p, wy.p, H, 0, T, 1, H, 1e-6);
+    check_close("gemma rmsnorm", y.p, wy.p, T * H);
+    rc_ok(pie_hip_gemma_fused_add_rmsnorm(x.p, H, r.p, H, s.p, H, y.p, H, w.p, T, H, 1e-6f, nullptr),
+          "gemma_add");
+    oracle_gemma_add_rmsnorm(x.p, r.p, w.p, ws.p, wy.p, T, H, 1e-6);
+    check_equal("gemma add s", s.p, ws.p, T * H);
+    check_close("gemma add y", y.p, wy.p, T * H);
+  }
+  const int64_t row = (Hq + 2 * Hkv) * D;
+  {
+    Buf<uint16_t> qkv(T * row), qw(D), kw(D), qo(T * Hq * D), ko(T * Hkv * D), wq(T * Hq * D),
+        wk(T * Hkv * D);
+    fill_normal(qkv);
+    fill_normal(qw, 0.f, .5f);
+    fill_normal(kw, 0.f, .5f);
+    rc_ok(pie_hip_gemma_qk_rmsnorm(qkv.p, row, D, qo.p, Hq * D, D, qkv.p + Hq * D, row, D, ko.p,
+                                   Hkv * D, D, qw.p, kw.p, T, Hq, Hkv, D, 1e-6f, nullptr), "gemma_qk");
+    oracle_gemma_rmsnorm(qkv.p, row, D, qw.p, wq.p, Hq * D, D, T, Hq, D, 1e-6);
+    oracle_gemma_rmsnorm(qkv.p + Hq * D, row, D, kw.p, wk.p, Hkv * D, D, T, Hkv, D, 1e-6);
+    check_close("gemma q", qo.p, wq.p, T * Hq * D);
+    check_close("gemma k", ko.p, wk.p, T * Hkv * D);
+  }
+  {
+    Buf<uint16_t> gu(T * 2 * I), o(T * I), wo(T * I);
+    fill_normal(gu, 0.f, 1.414f);
+    rc_ok(pie_hip_gelu_tanh_and_mul(gu.p, 2 * I, o.p, I, T, I, nullptr), "gelu");
+    oracle_gelu_tanh_and_mul(gu.p, 2 * I, wo.p, T, I);
+    check_close("gelu_tanh_and_mul", o.p, wo.p, T * I);
+  }
+  {
+    const int64_t V = 37;
+    Buf<uint16_t> W(V * H), o(T * H), wo(T * H);
+    Buf<int32_t> ids(T);
+    fill_normal(W);
+    std::uniform_int_distribution<int> d(0, (int)V - 1);
+    for (int64_t t = 0; t < T; ++t) ids[t] = d(rng);
+    if (T > 2) ids[1] = (int32_t)V, ids[2] = -1;
+    const float scale = sqrtf((float)H);
+    rc_ok(pie_hip_embedding_scaled(ids.p, T, W.p, V, H, H, o.p, H, scale, nullptr), "embed_scaled");
+    oracle_embedding_scaled(ids.p, T, W.p, V, H, scale, wo.p);
+    check_equal("embedding scaled", o.p, wo.p, T * H);
+  }
+  for (int il = 0; il < 4; ++il) {
+    const int64_t rd = il < 2 ? D : D / 2, rows = 64, ld = rd + 8;  // padded table rows: ld > rotary_dim
+    Buf<uint16_t> qkv(T * row), ref(T * row);
+    Buf<float> cs(rows * ld);
+    Buf<int32_t> pos(T);
+    fill_normal(qkv);
+    memcpy(ref.p, qkv.p, T * row * 2);
+    for (int64_t p = 0; p < rows; ++p)
+      for (int64_t i = 0; i < ld; ++i) {
+        const double f = pow(10000.0, -2.0 * (double)(i % (rd / 2)) / (double)rd);
+        cs[p * ld + i] = i >= rd ? NAN : i < rd / 2 ? (float)cos(p * f) : (float)sin(p * f);
+      }
+    std::uniform_int_distribution<int> dp(0, (int)rows - 1);
+    for (int64_t t = 0; t < T; ++t) pos[t] = dp(rng);
+    if (T > 2) pos[0] = (int32_t)rows, pos[2] = -3;  // out of the table: left unrotated
+    rc_ok(pie_hip_rope_cos_sin_cache_inplace(qkv.p, row, D, qkv.p + Hq * D, row, D, pos.p, T, Hq, Hkv,
+                                             D, il & 1, cs.p, rows, rd, ld, nullptr), "rope_cs");
+    oracle_rope_cs(ref.p, row, D, ref.p + Hq * D, row, D, pos.p, T, Hq, Hkv, rd, il & 1, cs.p, rows, ld);
+    const char* names[] = {"rope cos/sin table", "rope cos/sin table (interleaved)",
+                           "rope cos/sin table, rd = D/2", "rope cos/sin table, rd = D/2, interleaved"};
+    check_close(names[il], qkv.p, ref.p, T * row);
+  }
+}
+
 static void case_index(int64_t B) {
   printf("index helpers B=%lld\n", (long long)B);
   Paged pg = make_paged(B, 16, 0, 100, 0, 9);
@@ -341,6 +427,11 @@ int main(int argc, char** argv) {
     case_qk_fused(5, 4, 2, 128);  // fused kernel
     case_qk_fused(3, 4, 2, 64);   // D != 128: separate-kernel path
     case_qk_fused(3, 32, 8, 128);
+  }
+  if (all || c == "variants") {
+    case_variants(5, 2304, 4, 2, 128, 1536);   // vector paths
+    case_variants(3, 100, 2, 1, 64, 13);       // scalar / generic fallbacks
+    case_variants(4, 3584, 8, 4, 256, 2048);   // Gemma-2 9B widths, D = 256
   }
   printf("%s\n", failures ? "FAILURES" : "all ok");
   return failures ? 1 : 0;

@@ -329,3 +329,112 @@ def test_workload_positions_match_index_helpers():
     b, p = oracle.batch_indices_positions(N(pb.qo_indptr), sl, int(pb.qo_indptr[-1]))
     assert_bits_equal(b, N(pb.batch_indices))
     assert_bits_equal(p, N(pb.positions))
+
+
+# ----------------------------------------------------------------------------- variant ops
+def _gemma_torch(x, w, eps):
+    """The reference's expression (gemma2.py:514-526), run by torch-CPU. One substitution:
+    torch-CPU's bf16 rsqrt kernel is not correctly rounded (rsqrt(1.0234375) gives 0.9921875;
+    the fp32 value 0.98848 rounds to 0.98828125), while torch's GPU elementwise kernels compute
+    bf16 rsqrt in fp32 and round once, so the rsqrt is taken in fp32 and rounded here."""
+    variance = x.pow(2).mean(-1, keepdim=True)
+    x_normed = x * torch.rsqrt((variance + eps).float()).to(x.dtype)
+    return x_normed * (1.0 + w)
+
+
+def _assert_gemma_rows(got, x, w, eps, what):
+    """Rows whose bf16 variance (exact sum, one rounding) equals torch's must match torch bit for
+    bit; a row where torch's fp32 summation order rounds the variance one ulp the other way may
+    differ by the propagated amount (<= 2.5e-2 relative) and must differ in variance by exactly
+    one ulp."""
+    want = N(_gemma_torch(x, w, eps))
+    v_torch = N(x.pow(2).mean(-1, keepdim=True)).reshape(-1)
+    sq = oracle.bf16_to_f32(oracle.f32_to_bf16(oracle.bf16_to_f32(N(x)) ** 2)).astype(np.float64)
+    v_exact = oracle.f32_to_bf16((sq.sum(-1) / x.shape[-1]).astype(np.float32)).reshape(-1)
+    g2, w2 = got.reshape(-1, x.shape[-1]), want.reshape(-1, x.shape[-1])
+    same = v_exact == v_torch
+    assert same.mean() > 0.8, f"{what}: variance agreement {same.mean()}"
+    assert_bits_equal(g2[same], w2[same], f"{what} (rows with equal variance)")
+    if (~same).any():
+        assert ulp_diff(v_exact[~same], v_torch[~same]).max() == 1
+        assert_bf16_close(g2[~same], w2[~same], rtol=2.5e-2, what=f"{what} (variance 1 ulp apart)")
+
+
+@pytest.mark.parametrize("T,H", [(32, 3584), (16, 2304), (8, 256)])
+def test_gemma_rmsnorm_vs_torch(T, H):
+    x, w = wl.normal((T, H), 31), wl.normal((H,), 32, 0.0, 0.5)
+    _assert_gemma_rows(oracle.gemma_rmsnorm(N(x), N(w), 1e-6), x, w, 1e-6, "gemma rmsnorm")
+    # per-head form (gemma3 _qk_norm on [T, H, D])
+    q = wl.normal((4, 8, 256), 33)
+    wq = wl.normal((256,), 34, 0.0, 0.5)
+    _assert_gemma_rows(oracle.gemma_rmsnorm(N(q), N(wq), 1e-6), q, wq, 1e-6, "gemma per-head")
+
+
+def test_gemma_add_rmsnorm_vs_torch():
+    x, r, w = wl.normal((8, 3584), 35), wl.normal((8, 3584), 36), wl.normal((3584,), 37, 0.0, 0.5)
+    y, s = oracle.gemma_add_rmsnorm(N(x), N(r), N(w), 1e-6)
+    assert_bits_equal(s, N(r + x), "residual")
+    _assert_gemma_rows(y, r + x, w, 1e-6, "gemma add+norm")
+
+
+def test_gemma_rmsnorm_differs_from_standard():
+    """A dropped (1 + w) or a missing step rounding would make gemma equal standard*w."""
+    x, w = wl.normal((4, 512), 38), wl.normal((512,), 39, 0.0, 0.5)
+    g = oracle.bf16_to_f32(oracle.gemma_rmsnorm(N(x), N(w), 1e-6))
+    s1 = oracle.bf16_to_f32(oracle.rmsnorm(N(x), N((1.0 + w.float()).to(torch.bfloat16)), 1e-6))
+    np.testing.assert_allclose(g, s1, rtol=2e-2, atol=2e-2)  # same function up to roundings
+    assert not np.array_equal(g, oracle.bf16_to_f32(oracle.rmsnorm(N(x), N(w), 1e-6)))
+
+
+def test_gelu_tanh_and_mul_vs_torch():
+    gu = wl.normal((32, 2 * 1536), 40, 0.0, 2 ** 0.5)
+    g, u = torch.split(gu, [1536, 1536], -1)
+    want = F.gelu(g, approximate="tanh") * u
+    got = oracle.gelu_tanh_and_mul(N(gu))
+    assert_bf16_close(got, N(want), what="gelu*up")
+    # torch's fp32 1 + tanh(u) cancels for gate << 0 (values ~1e-6); elsewhere <= 1 ulp
+    big = np.abs(oracle.bf16_to_f32(N(want))) > 1e-3
+    assert ulp_diff(got, N(want))[big].max() <= 1
+    assert (got == N(want)).mean() > 0.99
+
+
+def test_gelu_special_values():
+    g = torch.tensor([0.0, 10.0, -10.0], dtype=torch.bfloat16)
+    u = torch.tensor([5.0, 2.0, 3.0], dtype=torch.bfloat16)
+    out = oracle.bf16_to_f32(oracle.gelu_tanh_and_mul(N(torch.cat([g, u])[None])))[0]
+    assert out[0] == 0.0 and out[1] == 20.0 and abs(out[2]) < 1e-6
+
+
+def test_embedding_scaled_vs_torch():
+    c = wl.cfg4(V=300, H=2304, T=64)
+    scale = math.sqrt(2304)
+    want = F.embedding(c["ids"], c["W"]) * scale
+    got, bad = oracle.embedding_scaled(N(c["ids"]), N(c["W"]), scale)
+    assert bad == 0
+    assert_bits_equal(got, N(want), "scaled embedding")
+
+
+def _yarnless_cache(rows, rd, theta):
+    f = oracle.inv_freq_std(rd, 1.0, theta)
+    ang = np.arange(rows, dtype=np.float64)[:, None] * f[None, :]
+    return np.concatenate([np.cos(ang), np.sin(ang)], -1).astype(np.float32), f
+
+
+@pytest.mark.parametrize("interleave", [False, True])
+def test_rope_cos_sin_table_matches_frequency_rope(interleave):
+    T, Hq, Hkv, D = 20, 4, 2, 64
+    q, k = wl.normal((T, Hq, D), 41), wl.normal((T, Hkv, D), 42)
+    pos = torch.randint(0, 500, (T,), generator=torch.Generator().manual_seed(43)).to(torch.int32)
+    cs, f = _yarnless_cache(512, D, 1.5e5)
+    gq, gk = oracle.rope_cos_sin(N(q), N(k), N(pos), cs, interleave)
+    wq, wk = oracle.rope(N(q), N(k), N(pos), f, interleave=interleave)
+    assert ulp_diff(gq, wq).max() <= 1 and ulp_diff(gk, wk).max() <= 1
+    # partial rotary dim: dims past the table's width are untouched
+    cs32, _ = _yarnless_cache(512, 32, 1.5e5)
+    pq, _ = oracle.rope_cos_sin(N(q), N(k), N(pos), cs32, interleave)
+    assert_bits_equal(pq[..., 32:], N(q)[..., 32:])
+    # a position outside the table leaves the token unchanged
+    pos2 = N(pos).copy()
+    pos2[0] = 600
+    oq, _ = oracle.rope_cos_sin(N(q), N(k), pos2, cs, interleave)
+    assert_bits_equal(oq[0], N(q)[0])
