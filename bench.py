@@ -149,6 +149,8 @@ def measure_ops(dev, cold_iters=20, only=None):
         res.extend(_ops_cfg3(dev, run))
     if want("cfg4"):
         res.extend(_ops_cfg4(dev, run))
+    if want("variants"):
+        res.extend(_ops_variants(dev, run))
     if want("cfg5"):
         res.extend(measure_chain(dev, flush, cold_iters))
     del scratch
@@ -217,6 +219,61 @@ def _ops_cfg3(dev, run):
             run(f"cfg3 fused rope+append T={T}", nb["fused"], lambda: make_rope("fused"))]
 
 
+def _ops_variants(dev, run):
+    """The model-family variants at the same Llama-3-8B prefill shapes as configurations 2-4, so
+    their bandwidth compares directly: Gemma add+RMSNorm and RMSNorm [8192, 4096], GELU-tanh-and-mul
+    [8192, 2x14336], the scaled embedding, and RoPE from a [2048, 128] fp32 cos/sin table on
+    configuration 3's q/k (the 1 MB table stays in cache; its reads are not counted)."""
+    import torch
+    from pie_amd import ops
+    from pie_amd import workloads as wl
+    c2 = wl.cfg2()
+    x0, r0, gu0 = (c2[k].to(dev) for k in ("x", "r", "gate_up"))
+    w = wl.normal((x0.shape[1],), 60, 0.0, 0.5).to(dev)
+    b_add, b_act = wl.cfg2_bytes()
+    b_norm = 2 * x0.numel() * 2 + w.numel() * 2
+
+    def make_gemma_add():
+        x, r = x0.clone(), r0.clone()
+        y, s = torch.empty_like(x), torch.empty_like(x)
+        return lambda: ops.gemma_add_rms_norm(x, r, w, 1e-6, out=y, residual_out=s)
+
+    def make_gemma():
+        x, y = x0.clone(), torch.empty_like(x0)
+        return lambda: ops.gemma_rms_norm(x, w, 1e-6, out=y)
+
+    def make_gelu():
+        gu = gu0.clone()
+        act = torch.empty((gu.shape[0], gu.shape[1] // 2), dtype=gu.dtype, device=dev)
+        return lambda: ops.gelu_tanh_and_mul(gu, out=act)
+    res = [run("variant gemma add+rmsnorm [8192,4096]", b_add, make_gemma_add),
+           run("variant gemma rmsnorm [8192,4096]", b_norm, make_gemma),
+           run("variant gelu_tanh_and_mul [8192,2x14336]", b_act, make_gelu)]
+    del x0, r0, gu0
+    c4 = wl.cfg4()
+    W0, ids = c4["W"].to(dev), c4["ids"].to(dev)
+
+    def make_embed():
+        W = W0.clone()
+        out = torch.empty((ids.numel(), W.shape[1]), dtype=W.dtype, device=dev)
+        return lambda: ops.embedding(ids, W, out=out, scale=64.0)
+    res.append(run("variant embedding x sqrt(H) [128256,4096] x16384", wl.cfg4_bytes(), make_embed))
+    del W0
+    c3 = wl.cfg3()
+    T = c3["qkv"].shape[0]
+    qkv0, pos = c3["qkv"].to(dev), c3["batch"].positions.to(dev)
+    inv = 1e4 ** (-torch.arange(0, 128, 2, dtype=torch.float64) / 128)
+    ang = torch.arange(2048, dtype=torch.float64)[:, None] * inv[None, :]
+    cs = torch.cat([ang.cos(), ang.sin()], -1).float().to(dev)
+
+    def make_rope_cs():
+        qkv = qkv0.clone()
+        q, k, _ = wl.split_qkv(qkv, 32, 8, 128)
+        return lambda: ops.apply_rope_with_cos_sin_cache_inplace(pos, q, k, 128, cs)
+    res.append(run(f"variant rope cos/sin table T={T}", wl.cfg3_bytes(T)["rope"], make_rope_cs))
+    return res
+
+
 def _ops_cfg4(dev, run):
     import torch
     from pie_amd import ops
@@ -282,7 +339,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", choices=["all", "main", "ops", "copy", "chain"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--op", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"], default=None,
+    ap.add_argument("--op", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "variants"], default=None,
                     help="with --only ops: measure one configuration")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -42,6 +42,14 @@ __device__ __forceinline__ uint16_t to_bf1(float f) {
 }
 // Round an fp32 value to bf16 and return it widened back to fp32.
 __device__ __forceinline__ float round_bf(float f) { return bf1(to_bf1(f)); }
+// Round a finite fp64 value straight to bf16 (round to nearest even on the 8-bit significand,
+// one rounding, no detour through fp32) and return it as fp32. Exact for results in fp32's
+// normal range.
+__device__ __forceinline__ float round_bf_d(double d) {
+  unsigned long long u = __builtin_bit_cast(unsigned long long, d);
+  u += ((1ull << 44) - 1) + ((u >> 45) & 1ull);
+  return (float)__builtin_bit_cast(double, u & ~((1ull << 45) - 1));
+}
 
 __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
   f[0] = bf_lo(v.x); f[1] = bf_hi(v.x); f[2] = bf_lo(v.y); f[3] = bf_hi(v.y);
@@ -80,6 +88,31 @@ __device__ __forceinline__ float row16_sum(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xF, 0xF, false));
   v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xF, 0xF, false));
   return v;
+}
+// fp64 form: each step moves both 32-bit halves with the same DPP rotation.
+template <int CTRL>
+__device__ __forceinline__ double dpp_ror_d(double v) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)u, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+__device__ __forceinline__ double row16_sum(double v) {
+  v += dpp_ror_d<0x128>(v);
+  v += dpp_ror_d<0x124>(v);
+  v += dpp_ror_d<0x122>(v);
+  v += dpp_ror_d<0x121>(v);
+  return v;
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  const unsigned lo = __builtin_amdgcn_readlane((int)(unsigned)u, l);
+  const unsigned hi = __builtin_amdgcn_readlane((int)(unsigned)(u >> 32), l);
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ double wave_sum(double v) {
+  v = row16_sum(v);
+  return readlane_d(v, 0) + readlane_d(v, 16) + readlane_d(v, 32) + readlane_d(v, 48);
 }
 // Full-wavefront sum, uniform result (scalar register).
 __device__ __forceinline__ float wave_sum(float v) {

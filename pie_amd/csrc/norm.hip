@@ -14,6 +14,8 @@
 // rows per wave instruction. Any other shape takes a generic two-pass path (one wave per row).
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "common.h"
 
 
@@ -44,17 +46,75 @@ struct NormArgs {
 // Gemma (pie/src/pie_worker/model/gemma2.py:514-526, gemma3.py:491-510): the expression
 //   variance = x.pow(2).mean(-1); x * rsqrt(variance + eps) * (1.0 + weight)
 // evaluated as separate bf16 torch ops, i.e. rounded to bf16 after every step.
+// Gemma sums its bf16-rounded squares in fp64: each term has an 8-bit significand, so the sum
+// is exact in any order (unless the squares span more than ~2^44) and the bf16 variance is the
+// correctly rounded mean, independent of the reduction tree. The mean and the rsqrt are formed
+// in fp32 and rounded to bf16, then checked against the two neighbouring bf16 midpoints with fp64
+// products that are exact (a 9-bit midpoint times a 17-bit column count, or a 9-bit midpoint
+// squared times an 8-bit t), and moved one bf16 step when they fall on the wrong side: an fp32
+// result a few ulp off can only misround by one bf16 step. Both are then correctly rounded.
+template <bool GEMMA>
+using acc_t = std::conditional_t<GEMMA, double, float>;
 template <bool GEMMA>
 __device__ __forceinline__ float nsq(float x) { return GEMMA ? round_bf(x * x) : x * x; }
+// ss += sum of the 8 squares. Gemma: a pairwise tree (exact, so the order is free and the
+// dependent chain is short); standard: sequential fp32 adds.
 template <bool GEMMA>
-__device__ __forceinline__ float nscale(float tot, float cols, float eps) {
-  if constexpr (GEMMA) return round_bf(rsqrtf(round_bf(round_bf(tot / cols) + eps)));
-  return rsqrtf(tot / cols + eps);
+__device__ __forceinline__ void accum8(acc_t<GEMMA>& ss, const float* f) {
+  if constexpr (GEMMA) {
+    double p[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) p[e] = (double)nsq<true>(f[2 * e]) + (double)nsq<true>(f[2 * e + 1]);
+    ss += (p[0] + p[1]) + (p[2] + p[3]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += nsq<false>(f[e]);
+  }
+}
+// bf16 neighbours of a non-negative bf16 value held as fp32 (NaN below zero: compares false).
+__device__ __forceinline__ float bf_step(float b, int d) {
+  return __builtin_bit_cast(float, __builtin_bit_cast(unsigned, b) + (unsigned)(d * 0x10000));
+}
+__device__ __forceinline__ bool bf_odd(float b) { return (__builtin_bit_cast(unsigned, b) >> 16) & 1u; }
+// Correctly rounded bf16(tot / cols) for tot >= 0 (exact fp64), ties to even.
+__device__ __forceinline__ float gemma_mean(double tot, int cols) {
+  float b = round_bf((float)tot / (float)cols);
+  const float dn = bf_step(b, -1), up = bf_step(b, 1);
+  const double lo = 0.5 * ((double)dn + (double)b) * cols, hi = 0.5 * ((double)b + (double)up) * cols;
+  if (tot < lo || (tot == lo && bf_odd(b))) b = dn;
+  else if (tot > hi || (tot == hi && bf_odd(b))) b = up;
+  return b;
+}
+// Correctly rounded bf16(1 / sqrt(t)) for a bf16 value t >= 0 (never exactly on a midpoint).
+__device__ __forceinline__ float gemma_rsqrt(float t) {
+  float b = round_bf(rsqrtf(t));
+  const double ml = 0.5 * ((double)bf_step(b, -1) + (double)b), mh = 0.5 * ((double)b + (double)bf_step(b, 1));
+  if (ml * ml * (double)t > 1.0) b = bf_step(b, -1);
+  else if (mh * mh * (double)t < 1.0) b = bf_step(b, 1);
+  return b;
 }
 template <bool GEMMA>
-__device__ __forceinline__ float napply(float x, float r, float w) {
-  if constexpr (GEMMA) return round_bf(x * r) * round_bf(1.0f + w);
-  return (x * r) * w;
+__device__ __forceinline__ float nscale(acc_t<GEMMA> tot, float cols, float eps) {
+  if constexpr (GEMMA) return gemma_rsqrt(round_bf(gemma_mean(tot, (int)cols) + eps));
+  return rsqrtf(tot / cols + eps);
+}
+// Weights enter napply already passed through wprep: Gemma's bf16(1 + w) is formed once, where
+// the weights are loaded, not per element.
+template <bool GEMMA>
+__device__ __forceinline__ float wprep(float w) { return GEMMA ? round_bf(1.0f + w) : w; }
+template <bool GEMMA>
+__device__ __forceinline__ uint4 wprep8(uint4 v) {
+  if constexpr (!GEMMA) return v;
+  float f[8];
+  unpack8(v, f);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = wprep<true>(f[e]);
+  return pack8(f);  // exact: every value is already a bf16
+}
+template <bool GEMMA>
+__device__ __forceinline__ float napply(float x, float r, float wp) {
+  if constexpr (GEMMA) return round_bf(x * r) * wp;
+  return (x * r) * wp;
 }
 
 __device__ __forceinline__ void row_offsets(const RowSet& s, int64_t r, int64_t& oi, int64_t& orr,
@@ -85,7 +145,7 @@ constexpr int kRowsPerGroup = 1;
 // squares through LDS in a fixed order. The weight row stays in registers across rows.
 template <int VPL, int RPG, bool ADD, bool GEMMA>
 __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
-  __shared__ float part[RPG][8];
+  __shared__ acc_t<GEMMA> part[RPG][8];
   const RowSet& s = a.set[0];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = wave / W, gsub = wave - grp * W;
@@ -96,7 +156,7 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
 
   uint4 wv[VPL];
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) wv[j] = ld16(s.w + (int64_t)(v0 + j * vstep) * 8);
+  for (int j = 0; j < VPL; ++j) wv[j] = wprep8<GEMMA>(ld16(s.w + (int64_t)(v0 + j * vstep) * 8));
 
   // A group handles RPG rows at once (rows base+grp, base+grp+G, ...): all their loads are in
   // flight before the first reduction. Block-uniform trip count: every thread reaches every
@@ -105,7 +165,7 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
     int64_t oo[RPG];
     bool live[RPG];
     uint4 xv[RPG][VPL];
-    float ss[RPG];
+    acc_t<GEMMA> ss[RPG];
 #pragma unroll
     for (int k = 0; k < RPG; ++k) {
       const int64_t r = base + grp + (int64_t)k * G;
@@ -113,7 +173,7 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
       int64_t oi = 0, orr = 0, os = 0;
       oo[k] = 0;
       if (live[k]) row_offsets(s, r, oi, orr, os, oo[k]);
-      ss[k] = 0.f;
+      ss[k] = 0;
       if (live[k]) {
 #pragma unroll
         for (int j = 0; j < VPL; ++j) xv[k][j] = ld16(s.in + oi + (int64_t)(v0 + j * vstep) * 8);
@@ -136,12 +196,11 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
         for (int j = 0; j < VPL; ++j) {
           float xf[8];
           unpack8(xv[k][j], xf);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) ss[k] += nsq<GEMMA>(xf[e]);
+          accum8<GEMMA>(ss[k], xf);
         }
       }
     }
-    float tot[RPG];
+    acc_t<GEMMA> tot[RPG];
 #pragma unroll
     for (int k = 0; k < RPG; ++k) tot[k] = wave_sum(ss[k]);
     if (W > 1) {
@@ -152,7 +211,7 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
       __syncthreads();
 #pragma unroll
       for (int k = 0; k < RPG; ++k) {
-        tot[k] = 0.f;
+        tot[k] = 0;
         for (int q = 0; q < W; ++q) tot[k] += part[k][grp * W + q];
       }
       __syncthreads();
@@ -223,11 +282,13 @@ __global__ __launch_bounds__(256) void rmsnorm_heads16(NormArgs a) {
     wc.load(s.w + sub * EPL);
     c.get(f);
     wc.get(wf);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) wf[e] = wprep<GEMMA>(wf[e]);
   } else {
 #pragma unroll
     for (int e = 0; e < EPL; ++e) f[e] = wf[e] = 0.f;
   }
-  float ss = 0.f;
+  acc_t<GEMMA> ss = 0;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) ss += nsq<GEMMA>(f[e]);
   const float rstd = nscale<GEMMA>(row16_sum(ss), (float)a.cols, a.eps);
@@ -256,7 +317,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_generic(NormArgs a) {
     int64_t oi, orr, os, oo;
     row_offsets(s, r, oi, orr, os, oo);
     const uint16_t* src = ADD ? s.sum + os : s.in + oi;
-    float ss = 0.f;
+    acc_t<GEMMA> ss = 0;
     for (int64_t j = lane; j < nv; j += 64) {
       float f[VEC];
       if constexpr (VEC == 8) {
@@ -287,12 +348,12 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_generic(NormArgs a) {
       if constexpr (VEC == 8) {
         float f[8], wf[8];
         unpack8(ld16(src + j * 8), f);
-        unpack8(ld16(s.w + j * 8), wf);
+        unpack8(wprep8<GEMMA>(ld16(s.w + j * 8)), wf);
 #pragma unroll
         for (int e = 0; e < 8; ++e) f[e] = napply<GEMMA>(f[e], rstd, wf[e]);
         st16(s.out + oo + j * 8, pack8(f));
       } else {
-        s.out[oo + j] = to_bf1(napply<GEMMA>(bf1(src[j]), rstd, bf1(s.w[j])));
+        s.out[oo + j] = to_bf1(napply<GEMMA>(bf1(src[j]), rstd, wprep<GEMMA>(bf1(s.w[j]))));
       }
     }
   }
@@ -324,14 +385,15 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
                    (a.set[1].rows == 0 || rowset_vec_ok(a.set[1], ADD));
   const dim3 blk(256);
   if (vec && a.set[1].rows == 0 && a.cols % 512 == 0 && a.cols <= 8 * 12 * 512) {
-    const int64_t n512 = a.cols / 512, target = (int64_t)num_cus() * 16;
-    // As many waves per row as divide it (up to 8): one or two 16-byte vectors per lane keeps
-    // VGPR use low, so more rows are in flight per CU and the last wave of rows is shorter
-    // (measured on configuration 2: 8 waves 46.0 us, 1 wave 50.4 us).
+    const int64_t n512 = a.cols / 512;
+    // Waves per row W (each lane then holds VPL = cols / (512 W) 16-byte vectors). Residual add:
+    // as many waves as divide the row, up to 8 (two input streams already keep 2 KiB per wave in
+    // flight; configuration 2: 8 waves 46.0 us, 1 wave 50.4 us). Plain norm: at least 4 vectors
+    // per lane, since one stream at one vector per lane leaves too few bytes in flight per CU
+    // ([8192, 4096]: 8 waves 31.6 us, 4 waves 26.6, 2 waves 26.0).
     int W = 0;
     for (int w = 8; w >= 1; w /= 2)
-      if (n512 % w == 0 && n512 / w <= 12) { W = w; break; }
-    (void)target;
+      if (n512 % w == 0 && n512 / w <= 12 && (ADD || n512 / w >= 4 || w == 1)) { W = w; break; }
     static const int forced = [] {  // tuning override: PIE_HIP_NORM_WAVES=1|2|4|8
       const char* e = getenv("PIE_HIP_NORM_WAVES");
       return e ? atoi(e) : 0;

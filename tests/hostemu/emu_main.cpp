@@ -278,12 +278,12 @@ static void case_variants(int64_t T, int64_t H, int64_t Hq, int64_t Hkv, int64_t
     fill_normal(w, 0.f, .5f);
     rc_ok(pie_hip_gemma_rmsnorm(x.p, H, w.p, y.p, H, T, H, 1e-6f, nullptr), "gemma_rmsnorm");
     oracle_gemma_rmsnorm(x.p, H, 0, w.p, wy.p, H, 0, T, 1, H, 1e-6);
-    check_close("gemma rmsnorm", y.p, wy.p, T * H);
+    check_equal("gemma rmsnorm", y.p, wy.p, T * H);
     rc_ok(pie_hip_gemma_fused_add_rmsnorm(x.p, H, r.p, H, s.p, H, y.p, H, w.p, T, H, 1e-6f, nullptr),
           "gemma_add");
     oracle_gemma_add_rmsnorm(x.p, r.p, w.p, ws.p, wy.p, T, H, 1e-6);
     check_equal("gemma add s", s.p, ws.p, T * H);
-    check_close("gemma add y", y.p, wy.p, T * H);
+    check_equal("gemma add y", y.p, wy.p, T * H);
   }
   const int64_t row = (Hq + 2 * Hkv) * D;
   {
@@ -296,8 +296,8 @@ static void case_variants(int64_t T, int64_t H, int64_t Hq, int64_t Hkv, int64_t
                                    Hkv * D, D, qw.p, kw.p, T, Hq, Hkv, D, 1e-6f, nullptr), "gemma_qk");
     oracle_gemma_rmsnorm(qkv.p, row, D, qw.p, wq.p, Hq * D, D, T, Hq, D, 1e-6);
     oracle_gemma_rmsnorm(qkv.p + Hq * D, row, D, kw.p, wk.p, Hkv * D, D, T, Hkv, D, 1e-6);
-    check_close("gemma q", qo.p, wq.p, T * Hq * D);
-    check_close("gemma k", ko.p, wk.p, T * Hkv * D);
+    check_equal("gemma q", qo.p, wq.p, T * Hq * D);
+    check_equal("gemma k", ko.p, wk.p, T * Hkv * D);
   }
   {
     Buf<uint16_t> gu(T * 2 * I), o(T * I), wo(T * I);
