@@ -151,6 +151,8 @@ def measure_ops(dev, cold_iters=20, only=None):
         res.extend(_ops_cfg4(dev, run))
     if want("variants"):
         res.extend(_ops_variants(dev, run))
+    if want("attn"):
+        res.extend(_ops_attention(dev, run))
     if want("cfg5"):
         res.extend(measure_chain(dev, flush, cold_iters))
     del scratch
@@ -288,6 +290,30 @@ def _ops_cfg4(dev, run):
     return [run("cfg4 embedding [128256,4096] x16384", wl.cfg4_bytes(), make_embed)]
 
 
+def _ops_attention(dev, run):
+    """Paged decode attention at the Qwen3-8B decode-chain shape (256 sequences, contexts
+    U[128, 4096], Hq 32 / Hkv 8 / D 128, page 16; the ~2.2 GB cache exceeds the last-level cache,
+    so the launches share it and rotate only q / out). Bytes: q + out + every cached k/v row +
+    page table (workloads.attn_bytes)."""
+    import torch
+    from pie_amd import attention
+    from pie_amd import workloads as wl
+    a = wl.attn_decode_cfg()
+    pb = a["batch"]
+    cache, q0 = a["cache"].to(dev), a["q"].to(dev)
+    ws = torch.zeros(128 << 20, dtype=torch.uint8, device=dev)
+    w = attention.BatchDecodeWithPagedKVCacheWrapper(ws, "NHD")
+    w.plan(pb.kv_indptr.to(dev), pb.kv_indices.to(dev), pb.kv_last_page_len.to(dev), 32, 8, 128, 16)
+    nbytes = wl.attn_bytes(pb, 32, 8, 128)
+
+    def make():
+        q, out = q0.clone(), torch.empty_like(q0)
+        return lambda: w.run(q, cache, out=out)
+    res = [run(f"attn decode B=256 ctx U[128,4096] (splits {w._plan['splits']})", nbytes, make)]
+    del cache, ws
+    return res
+
+
 def _back_to_back(fn, n, reps=5):
     """µs per call over n back-to-back calls between two events (median of reps)."""
     import torch
@@ -339,7 +365,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", choices=["all", "main", "ops", "copy", "chain"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--op", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "variants"], default=None,
+    ap.add_argument("--op", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "variants", "attn"], default=None,
                     help="with --only ops: measure one configuration")
     args = ap.parse_args()
     if args.gpus != 1:

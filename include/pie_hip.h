@@ -260,6 +260,38 @@ int pie_hip_get_batch_indices_positions(const int32_t* append_indptr, const int3
                                         int32_t* batch_indices, int32_t* positions,
                                         void* stream);
 
+
+/*
+ * Paged attention, decode form: one query token per request (query row b = request b),
+ *   out[b, h, :] = softmax_t( q[b,h,:] . k_t * sm_scale ) @ v_t   over the request's kv_len tokens,
+ * k_t / v_t of kv head h / (Hq/Hkv) read from the paged cache (token t in page
+ * kv_indices[kv_indptr[b] + t/P], slot t%P; element (page, slot, head, d) at
+ * page*page_stride + slot*slot_stride + head*head_stride + d from k_cache / v_cache).
+ * Replaces flashinfer.BatchDecodeWithPagedKVCacheWrapper.plan/.run as Pie calls them:
+ *   pie/src/pie_worker/model/llama3.py:293-301, :765-777 (plan), :689 (run); the API restated
+ *   in pie/src/flashinfer_metal/ops.py:226-282.
+ *
+ * pie_hip_attention_decode_plan (host only) picks `splits`, the number of pieces each request's
+ * kv range is cut into (max_kv_len < 0: unknown). pie_hip_attention_decode launches
+ * batch * splits work groups per kv head; each piece's range is derived on the device from the
+ * request's current length, so one launch configuration (and one captured graph) serves any
+ * lengths, as Pie's graph replay requires (llama3.py:340-414, :905-950). With splits > 1 the
+ * run needs `workspace` (16-byte aligned) of batch * splits * num_qo_heads * (head_dim + 1) * 4
+ * bytes. head_dim in {64, 128, 256}; num_qo_heads / num_kv_heads <= 16. Page ids outside
+ * [0, num_pages) are treated as masked positions.
+ */
+int pie_hip_attention_decode_plan(int64_t batch, int64_t num_kv_heads, int64_t max_kv_len,
+                                  int64_t num_cus, int64_t* splits);
+int pie_hip_attention_decode(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                             const pie_bf16* k_cache, const pie_bf16* v_cache, int64_t page_stride,
+                             int64_t slot_stride, int64_t head_stride, int64_t num_pages,
+                             const int32_t* kv_indptr, const int32_t* kv_indices,
+                             const int32_t* kv_last_page_len, int64_t batch, int64_t num_qo_heads,
+                             int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                             float sm_scale, int64_t splits, void* workspace, int64_t workspace_bytes,
+                             pie_bf16* out, int64_t o_tok_stride, int64_t o_head_stride,
+                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,10 @@ Each function cites the reference behaviour it restates (paths in the zyma98/pie
   rope / inv_freq_*       pie/src/flashinfer_metal/kernels/metal_rope.metal:26-107
   append                  pie/src/flashinfer_metal/kernels/metal_append_paged_kv_cache.metal:23-107
   seq_lens, batch_indices_positions   pie/src/flashinfer_metal/ops.py:392-436
+  attention               flashinfer Batch{Prefill,Decode}WithPagedKVCacheWrapper.run, restated in
+                          pie/src/flashinfer_metal/ops.py:163-282 and
+                          kernels/metal_attention_simdgroup_opt.metal:120-470; custom masks as
+                          built at pie/src/pie_worker/batching.py:335-386
 
 How each function is pinned (tests/test_oracle.py): against torch-CPU running the
 reference's own expressions (rmsnorm, add, silu*mul, embedding), against transformers'
@@ -74,6 +78,9 @@ def _load():
         "oracle_embedding_scaled": (i64, [_i32p, i64, _u16p, i64, i64, C.c_float, _u16p]),
         "oracle_rope_cs": (None, [_u16p, i64, i64, _u16p, i64, i64, _i32p, i64, i64, i64, i64,
                                   C.c_int, _f32p, i64, i64]),
+        "oracle_attention": (None, [_u16p, i64, i64, C.c_void_p, C.c_void_p, i64, i64, i64,
+                                    _i32p, _i32p, _i32p, _i32p, C.c_void_p, C.c_void_p, i64, i64,
+                                    i64, i64, i64, C.c_double, _u16p, i64, i64, C.c_void_p]),
         "oracle_f32_to_bf16": (C.c_uint16, [C.c_float]),
         "oracle_f64_to_bf16": (C.c_uint16, [C.c_double]),
     }
@@ -278,3 +285,46 @@ def batch_indices_positions(append_indptr, seq_lens_, nnz: int, fill: int = -1):
     _load().oracle_batch_indices_positions(append_indptr, np.ascontiguousarray(seq_lens_, np.int32),
                                            B, nnz, bidx, pos)
     return bidx, pos
+
+
+def attention(q: np.ndarray, cache: np.ndarray, qo_indptr, kv_indptr, kv_indices, last_page_len,
+              custom_mask=None, sm_scale: float | None = None, layout: str = "NHD",
+              return_lse: bool = False):
+    """Paged attention over cache [pages, 2, P, Hkv, D] (NHD) or [pages, 2, Hkv, P, D] (HND).
+    q [T, Hq, D] bf16 bits -> out [T, Hq, D] bf16 bits (and lse [T, Hq] float64, natural log).
+    custom_mask: flat bool/uint8, per request a row-major [qo_len, kv_len] block, concatenated
+    in request order; None means the causal window t <= kv_len - qo_len + i."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    assert cache.flags.c_contiguous and cache.dtype == np.uint16
+    T, Hq, D = q.shape
+    qo_indptr = np.ascontiguousarray(qo_indptr, np.int32)
+    kv_indptr = np.ascontiguousarray(kv_indptr, np.int32)
+    last = np.ascontiguousarray(last_page_len, np.int32)
+    B = qo_indptr.size - 1
+    if layout == "NHD":
+        P, Hkv = cache.shape[2], cache.shape[3]
+        ss, hs = Hkv * D, D
+    else:
+        Hkv, P = cache.shape[2], cache.shape[3]
+        ss, hs = D, P * D
+    ps = 2 * P * Hkv * D
+    scale = 1.0 / np.sqrt(D) if sm_scale is None else float(sm_scale)
+    out = np.zeros((T, Hq, D), dtype=np.uint16)
+    lse = np.zeros((T, Hq), dtype=np.float64)
+    mask_arr = off = None
+    if custom_mask is not None:
+        mask_arr = np.ascontiguousarray(custom_mask, dtype=np.uint8)
+        npg = np.diff(kv_indptr)
+        kvl = np.where(npg > 0, (npg - 1) * P + last, 0).astype(np.int64)
+        qol = np.diff(qo_indptr).astype(np.int64)
+        off = np.zeros(B, dtype=np.int64)
+        off[1:] = np.cumsum(qol * kvl)[:-1]
+        assert mask_arr.size >= int((qol * kvl).sum()), "custom_mask too short"
+    base = cache.ctypes.data
+    _load().oracle_attention(
+        q, Hq * D, D, base, base + P * Hkv * D * 2, ps, ss, hs, qo_indptr, kv_indptr,
+        np.ascontiguousarray(kv_indices, np.int32), last,
+        None if mask_arr is None else mask_arr.ctypes.data,
+        None if off is None else off.ctypes.data, B, Hq, Hkv, D, P, scale, out, Hq * D, D,
+        lse.ctypes.data)
+    return (out, lse) if return_lse else out

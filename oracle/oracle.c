@@ -22,8 +22,13 @@
  *   append             pie/src/flashinfer_metal/kernels/metal_append_paged_kv_cache.metal:23-107
  *   seq_lens           pie/src/flashinfer_metal/ops.py:392-407
  *   batch_indices_positions  pie/src/flashinfer_metal/ops.py:410-436
+ *   attention          flashinfer Batch{Prefill,Decode}WithPagedKVCacheWrapper.run as restated
+ *                      in pie/src/flashinfer_metal/ops.py:163-282 and
+ *                      kernels/metal_attention_simdgroup_opt.metal:120-470 (causal window),
+ *                      custom masks as built at pie/src/pie_worker/batching.py:335-386
  */
 #include <math.h>
+#include <stdlib.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -299,5 +304,67 @@ void oracle_batch_indices_positions(const int32_t* indptr, const int32_t* seq_le
       bidx[t] = (int32_t)b;
       pos[t] = seq_lens[b] - n + (t - start);
     }
+  }
+}
+
+/* ------------------------------------------------------------------ paged attention
+ * For request b: kv_len = (npages-1)*P + last_len[b] (0 with no pages), qo_len =
+ * qo_indptr[b+1]-qo_indptr[b]. Query token i of the request attends kv position t iff
+ *   custom mask:  mask[mask_off[b] + i*kv_len + t] != 0   (row-major [qo_len, kv_len] per request,
+ *                 the layout decode_brle_batch writes, batching.py:335-386)
+ *   otherwise:    t <= kv_len - qo_len + i                  (metal_attention...:176, 243)
+ * Head h reads kv head h / (Hq/Hkv). Scores are q.k * sm_scale in float64, softmax in float64,
+ * output rounded once to bf16. A row with no allowed position gives 0 and lse = -inf.
+ * Token t of request b lives in page kv_indices[kv_indptr[b] + t/P], slot t%P; k and v are
+ * addressed as k_cache/v_cache + page*page_stride + slot*slot_stride + head*head_stride.
+ * lse (optional, [T, Hq]) is the natural-log sum of exp(scaled scores).                  */
+void oracle_attention(const uint16_t* q, int64_t q_ts, int64_t q_hs, const uint16_t* kc,
+                      const uint16_t* vc, int64_t page_stride, int64_t slot_stride,
+                      int64_t head_stride, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                      const int32_t* kv_indices, const int32_t* last_len, const uint8_t* mask,
+                      const int64_t* mask_off, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                      int64_t P, double sm_scale, uint16_t* out, int64_t o_ts, int64_t o_hs,
+                      double* lse) {
+  const int64_t G = Hq / Hkv;
+  for (int64_t b = 0; b < B; ++b) {
+    const int64_t np = kv_indptr[b + 1] - kv_indptr[b];
+    const int64_t kv_len = np > 0 ? (np - 1) * P + last_len[b] : 0;
+    const int64_t q0 = qo_indptr[b], qo_len = qo_indptr[b + 1] - q0;
+    double* s = (double*)malloc(sizeof(double) * (size_t)(kv_len > 0 ? kv_len : 1));
+    double* acc = (double*)malloc(sizeof(double) * (size_t)D);
+    for (int64_t i = 0; i < qo_len; ++i) {
+      for (int64_t h = 0; h < Hq; ++h) {
+        const uint16_t* qv = q + (q0 + i) * q_ts + h * q_hs;
+        const int64_t kh = h / G;
+        double mx = -INFINITY;
+        for (int64_t t = 0; t < kv_len; ++t) {
+          int ok = mask ? mask[mask_off[b] + i * kv_len + t] != 0 : t <= kv_len - qo_len + i;
+          if (!ok) { s[t] = -INFINITY; continue; }
+          const int64_t page = kv_indices[kv_indptr[b] + t / P];
+          const uint16_t* kv = kc + page * page_stride + (t % P) * slot_stride + kh * head_stride;
+          double d = 0;
+          for (int64_t e = 0; e < D; ++e) d += (double)bf2f(qv[e]) * (double)bf2f(kv[e]);
+          s[t] = d * sm_scale;
+          if (s[t] > mx) mx = s[t];
+        }
+        for (int64_t e = 0; e < D; ++e) acc[e] = 0;
+        double den = 0;
+        if (mx > -INFINITY) {
+          for (int64_t t = 0; t < kv_len; ++t) {
+            if (s[t] == -INFINITY) continue;
+            const double p = exp(s[t] - mx);
+            den += p;
+            const int64_t page = kv_indices[kv_indptr[b] + t / P];
+            const uint16_t* vv = vc + page * page_stride + (t % P) * slot_stride + kh * head_stride;
+            for (int64_t e = 0; e < D; ++e) acc[e] += p * (double)bf2f(vv[e]);
+          }
+        }
+        uint16_t* o = out + (q0 + i) * o_ts + h * o_hs;
+        for (int64_t e = 0; e < D; ++e) o[e] = den > 0 ? d2bf(acc[e] / den) : 0;
+        if (lse) lse[(q0 + i) * Hq + h] = den > 0 ? mx + log(den) : -INFINITY;
+      }
+    }
+    free(s);
+    free(acc);
   }
 }

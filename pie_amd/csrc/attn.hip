@@ -1,0 +1,429 @@
+// Paged attention over the KV cache the append kernels write: flashinfer's
+// BatchDecodeWithPagedKVCacheWrapper.run and BatchPrefillWithPagedKVCacheWrapper.run as Pie
+// calls them (pie/src/pie_worker/model/llama3.py:293-313, :689, :765-790; semantics restated in
+// pie/src/flashinfer_metal/ops.py:163-282 and kernels/metal_attention_simdgroup_opt.metal).
+//
+// For request b with kv_len = (npages-1)*P + last_len[b] cached tokens and qo_len query tokens,
+// query token i attends kv positions t <= kv_len - qo_len + i (or where the custom mask is set),
+// head h reads kv head h / (Hq/Hkv), scores are q.k * sm_scale, output is softmax(scores) @ v.
+//
+// MI355X mapping. Both kernels run the matrix products on MFMA v_mfma_f32_16x16x32_bf16:
+//   S^T = K Q^T   A = 16 kv tokens x 32 head dims (straight from HBM into registers: lane
+//                 (n, g) holds token n's dims 8(4s+g)..+8 at step s, one 64-byte run per token
+//                 per step), B = 16 query rows (the same dims permutation), C = S^T tile with
+//                 lane (n, g) holding tokens 4g..4g+3 of query row n;
+//   O  = P V      A = the probabilities in exactly that C layout read as 8 tokens per lane
+//                 (two 16-token subtiles: tokens 4g+i and 16+4g+i), B = V staged row-major in
+//                 LDS and read with ds_read_b64_tr_b16, whose 16-lane transpose turns 4 rows x
+//                 4 dims into the 8-tokens-of-one-dim operand the MFMA wants.
+// The query rows of one MFMA tile are (token, head) pairs of one kv-head group (GQA packing),
+// so a decode step with 4 heads per kv head shares every K/V byte between its 4 heads.
+// Softmax is online in the exp2 domain (scores pre-multiplied by sm_scale*log2 e); P is
+// rounded to bf16 for the second product as flashinfer does; everything else is fp32.
+#include <math.h>
+
+#include <algorithm>
+
+#include "common.h"
+
+namespace pie {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma_16x16x32(const u32x4_t& a, const u32x4_t& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, output lane r element j is element r%4 of
+// the 8 bytes addressed by lane 4j + r/4 (measured on gfx950).
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+  const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+
+__device__ __forceinline__ float lane_read(float v, int src_lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, v)));
+}
+
+__device__ __forceinline__ u32x4_t ld16v(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Kernel argument: the paged KV cache and its page table.
+struct PagedKV {
+  const uint16_t* k;       // k of page 0, slot 0, head 0
+  const uint16_t* v;       // v of page 0, slot 0, head 0
+  int64_t page_stride, slot_stride, head_stride;  // elements
+  const int32_t* indptr;   // [B+1] pages per request
+  const int32_t* indices;  // [sum pages] physical page ids
+  const int32_t* last_len; // [B]
+  int32_t num_pages;       // pages in the pool (ids outside [0, num_pages) are masked out)
+  int32_t page_size;
+  FastDiv pdiv;
+};
+
+__device__ __forceinline__ int kv_length(const PagedKV& kv, int b) {
+  const int np = kv.indptr[b + 1] - kv.indptr[b];
+  return np > 0 ? (np - 1) * kv.page_size + kv.last_len[b] : 0;
+}
+
+// Element offset of (token t of the request whose pages start at indices[page0], kv head h);
+// -1 if its page id is out of range.
+__device__ __forceinline__ int64_t kv_offset(const PagedKV& kv, int page0, int t, int h) {
+  const uint32_t lp = kv.pdiv.div((uint32_t)t);
+  const int slot = t - (int)lp * kv.page_size;
+  const int page = kv.indices[page0 + (int)lp];
+  if ((unsigned)page >= (unsigned)kv.num_pages) return -1;
+  return (int64_t)page * kv.page_stride + (int64_t)slot * kv.slot_stride + (int64_t)h * kv.head_stride;
+}
+
+constexpr int kTileTokens = 32;  // kv tokens per wave iteration (two 16-token MFMA subtiles)
+constexpr int kPad = 16;         // LDS row padding (elements) against bank conflicts
+
+// One wave's running state for 16 query rows over a stream of 32-token kv tiles.
+template <int D>
+struct WaveAttn {
+  static constexpr int NS = D / 32;  // MFMA k-steps over the head dim
+  static constexpr int NB = D / 16;  // 16-dim output blocks
+  static constexpr int PITCH = D + kPad;
+  u32x4_t qb[NS];     // B operand: query row n, dims 8(4s+g)..+8
+  f32x4_t o[NB];      // C layout: rows 4g+i, dim 16nb+n
+  float m;            // running max (exp2 domain) of row n, same in all four lane groups
+  float l;            // this lane's partial sum of row n's probabilities
+
+  __device__ __forceinline__ void init() {
+    #pragma unroll
+    for (int nb = 0; nb < NB; ++nb) o[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    m = -INFINITY;
+    l = 0.f;
+  }
+
+  // One 32-token tile: ka = K A-operands of the two subtiles (already loaded), ok[u][i] says
+  // whether token 16u+4g+i is visible to row n, vt = the tile's V rows in LDS ([32][PITCH]).
+  __device__ __forceinline__ void tile(const u32x4_t (&ka)[2][NS], const bool (&ok)[2][4],
+                                       const uint16_t* vt, float scale_log2, int lane) {
+    float s[2][4];
+    #pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      #pragma unroll
+      for (int st = 0; st < NS; ++st) acc = mfma_16x16x32(ka[u][st], qb[st], acc);
+      #pragma unroll
+      for (int i = 0; i < 4; ++i) s[u][i] = ok[u][i] ? acc[i] * scale_log2 : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    mx = fmaxf(mx, lane_read(mx, lane ^ 16));
+    mx = fmaxf(mx, lane_read(mx, lane ^ 32));
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = fast_exp2(m - m_use);
+    float p[2][4], psum = 0.f;
+    #pragma unroll
+    for (int u = 0; u < 2; ++u)
+      #pragma unroll
+      for (int i = 0; i < 4; ++i) { p[u][i] = fast_exp2(s[u][i] - m_use); psum += p[u][i]; }
+    l = l * alpha + psum;
+    m = m_new;
+    // O rows 4g+i take the factor of row 4g+i (held by lane 4g+i of every group)
+    const int g = lane >> 4;
+    float a[4];
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = lane_read(alpha, 4 * g + i);
+    const u32x4_t pa = {pack_bf2(p[0][0], p[0][1]), pack_bf2(p[0][2], p[0][3]),
+                        pack_bf2(p[1][0], p[1][1]), pack_bf2(p[1][2], p[1][3])};
+    // tr16 source addresses: lane 16g + 4j + q reads row (16h + 4g + j), dims 16nb + 4q..+3
+    const int j = (lane >> 2) & 3, q = lane & 3;
+    const uint16_t* r0 = vt + (4 * g + j) * PITCH + 4 * q;
+    const uint16_t* r1 = r0 + 16 * PITCH;
+    #pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const uint2 lo = lds_read_tr16(r0 + 16 * nb);
+      const uint2 hi = lds_read_tr16(r1 + 16 * nb);
+      const u32x4_t vb = {lo.x, lo.y, hi.x, hi.y};
+      f32x4_t c = o[nb];
+      #pragma unroll
+      for (int i = 0; i < 4; ++i) c[i] *= a[i];
+      o[nb] = mfma_16x16x32(pa, vb, c);
+    }
+  }
+
+  // Row n's total probability mass (sum of the four lane groups' partials).
+  __device__ __forceinline__ float row_sum(int lane) const {
+    float t = l + lane_read(l, lane ^ 16);
+    return t + lane_read(t, lane ^ 32);
+  }
+};
+
+// ------------------------------------------------------------------------------ decode
+// Grid (batch * splits, kv heads): work group x handles request x / splits, split x % splits of
+// its kv range. The split is derived on the device from the request's current kv length
+// (chunks of ceil(kv_len / splits) rounded up to whole 32-token tiles, at least kMinChunk), so a
+// launch depends only on (batch, splits) and a captured graph replays correctly for any lengths.
+// With one split the work group writes the output; otherwise it writes an fp32 partial output
+// and its log2-sum-exp to slot x, and attn_merge_kernel combines the splits.
+constexpr int kMinChunk = 128;
+
+__device__ __forceinline__ void split_range(int kv_len, int splits, int j, int& kv0, int& kv1) {
+  int chunk = (kv_len + splits - 1) / splits;
+  chunk = max(kMinChunk, (chunk + kTileTokens - 1) / kTileTokens * kTileTokens);
+  kv0 = min(kv_len, j * chunk);
+  kv1 = min(kv_len, kv0 + chunk);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_decode_kernel(
+    const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv, int G, int Hq,
+    float scale_log2, int splits, uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs,
+    float* __restrict__ part_o, float* __restrict__ part_lse) {
+  using W = WaveAttn<D>;
+  constexpr int PITCH = W::PITCH;
+  constexpr int kVtile = kTileTokens * PITCH;                     // elements per wave
+  constexpr int kSmem = (4 * kVtile * 2 > 4 * 16 * (D + 2) * 4) ? 4 * kVtile * 2 : 4 * 16 * (D + 2) * 4;
+  __shared__ __attribute__((aligned(16))) char smem[kSmem];
+
+  const int slot = blockIdx.x;
+  const int b = slot / splits;
+  const int kvh = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int kv_len = kv_length(kv, b);
+  int kv0, kv1;
+  split_range(kv_len, splits, slot - b * splits, kv0, kv1);
+  const int page0 = kv.indptr[b];
+
+  W st;
+  st.init();
+  // query rows of this kv head: heads kvh*G + n (rows n >= G are zero)
+  {
+    const bool valid = n < G;
+    const uint16_t* qp = q + (int64_t)b * q_ts + (int64_t)(kvh * G + (valid ? n : 0)) * q_hs;
+    #pragma unroll
+    for (int s = 0; s < W::NS; ++s) {
+      const u32x4_t z = {0u, 0u, 0u, 0u};
+      st.qb[s] = valid ? ld16v(qp + 8 * (4 * s + g)) : z;
+    }
+  }
+  uint16_t* vt = reinterpret_cast<uint16_t*>(smem) + w * kVtile;
+  constexpr int CH = D / 8;              // 16-byte chunks per row
+  constexpr int RPI = 64 / CH;           // rows per load instruction
+  constexpr int NVL = kTileTokens / RPI; // V load instructions per tile
+  for (int t0 = kv0 + kTileTokens * w; t0 < kv1; t0 += 4 * kTileTokens) {
+    u32x4_t ka[2][W::NS];
+    bool ok[2][4];
+    #pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int tok = t0 + 16 * u + n;
+      const int64_t off = kv_offset(kv, page0, min(tok, kv1 - 1), kvh);
+      const uint16_t* kp = kv.k + (off < 0 ? 0 : off);
+      #pragma unroll
+      for (int s = 0; s < W::NS; ++s) ka[u][s] = ld16v(kp + 8 * (4 * s + g));
+      // token 16u+n is visible if inside [t0, kv1) with a valid page (decode has no causal
+      // cut: the query is the last position); row n's lanes need tokens 16u+4g+i
+      const uint64_t vis = __builtin_amdgcn_ballot_w64(tok < kv1 && off >= 0);
+      #pragma unroll
+      for (int i = 0; i < 4; ++i) ok[u][i] = (vis >> (4 * g + i)) & 1ull;
+    }
+    u32x4_t vv[NVL];
+    bool vok[NVL];
+    #pragma unroll
+    for (int i = 0; i < NVL; ++i) {
+      const int r = RPI * i + lane / CH;
+      const int64_t off = kv_offset(kv, page0, min(t0 + r, kv1 - 1), kvh);
+      vok[i] = off >= 0;
+      vv[i] = ld16v(kv.v + (off < 0 ? 0 : off) + 8 * (lane % CH));
+    }
+    #pragma unroll
+    for (int i = 0; i < NVL; ++i) {
+      const int r = RPI * i + lane / CH;
+      const u32x4_t z = {0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4_t*>(vt + r * PITCH + 8 * (lane % CH)) = vok[i] ? vv[i] : z;
+    }
+    st.tile(ka, ok, vt, scale_log2, lane);
+  }
+  const float lsum = st.row_sum(lane);
+
+  // merge the four waves through LDS: m[4][16], l[4][16], o[4][16][D] (fp32)
+  __syncthreads();
+  float* ms = reinterpret_cast<float*>(smem);
+  float* ls = ms + 4 * 16;
+  float* os = ls + 4 * 16;
+  if (g == 0) { ms[w * 16 + n] = st.m; ls[w * 16 + n] = lsum; }
+  #pragma unroll
+  for (int nb = 0; nb < W::NB; ++nb)
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) os[(w * 16 + 4 * g + i) * D + 16 * nb + n] = st.o[nb][i];
+  __syncthreads();
+  for (int u = threadIdx.x; u < G * CH; u += 256) {
+    const int row = u / CH, c = u % CH;
+    float M = -INFINITY;
+    #pragma unroll
+    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, ms[ww * 16 + row]);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float L = 0.f;
+    if (M != -INFINITY) {
+      #pragma unroll
+      for (int ww = 0; ww < 4; ++ww) {
+        const float f = fast_exp2(ms[ww * 16 + row] - M);
+        L += ls[ww * 16 + row] * f;
+        const float* src = os + (ww * 16 + row) * D + 8 * c;
+        #pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += src[e] * f;
+      }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    #pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= inv;
+    const int hq = kvh * G + row;
+    if (splits == 1) {
+      st16(out + (int64_t)b * o_ts + (int64_t)hq * o_hs + 8 * c, pack8(acc));
+    } else {
+      float* dst = part_o + ((int64_t)slot * Hq + hq) * D + 8 * c;
+      #pragma unroll
+      for (int e = 0; e < 8; ++e) dst[e] = acc[e];
+      if (c == 0) part_lse[(int64_t)slot * Hq + hq] = L > 0.f ? M + log2f(L) : -INFINITY;
+    }
+  }
+}
+
+// Combines the `splits` partial results of each (request, head).
+template <int D>
+__global__ __launch_bounds__(64) void attn_merge_kernel(int B, int Hq, int splits,
+                                                        const float* __restrict__ part_o,
+                                                        const float* __restrict__ part_lse,
+                                                        uint16_t* __restrict__ out, int64_t o_ts,
+                                                        int64_t o_hs) {
+  constexpr int CH = D / 8;
+  const int b = blockIdx.x;
+  const int hq = blockIdx.y * (64 / CH) + threadIdx.x / CH;
+  const int c = threadIdx.x % CH;
+  if (b >= B || hq >= Hq) return;
+  const int s0 = b * splits, ns = splits;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, part_lse[(int64_t)(s0 + s) * Hq + hq]);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float L = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < ns; ++s) {
+      const float f = fast_exp2(part_lse[(int64_t)(s0 + s) * Hq + hq] - M);
+      L += f;
+      const float* src = part_o + ((int64_t)(s0 + s) * Hq + hq) * D + 8 * c;
+      #pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += src[e] * f;
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  #pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] *= inv;
+  st16(out + (int64_t)b * o_ts + (int64_t)hq * o_hs + 8 * c, pack8(acc));
+}
+
+}  // namespace pie
+
+using namespace pie;
+
+// Host: how many splits per request. Aims at ~16 work groups per CU over all (request, kv head,
+// split) triples; when the longest context is known (max_kv_len >= 0) no split is shorter than
+// kMinChunk tokens. The result depends on the batch only, so one plan serves a captured graph.
+extern "C" int pie_hip_attention_decode_plan(int64_t batch, int64_t num_kv_heads, int64_t max_kv_len,
+                                             int64_t num_cus, int64_t* splits) {
+  PIE_REQUIRE(splits && batch >= 0 && num_kv_heads > 0, "decode_plan: bad batch %lld / num_kv_heads %lld",
+              (long long)batch, (long long)num_kv_heads);
+  const int64_t cus = num_cus > 0 ? num_cus : 256;
+  const int64_t per = std::max<int64_t>(1, batch * num_kv_heads);
+  int64_t s = (16 * cus + per - 1) / per;
+  if (max_kv_len >= 0) s = std::min<int64_t>(s, std::max<int64_t>(1, (max_kv_len + kMinChunk - 1) / kMinChunk));
+  *splits = std::max<int64_t>(1, std::min<int64_t>(s, 64));
+  return PIE_HIP_OK;
+}
+
+static int paged_kv_desc(PagedKV* kv, const uint16_t* k_cache, const uint16_t* v_cache,
+                         int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                         int64_t num_pages, const int32_t* kv_indptr, const int32_t* kv_indices,
+                         const int32_t* kv_last_page_len, int64_t page_size, int64_t D,
+                         const char* what) {
+  PIE_REQUIRE(k_cache && v_cache && kv_indptr && kv_indices && kv_last_page_len, "%s: null cache or page table", what);
+  PIE_REQUIRE(page_size > 0 && page_size <= 65536 && num_pages > 0 && num_pages < (1ll << 31),
+              "%s: bad page_size %lld / num_pages %lld", what, (long long)page_size, (long long)num_pages);
+  PIE_REQUIRE(aligned16(k_cache) && aligned16(v_cache) && page_stride % 8 == 0 && slot_stride % 8 == 0 &&
+                  head_stride % 8 == 0,
+              "%s: cache pointers and strides must be 16-byte aligned", what);
+  (void)D;
+  kv->k = k_cache;
+  kv->v = v_cache;
+  kv->page_stride = page_stride;
+  kv->slot_stride = slot_stride;
+  kv->head_stride = head_stride;
+  kv->indptr = kv_indptr;
+  kv->indices = kv_indices;
+  kv->last_len = kv_last_page_len;
+  kv->num_pages = (int32_t)num_pages;
+  kv->page_size = (int32_t)page_size;
+  kv->pdiv = FastDiv::make((uint32_t)page_size);
+  return PIE_HIP_OK;
+}
+
+template <int D>
+static void launch_decode(hipStream_t st, const uint16_t* q, int64_t q_ts, int64_t q_hs,
+                          const PagedKV& kv, int G, int Hq, int Hkv, float sl2, int B, int splits,
+                          uint16_t* out, int64_t o_ts, int64_t o_hs, float* po, float* pl) {
+  hipLaunchKernelGGL(attn_decode_kernel<D>, dim3(B * splits, Hkv), dim3(256), 0, st, q, q_ts, q_hs, kv,
+                     G, Hq, sl2, splits, out, o_ts, o_hs, po, pl);
+  if (splits > 1)
+    hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(B, (Hq + 64 / (D / 8) - 1) / (64 / (D / 8))), dim3(64), 0,
+                       st, B, Hq, splits, po, pl, out, o_ts, o_hs);
+}
+
+extern "C" int pie_hip_attention_decode(
+    const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride, const pie_bf16* k_cache,
+    const pie_bf16* v_cache, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+    int64_t num_pages, const int32_t* kv_indptr, const int32_t* kv_indices,
+    const int32_t* kv_last_page_len, int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
+    int64_t head_dim, int64_t page_size, float sm_scale, int64_t splits, void* workspace,
+    int64_t workspace_bytes, pie_bf16* out, int64_t o_tok_stride, int64_t o_head_stride,
+    void* stream) {
+  PagedKV kv;
+  int rc = paged_kv_desc(&kv, k_cache, v_cache, page_stride, slot_stride, head_stride, num_pages,
+                         kv_indptr, kv_indices, kv_last_page_len, page_size, head_dim,
+                         "attention_decode");
+  if (rc) return rc;
+  PIE_REQUIRE(q && out, "attention_decode: null q or out");
+  PIE_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
+              "attention_decode: head_dim %lld not in {64, 128, 256}", (long long)head_dim);
+  PIE_REQUIRE(num_kv_heads > 0 && num_qo_heads % num_kv_heads == 0 && num_qo_heads / num_kv_heads <= 16 &&
+                  num_kv_heads <= 65535,
+              "attention_decode: need num_qo_heads = G * num_kv_heads with G <= 16 (got %lld / %lld)",
+              (long long)num_qo_heads, (long long)num_kv_heads);
+  PIE_REQUIRE(batch >= 0 && splits >= 1 && splits <= 64 && batch * splits < (1ll << 31),
+              "attention_decode: bad batch %lld / splits %lld", (long long)batch, (long long)splits);
+  PIE_REQUIRE(aligned16(q) && aligned16(out) && q_tok_stride % 8 == 0 && q_head_stride % 8 == 0 &&
+                  o_tok_stride % 8 == 0 && o_head_stride % 8 == 0,
+              "attention_decode: q/out pointers and strides must be 16-byte aligned");
+  const int64_t slots = splits > 1 ? batch * splits : 0;
+  const int64_t need = slots * num_qo_heads * (head_dim + 1) * 4;
+  PIE_REQUIRE(slots == 0 || (workspace && workspace_bytes >= need && aligned16(workspace)),
+              "attention_decode: workspace of %lld bytes < %lld needed for %lld splits",
+              (long long)workspace_bytes, (long long)need, (long long)splits);
+  if (batch == 0) return PIE_HIP_OK;
+  float* po = static_cast<float*>(workspace);
+  float* pl = po ? po + slots * num_qo_heads * head_dim : nullptr;
+  const int G = (int)(num_qo_heads / num_kv_heads);
+  const float sl2 = sm_scale * 1.4426950408889634f;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int B = (int)batch, S = (int)splits, Hq = (int)num_qo_heads, Hkv = (int)num_kv_heads;
+  switch (head_dim) {
+    case 64: launch_decode<64>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, out,
+                               o_tok_stride, o_head_stride, po, pl); break;
+    case 128: launch_decode<128>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, out,
+                                 o_tok_stride, o_head_stride, po, pl); break;
+    default: launch_decode<256>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, out,
+                                o_tok_stride, o_head_stride, po, pl); break;
+  }
+  return check_launch("attention_decode");
+}

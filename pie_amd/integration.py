@@ -7,7 +7,7 @@ The model files choose their kernel namespace at import time
     else:                  import flashinfer as ops
 
 ``install()`` registers a module named ``flashinfer`` whose hot-path functions are this
-package's gfx950 kernels. Every other attribute (the attention wrappers, sampling, ...) is
+package's gfx950 kernels, as are the paged-attention wrappers. Every other attribute (sampling, ...) is
 looked up in the real flashinfer package when one is importable, and raises AttributeError
 otherwise. Call it before the model modules are imported; it is idempotent.
 """
@@ -17,7 +17,7 @@ import importlib
 import sys
 import types
 
-from . import ops
+from . import attention, ops
 
 # flashinfer names this package serves (the calls at llama3.py:660-755, qwen3.py:665-684,
 # gemma2.py:608, gpt_oss.py:671-678).
@@ -33,6 +33,8 @@ HOT_PATH = (
     "gelu_tanh_and_mul",
     "apply_rope_with_cos_sin_cache_inplace",
 )
+# flashinfer's attention wrapper classes (llama3.py:293-313)
+ATTENTION = ("BatchDecodeWithPagedKVCacheWrapper",)
 
 
 class _Namespace(types.ModuleType):
@@ -42,6 +44,8 @@ class _Namespace(types.ModuleType):
         self._fallback = fallback
         for n in HOT_PATH:
             setattr(self, n, getattr(ops, n))
+        for n in ATTENTION:
+            setattr(self, n, getattr(attention, n))
 
     def __getattr__(self, item):
         fb = self.__dict__.get("_fallback")

@@ -408,31 +408,32 @@ def apply_rope_with_cos_sin_cache_inplace(positions: torch.Tensor, query: torch.
 
 
 # ----------------------------------------------------------------------------- paged KV append
-def _cache_desc(paged_kv_cache, kv_layout: str, Hkv: int, D: int):
+def _cache_desc(paged_kv_cache, kv_layout: str, Hkv: int, D: int,
+                name: str = "append_paged_kv_cache"):
     """(k_cache, v_cache, num_pages, page_stride, slot_stride, head_stride, page_size)."""
     if kv_layout not in ("NHD", "HND"):
-        raise ValueError(f"append_paged_kv_cache: kv_layout must be 'NHD' or 'HND', got {kv_layout!r}")
+        raise ValueError(f"{name}: kv_layout must be 'NHD' or 'HND', got {kv_layout!r}")
     if isinstance(paged_kv_cache, (tuple, list)):
         kc, vc = paged_kv_cache
-        _check("append_paged_kv_cache", _BF16, k_cache=kc, v_cache=vc)
+        _check(name, _BF16, k_cache=kc, v_cache=vc)
         if kc.dim() != 4 or kc.shape != vc.shape or kc.stride() != vc.stride():
-            raise ValueError("append_paged_kv_cache: k/v caches must be matching 4-D tensors")
+            raise ValueError(f"{name}: k/v caches must be matching 4-D tensors")
         sl, hd = (1, 2) if kv_layout == "NHD" else (2, 1)
         shape, st = kc.shape, kc.stride()
         k_ptr, v_ptr = kc.data_ptr(), vc.data_ptr()
         page_stride = st[0]
     else:
         c = paged_kv_cache
-        _check("append_paged_kv_cache", _BF16, paged_kv_cache=c)
+        _check(name, _BF16, paged_kv_cache=c)
         if c.dim() != 5 or c.shape[1] != 2:
-            raise ValueError("append_paged_kv_cache: cache must be [pages, 2, ...] (5-D)")
+            raise ValueError(f"{name}: cache must be [pages, 2, ...] (5-D)")
         sl, hd = (2, 3) if kv_layout == "NHD" else (3, 2)
         shape, st = c.shape, c.stride()
         k_ptr = c.data_ptr()
         v_ptr = k_ptr + st[1] * c.element_size()
         page_stride = st[0]
     if shape[hd] != Hkv or shape[-1] != D or st[-1] != 1:
-        raise ValueError(f"append_paged_kv_cache: cache shape {tuple(shape)} does not hold "
+        raise ValueError(f"{name}: cache shape {tuple(shape)} does not hold "
                          f"{Hkv} kv heads of dim {D} ({kv_layout})")
     return k_ptr, v_ptr, shape[0], page_stride, st[sl], st[hd], shape[sl]
 

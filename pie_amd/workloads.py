@@ -170,3 +170,57 @@ def cfg5_bytes(B: int = 256, H: int = 4096, Hq: int = 32, Hkv: int = 8, D: int =
         "append": B * (2 * 2 * 2 * Hkv * D + 8),
         "silu_and_mul": B * 2 * I * 2 + B * I * 2,
     }
+
+
+# ----------------------------------------------------------------------------- paged attention
+def attn_batch(ctx_before, new_tokens, Hq: int = 32, Hkv: int = 8, D: int = 128,
+               page_size: int = 16, pool_pages: int | None = None, seed: int = 30,
+               layout: str = "NHD") -> dict:
+    """Paged attention inputs: requests holding ctx_before[b] cached tokens and ending with
+    new_tokens[b] query tokens (whose k/v are already in the cache, as after the append of
+    llama3.py:675-685). The cache is filled with N(0,1) everywhere, q [T, Hq, D] ~ N(0,1)."""
+    ctx_before = torch.as_tensor(ctx_before, dtype=torch.int32)
+    new_tokens = torch.as_tensor(new_tokens, dtype=torch.int32)
+    total = ctx_before + new_tokens
+    need = int(((total + page_size - 1) // page_size).sum())
+    pool = need if pool_pages is None else pool_pages
+    pb = paged_batch(ctx_before, new_tokens, page_size, pool, seed + 1)
+    T = int(new_tokens.sum())
+    shape = (pool, 2, page_size, Hkv, D) if layout == "NHD" else (pool, 2, Hkv, page_size, D)
+    return {"q": normal((T, Hq, D), seed + 2), "cache": normal(shape, seed + 3), "batch": pb,
+            "Hq": Hq, "Hkv": Hkv, "D": D, "layout": layout}
+
+
+def attn_decode_cfg(B: int = 256, ctx_lo: int = 128, ctx_hi: int = 4096, **kw) -> dict:
+    """Decode attention at the Qwen3-8B decode-chain shape: B sequences x 1 query token over
+    contexts U[ctx_lo, ctx_hi] (the same draw as cfg5), Hq 32 / Hkv 8 / D 128, page 16."""
+    ctx = torch.randint(ctx_lo, ctx_hi + 1, (B,), generator=_gen(14)).to(torch.int32)
+    return attn_batch(ctx, torch.ones(B, dtype=torch.int32), seed=40, **kw)
+
+
+def attn_prefill_cfg(B: int = 64, max_len: int = 2048, **kw) -> dict:
+    """Causal prefill attention over cfg3's ragged batch (64 requests, lengths U[1, 2048], the
+    same draw), Llama-3-8B heads (Hq 32 / Hkv 8 / D 128), page 16."""
+    lens = torch.randint(1, max_len + 1, (B,), generator=_gen(7)).to(torch.int32)
+    return attn_batch(torch.zeros(B, dtype=torch.int32), lens, seed=50, **kw)
+
+
+def attn_bytes(pb: PagedBatch, Hq: int, Hkv: int, D: int) -> int:
+    """Algorithmic HBM bytes of one attention call: q read + out written once, every cached
+    k/v row of every request read once, plus the page table and indptr arrays."""
+    T = int(pb.qo_indptr[-1])
+    kv_tokens = int(pb.seq_lens.sum())
+    B = pb.seq_lens.numel()
+    return (2 * T * Hq * D * 2 + kv_tokens * Hkv * D * 2 * 2 + pb.kv_indices.numel() * 4
+            + (3 * B + 2) * 4)
+
+
+def attn_flops(pb: PagedBatch, Hq: int, D: int, causal: bool = True) -> int:
+    """Useful flops (QK^T and PV, 2 per multiply-add) over the causal window."""
+    qo = (pb.qo_indptr[1:] - pb.qo_indptr[:-1]).to(torch.int64)
+    kv = pb.seq_lens.to(torch.int64)
+    if causal:  # query i sees kv - qo + i + 1 positions
+        pairs = (qo * (kv - qo) + qo * (qo + 1) // 2).sum()
+    else:
+        pairs = (qo * kv).sum()
+    return int(pairs) * Hq * D * 4

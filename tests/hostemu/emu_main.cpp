@@ -3,12 +3,13 @@
 // the results with the CPU oracle (oracle/oracle.c). TEST INFRASTRUCTURE.
 //
 //   emu_main <case>    case = norm | qk | silu | embed | rope | fused | decode | index | qkfused |
-//                      variants | fastdiv | all | big
+//                      variants | fastdiv | attn | all | big
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <random>
 #include <string>
 #include <vector>
@@ -39,6 +40,10 @@ int64_t oracle_embedding_scaled(const int32_t*, int64_t, const uint16_t*, int64_
                                 uint16_t*);
 void oracle_rope_cs(uint16_t*, int64_t, int64_t, uint16_t*, int64_t, int64_t, const int32_t*, int64_t,
                     int64_t, int64_t, int64_t, int, const float*, int64_t, int64_t);
+void oracle_attention(const uint16_t*, int64_t, int64_t, const uint16_t*, const uint16_t*, int64_t,
+                      int64_t, int64_t, const int32_t*, const int32_t*, const int32_t*, const int32_t*,
+                      const uint8_t*, const int64_t*, int64_t, int64_t, int64_t, int64_t, int64_t, double,
+                      uint16_t*, int64_t, int64_t, double*);
 void oracle_seq_lens(const int32_t*, const int32_t*, int64_t, int64_t, int32_t*);
 void oracle_batch_indices_positions(const int32_t*, const int32_t*, int64_t, int64_t, int32_t*, int32_t*);
 }
@@ -343,6 +348,58 @@ static void case_variants(int64_t T, int64_t H, int64_t Hq, int64_t Hkv, int64_t
   }
 }
 
+// ---------------------------------------------------------------------------- attention
+// Paged decode attention: contexts in [lo, hi], random page permutation of an exact-size pool,
+// NHD cache; `chunk` = splits per request (0 = the library's choice).
+static void case_attn_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int lo, int hi,
+                             int64_t chunk) {
+  printf("attn_decode B=%lld Hq=%lld Hkv=%lld D=%lld P=%lld ctx=[%d,%d] chunk=%lld\n", (long long)B,
+         (long long)Hq, (long long)Hkv, (long long)D, (long long)P, lo, hi, (long long)chunk);
+  std::vector<int32_t> len(B), indptr(B + 1, 0), last(B);
+  std::uniform_int_distribution<int> dl(lo, hi);
+  for (int64_t b = 0; b < B; ++b) {
+    len[b] = dl(rng);
+    const int np = (len[b] + P - 1) / P;
+    indptr[b + 1] = indptr[b] + np;
+    last[b] = np ? len[b] - (np - 1) * (int)P : 0;
+  }
+  const int64_t pages = std::max<int64_t>(indptr[B], 1);
+  Buf<int32_t> ip(B + 1), idx(pages), ll(B);
+  std::vector<int32_t> perm(pages);
+  for (int64_t i = 0; i < pages; ++i) perm[i] = (int32_t)i;
+  std::shuffle(perm.begin(), perm.end(), rng);
+  for (int64_t i = 0; i < pages; ++i) idx[i] = perm[i];
+  for (int64_t b = 0; b <= B; ++b) ip[b] = indptr[b];
+  for (int64_t b = 0; b < B; ++b) ll[b] = last[b];
+  const int64_t page_elems = 2 * P * Hkv * D;
+  Buf<uint16_t> cache(pages * page_elems), q(B * Hq * D), out(B * Hq * D), want(B * Hq * D);
+  fill_normal(cache);
+  fill_normal(q);
+  int64_t splits = chunk;
+  if (splits <= 0) rc_ok(pie_hip_attention_decode_plan(B, Hkv, hi, 4, &splits), "decode_plan");
+  Buf<float> ws(std::max<int64_t>(B * splits * Hq * (D + 1), 1));
+  rc_ok(pie_hip_attention_decode(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D,
+                                 pages, ip.p, idx.p, ll.p, B, Hq, Hkv, D, P, 1.f / sqrtf((float)D),
+                                 splits, ws.p, (int64_t)(ws.n * 4), out.p, Hq * D, D, nullptr),
+        "attention_decode");
+  std::vector<int32_t> qo(B + 1);
+  for (int64_t b = 0; b <= B; ++b) qo[b] = (int32_t)b;
+  oracle_attention(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, qo.data(), ip.p,
+                   idx.p, ll.p, nullptr, nullptr, B, Hq, Hkv, D, P, 1.0 / sqrt((double)D), want.p, Hq * D,
+                   D, nullptr);
+  printf("  splits %lld\n", (long long)splits);
+  check_close("decode attention", out.p, want.p, B * Hq * D);
+  // tighter: attention outputs are averages (|o| < 1 here), so a dropped or doubled token
+  // shows as an error of ~1/kv_len; rounding P to bf16 stays well below 1/256
+  float worst = 0.f;
+  for (int64_t i = 0; i < B * Hq * D; ++i) {
+    const float w = bf2f(want[i]);
+    worst = fmaxf(worst, fabsf(bf2f(out[i]) - w) / (1.f / 256 + fabsf(w) / 128));
+  }
+  printf("  max |err| / (1/256 + |want|/128) = %.3f\n", worst);
+  failures += !(worst <= 1.f);
+}
+
 static void case_index(int64_t B) {
   printf("index helpers B=%lld\n", (long long)B);
   Paged pg = make_paged(B, 16, 0, 100, 0, 9);
@@ -423,6 +480,13 @@ int main(int argc, char** argv) {
     case_norm(6, 4096);
   }
   if (all || c == "index") case_index(40);
+  if (all || c == "attn") {
+    case_attn_decode(3, 8, 2, 128, 16, 1, 90, 1);     // one work group per request
+    case_attn_decode(3, 8, 2, 128, 16, 100, 400, 3);  // 3 splits + merge (some empty)
+    case_attn_decode(2, 4, 4, 64, 4, 0, 50, 2);       // G = 1, page 4, an empty request possible
+    case_attn_decode(2, 6, 1, 256, 8, 30, 300, 0);    // G = 6, D = 256, library's split count
+    case_attn_decode(2, 16, 1, 128, 5, 20, 700, 5);   // G = 16, page size 5
+  }
   if (all || c == "qkfused") {
     case_qk_fused(5, 4, 2, 128);  // fused kernel
     case_qk_fused(3, 4, 2, 64);   // D != 128: separate-kernel path

@@ -4,7 +4,8 @@
 //
 // Emulated: thread/block indices, __shared__ (function-local statics: blocks run one after
 // another), __syncthreads (block barrier), DPP row_ror / quad_perm, readlane, readfirstlane
-// (wave barriers), the fp builtins used, hipLaunchKernelGGL and the few runtime calls made.
+// (wave barriers), ballot, ds_bpermute, MFMA 16x16x32 bf16, ds_read_b64_tr_b16 (wave-wide
+// gathers), the fp builtins used, hipLaunchKernelGGL and the few runtime calls made.
 #pragma once
 
 #include <barrier>
@@ -52,6 +53,8 @@ struct Wave {
   std::barrier<> bar{64};
   uint32_t xchg[64];
   bool live[64] = {};
+  uint16_t ma[64][8], mb[64][8];  // MFMA operands of every lane
+  const void* addr[64];           // LDS addresses of a transpose read
 };
 struct Ctx {
   dim3 tid, bid, bdim, gdim;
@@ -102,6 +105,71 @@ inline int readfirstlane(int v) {
   return (int)r;
 }
 
+inline uint64_t ballot(bool v) {
+  Wave* w = ctx->wave;
+  w->xchg[ctx->lane] = v ? 1u : 0u;
+  w->bar.arrive_and_wait();
+  uint64_t r = 0;
+  for (int l = 0; l < 64; ++l) r |= (uint64_t)(w->xchg[l] & 1u) << l;
+  w->bar.arrive_and_wait();
+  return r;
+}
+
+inline int bpermute(int addr, int v) { return (int)exchange_read((uint32_t)v, (addr >> 2) & 63); }
+
+inline float bf16_bits_to_float(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+// v_mfma_f32_16x16x32_bf16: lane l supplies A[l%16][8(l/16)+j] and B[8(l/16)+j][l%16] and
+// receives C[4(l/16)+i][l%16]; fp32 products of bf16 values are exact, summed in fp32.
+template <typename VA, typename VB, typename VC>
+VC mfma_16x16x32_bf16(VA a, VB b, VC c, int, int, int) {
+  static_assert(sizeof(VA) == 16 && sizeof(VB) == 16 && sizeof(VC) == 16, "operand sizes");
+  Wave* w = ctx->wave;
+  const int lane = ctx->lane;
+  memcpy(w->ma[lane], &a, 16);
+  memcpy(w->mb[lane], &b, 16);
+  w->bar.arrive_and_wait();
+  float cf[4];
+  memcpy(cf, &c, 16);
+  const int col = lane % 16;
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * (lane / 16) + i;
+    float acc = cf[i];
+    for (int k = 0; k < 32; ++k)
+      acc += bf16_bits_to_float(w->ma[row + 16 * (k / 8)][k % 8]) *
+             bf16_bits_to_float(w->mb[col + 16 * (k / 8)][k % 8]);
+    cf[i] = acc;
+  }
+  w->bar.arrive_and_wait();
+  VC r;
+  memcpy(&r, cf, 16);
+  return r;
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, output lane r element j is element r%4 of
+// the 8 bytes addressed by lane 4j + r/4 of the group.
+template <typename P>
+auto ds_read_tr16_b64(P p) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  Wave* w = ctx->wave;
+  const int lane = ctx->lane;
+  w->addr[lane] = (const void*)p;
+  w->bar.arrive_and_wait();
+  const int g = lane / 16, r = lane % 16;
+  s4 out;
+  for (int j = 0; j < 4; ++j) {
+    const uint16_t* src = (const uint16_t*)w->addr[16 * g + 4 * j + r / 4];
+    out[j] = (short)src[r % 4];
+  }
+  w->bar.arrive_and_wait();
+  return out;
+}
+
 template <typename K, typename... A>
 void launch(K kernel, dim3 grid, dim3 block, A... args) {
   const unsigned nt = block.x * block.y * block.z;
@@ -116,7 +184,7 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
       ths.emplace_back([&, t]() {
         Ctx c;
         c.tid = dim3(t, 0, 0);
-        c.bid = dim3(b, 0, 0);
+        c.bid = dim3(b % grid.x, (b / grid.x) % grid.y, b / (grid.x * grid.y));
         c.bdim = block;
         c.gdim = grid;
         c.lane = t & 63;
@@ -143,9 +211,15 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 #define __builtin_amdgcn_readlane emu::readlane
 #define __builtin_amdgcn_readfirstlane emu::readfirstlane
 #define __builtin_amdgcn_exp2f exp2f
+#define __builtin_amdgcn_ballot_w64 emu::ballot
+#define __builtin_amdgcn_ds_bpermute emu::bpermute
+#define __builtin_amdgcn_mfma_f32_16x16x32_bf16 emu::mfma_16x16x32_bf16
+#define __builtin_amdgcn_ds_read_tr16_b64_v4i16 emu::ds_read_tr16_b64
 #define __builtin_amdgcn_rcpf(x) (1.0f / (x))
 #define hipLaunchKernelGGL(k, g, b, shm, st, ...) emu::launch(k, dim3(g), dim3(b), __VA_ARGS__)
 
 inline float __uint_as_float(unsigned u) { float f; memcpy(&f, &u, 4); return f; }
+inline int min(int a, int b) { return a < b ? a : b; }
+inline int max(int a, int b) { return a > b ? a : b; }
 inline float rsqrtf(float x) { return 1.0f / sqrtf(x); }
 inline unsigned __umulhi(unsigned a, unsigned b) { return (unsigned)(((unsigned long long)a * b) >> 32); }

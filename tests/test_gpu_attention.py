@@ -1,0 +1,163 @@
+"""GPU parity of paged attention (flashinfer's decode and prefill wrappers) against the float64
+oracle: bf16 outputs within 1e-2 relative / 2e-2 absolute (RTOL/ATOL in tests/_util.py), plus
+tighter structural checks (uniform keys give the exact mean of the visible v rows, so a dropped
+or extra position shows), graph capture with re-planned page tables, and the decode
+configuration at full size (Qwen3-8B, 256 sequences, contexts U[128, 4096])."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from pie_amd import attention
+from pie_amd import workloads as wl
+from tests._util import assert_bf16_close
+
+pytestmark = pytest.mark.gpu
+N = oracle.to_np
+WS_BYTES = 128 * 1024 * 1024  # Pie's workspace (llama3.py:230-232)
+
+
+def _workspace(dev):
+    return torch.zeros(WS_BYTES, dtype=torch.uint8, device=dev)
+
+
+def _decode(dev, a, splits=None, out=None):
+    pb, lay = a["batch"], a["layout"]
+    w = attention.BatchDecodeWithPagedKVCacheWrapper(_workspace(dev), lay)
+    w.plan(pb.kv_indptr.to(dev), pb.kv_indices.to(dev), pb.kv_last_page_len.to(dev),
+           a["Hq"], a["Hkv"], a["D"], pb.page_size, pos_encoding_mode="NONE",
+           q_data_type=torch.bfloat16)
+    if splits is not None:
+        w._plan["splits"] = splits
+    o = w.run(a["q"].to(dev), a["cache"].to(dev), out=out)
+    torch.cuda.synchronize()
+    return o
+
+
+def _want(a, custom=None):
+    pb = a["batch"]
+    return oracle.attention(N(a["q"]), N(a["cache"]), N(pb.qo_indptr), N(pb.kv_indptr),
+                            N(pb.kv_indices), N(pb.kv_last_page_len), custom_mask=custom,
+                            layout=a["layout"])
+
+
+def _tight(got, want, what):
+    """|err| <= 1/256 + |want|/128: averages of N(0,1) rows rounded once to bf16."""
+    g = oracle.bf16_to_f32(N(got) if isinstance(got, torch.Tensor) else got).astype(np.float64)
+    w = oracle.bf16_to_f32(want).astype(np.float64)
+    r = np.abs(g - w) / (1 / 256 + np.abs(w) / 128)
+    assert r.max() <= 1.0, f"{what}: worst error {r.max():.3f} of the bound at {np.unravel_index(r.argmax(), r.shape)}"
+
+
+@pytest.mark.parametrize("layout", ["NHD", "HND"])
+@pytest.mark.parametrize("Hq,Hkv,D,P", [(32, 8, 128, 16), (8, 8, 64, 16), (16, 2, 256, 8),
+                                        (28, 4, 128, 5), (16, 1, 128, 32)])
+@pytest.mark.parametrize("splits", [None, 1, 3])
+def test_decode_vs_oracle(dev, layout, Hq, Hkv, D, P, splits):
+    print(f"decode Hq={Hq} Hkv={Hkv} D={D} P={P} layout={layout} splits={splits}", flush=True)
+    g = torch.Generator().manual_seed(Hq * 7 + D + P)
+    ctx = torch.randint(0, 700, (9,), generator=g).to(torch.int32)
+    ctx[0] = 0  # a request whose only kv token is the new one
+    a = wl.attn_batch(ctx, torch.ones(9, dtype=torch.int32), Hq=Hq, Hkv=Hkv, D=D, page_size=P,
+                      pool_pages=int(((ctx + P) // P).sum()) + 3, seed=int(ctx.sum()) % 1000,
+                      layout=layout)
+    got = _decode(dev, a, splits)
+    want = _want(a)
+    assert_bf16_close(N(got), want, what="decode")
+    _tight(got, want, "decode")
+
+
+def test_decode_uniform_keys_average_visible_rows(dev):
+    """Every key equal: the output is the plain mean of exactly the request's kv_len v rows."""
+    a = wl.attn_batch(torch.tensor([0, 15, 16, 17, 300, 511]), torch.ones(6, dtype=torch.int32),
+                      Hq=8, Hkv=2, D=128, page_size=16, seed=60)
+    pb = a["batch"]
+    a["cache"][:, 0] = a["cache"][0, 0, 0, 0]  # one k row everywhere
+    a["cache"][:, 1] = wl.normal(a["cache"][:, 1].shape, 61, 0.0, 1.0)
+    for splits in (1, 4):
+        got = oracle.bf16_to_f32(N(_decode(dev, a, splits))).astype(np.float64)
+        for b in range(6):
+            L = int(pb.seq_lens[b])
+            pages = pb.kv_indices[int(pb.kv_indptr[b]):int(pb.kv_indptr[b + 1])].long()
+            v = a["cache"][pages, 1].to(torch.float64).reshape(-1, 2, 128)[:L]  # [L, Hkv, D]
+            mean = v.mean(0).repeat_interleave(4, 0).numpy()
+            assert np.abs(got[b] - mean).max() <= 1 / 256 + np.abs(mean).max() / 128, \
+                f"request {b} (kv_len {L}) splits {splits}"
+
+
+def test_decode_graph_replay_with_new_tables(dev):
+    """Pie's graph mode: plan once on dummy one-page tables, capture, then replay after copying
+    new page tables and lengths into the fixed buffers (llama3.py:340-414, :905-950)."""
+    B, Hq, Hkv, D, P = 16, 32, 8, 128, 16
+    pool = 16 * 64
+    cache = wl.normal((pool + 1, 2, P, Hkv, D), 70).to(dev)
+    ib = torch.zeros(B + 1, dtype=torch.int32, device=dev)
+    xb = torch.zeros(pool + 1, dtype=torch.int32, device=dev)
+    lb = torch.zeros(B, dtype=torch.int32, device=dev)
+    w = attention.BatchDecodeWithPagedKVCacheWrapper(_workspace(dev), "NHD", use_cuda_graph=True,
+                                                     paged_kv_indptr_buffer=ib,
+                                                     paged_kv_indices_buffer=xb,
+                                                     paged_kv_last_page_len_buffer=lb)
+    ib.copy_(torch.arange(B + 1, dtype=torch.int32))
+    lb.fill_(1)
+    xb[:B].fill_(pool)
+    w.plan(ib, xb, lb, Hq, Hkv, D, P, q_data_type=torch.bfloat16)
+    q = torch.zeros((B, Hq, D), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=dev)
+    w.run(q, cache, out=out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        w.run(q, cache, out=out)
+    g = torch.Generator().manual_seed(71)
+    for rep in range(3):
+        ctx = torch.randint(1, 64 * P - 1, (B,), generator=g).to(torch.int32)
+        pb = wl.paged_batch(ctx, torch.ones(B, dtype=torch.int32), P, pool, 72 + rep)
+        ib.copy_(pb.kv_indptr)
+        xb[: pb.kv_indices.numel()].copy_(pb.kv_indices)
+        lb.copy_(pb.kv_last_page_len)
+        q.copy_(wl.normal((B, Hq, D), 73 + rep))
+        graph.replay()
+        torch.cuda.synchronize()
+        a = {"q": q.cpu(), "cache": cache.cpu(), "batch": pb, "layout": "NHD"}
+        want = _want(a)
+        assert_bf16_close(N(out), want, what=f"replay {rep}")
+        _tight(out, want, f"replay {rep}")
+        # eager work between replays
+        torch.cuda.synchronize()
+
+
+def test_decode_full_config_sampled(dev):
+    """Configuration: Qwen3-8B decode attention, 256 sequences, contexts U[128, 4096] (+1 new
+    token), cache ~2.2 GB. The oracle checks 24 sampled requests against the full output."""
+    a = wl.attn_decode_cfg()
+    pb = a["batch"]
+    got = N(_decode(dev, a))
+    cache = N(a["cache"])
+    pick = np.random.default_rng(0).choice(pb.seq_lens.numel(), 24, replace=False)
+    for b in pick:
+        b = int(b)
+        ind = pb.kv_indices[int(pb.kv_indptr[b]):int(pb.kv_indptr[b + 1])]
+        want = oracle.attention(N(a["q"][b:b + 1]), cache, np.array([0, 1], np.int32),
+                                np.array([0, ind.numel()], np.int32), N(ind),
+                                N(pb.kv_last_page_len[b:b + 1]))
+        assert_bf16_close(got[b:b + 1], want, what=f"request {b}")
+        _tight(got[b:b + 1], want, f"request {b}")
+
+
+def test_decode_rejects_bad_input(dev):
+    a = wl.attn_batch([5], [1], Hq=8, Hkv=2, D=128, page_size=16, seed=80)
+    pb = a["batch"]
+    w = attention.BatchDecodeWithPagedKVCacheWrapper(_workspace(dev), "NHD")
+    with pytest.raises(RuntimeError):
+        w.run(a["q"].to(dev), a["cache"].to(dev))  # before plan
+    w.plan(pb.kv_indptr.to(dev), pb.kv_indices.to(dev), pb.kv_last_page_len.to(dev), 8, 2, 128, 16)
+    with pytest.raises(ValueError):
+        w.run(a["q"].to(dev)[:, :4], a["cache"].to(dev))  # wrong head count
+    with pytest.raises(ValueError):
+        w.run(a["q"].to(dev).float(), a["cache"].to(dev))
+    with pytest.raises(NotImplementedError):
+        w.plan(pb.kv_indptr.to(dev), pb.kv_indices.to(dev), pb.kv_last_page_len.to(dev), 8, 2,
+               128, 16, pos_encoding_mode="ROPE_LLAMA")

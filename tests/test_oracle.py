@@ -438,3 +438,125 @@ def test_rope_cos_sin_table_matches_frequency_rope(interleave):
     pos2[0] = 600
     oq, _ = oracle.rope_cos_sin(N(q), N(k), pos2, cs, interleave)
     assert_bits_equal(oq[0], N(q)[0])
+
+
+# ----------------------------------------------------------------------------- paged attention
+def _gather_kv(cache, pb, b, layout="NHD"):
+    """Request b's k, v as float64 [kv_len, Hkv, D], read page by page (brute force)."""
+    P = pb.page_size
+    kv_len = int(pb.seq_lens[b])
+    pages = pb.kv_indices[int(pb.kv_indptr[b]):int(pb.kv_indptr[b + 1])].tolist()
+    c = cache.to(torch.float64)
+    rows_k, rows_v = [], []
+    for t in range(kv_len):
+        pg, sl = pages[t // P], t % P
+        if layout == "NHD":
+            rows_k.append(c[pg, 0, sl]); rows_v.append(c[pg, 1, sl])
+        else:
+            rows_k.append(c[pg, 0, :, sl]); rows_v.append(c[pg, 1, :, sl])
+    return torch.stack(rows_k), torch.stack(rows_v)
+
+
+def _sdpa_reference(a, custom=None):
+    """torch-CPU scaled_dot_product_attention in float64, one request at a time, with the
+    causal window written as an explicit boolean mask (or the custom mask)."""
+    pb, q = a["batch"], a["q"].to(torch.float64)
+    G = a["Hq"] // a["Hkv"]
+    out = torch.zeros_like(q)
+    moff = 0
+    for b in range(pb.seq_lens.numel()):
+        q0, q1 = int(pb.qo_indptr[b]), int(pb.qo_indptr[b + 1])
+        kv_len, qo_len = int(pb.seq_lens[b]), q1 - q0
+        if qo_len == 0 or kv_len == 0:
+            continue
+        k, v = _gather_kv(a["cache"], pb, b, a["layout"])
+        if custom is None:
+            m = torch.tensor([[t <= kv_len - qo_len + i for t in range(kv_len)] for i in range(qo_len)])
+        else:
+            m = torch.as_tensor(custom[moff:moff + qo_len * kv_len]).view(qo_len, kv_len).bool()
+            moff += qo_len * kv_len
+        k = k.repeat_interleave(G, dim=1).transpose(0, 1)  # [Hq, kv, D]
+        v = v.repeat_interleave(G, dim=1).transpose(0, 1)
+        o = F.scaled_dot_product_attention(q[q0:q1].transpose(0, 1), k, v, attn_mask=m)
+        o = torch.where(m.any(1)[None, :, None], o, torch.zeros_like(o))  # empty rows -> 0
+        out[q0:q1] = o.transpose(0, 1)
+    return out
+
+
+def _oracle_attn(a, custom=None, **kw):
+    pb = a["batch"]
+    return oracle.attention(N(a["q"]), N(a["cache"]), N(pb.qo_indptr), N(pb.kv_indptr),
+                            N(pb.kv_indices), N(pb.kv_last_page_len), custom_mask=custom,
+                            layout=a["layout"], **kw)
+
+
+@pytest.mark.parametrize("layout", ["NHD", "HND"])
+def test_attention_vs_torch_sdpa(layout):
+    # decode rows, a chunked prefill over cached context, a fresh prefill, an empty request
+    a = wl.attn_batch([37, 0, 5, 60, 0], [1, 19, 12, 3, 0], Hq=8, Hkv=2, D=64, page_size=16,
+                      seed=3, layout=layout)
+    want = _sdpa_reference(a).to(torch.float32)
+    got = oracle.bf16_to_f32(_oracle_attn(a))
+    assert np.abs(got - want.numpy()).max() <= 2 ** -8 * np.abs(want.numpy()).max() + 1e-6
+
+
+def test_attention_square_causal_is_torch_is_causal():
+    # kv_len == qo_len: the window t <= i is torch's own is_causal definition
+    a = wl.attn_batch([0], [23], Hq=4, Hkv=4, D=32, page_size=4, seed=5)
+    k, v = _gather_kv(a["cache"], a["batch"], 0)
+    q = a["q"].to(torch.float64).transpose(0, 1)
+    want = F.scaled_dot_product_attention(q, k.transpose(0, 1), v.transpose(0, 1), is_causal=True)
+    got = oracle.bf16_to_f32(_oracle_attn(a))
+    np.testing.assert_allclose(got, want.transpose(0, 1).numpy(), rtol=2 ** -8, atol=1e-6)
+
+
+def test_attention_custom_mask_vs_sdpa_and_causal():
+    a = wl.attn_batch([9, 30], [7, 4], Hq=4, Hkv=2, D=32, page_size=8, seed=7)
+    pb = a["batch"]
+    g = torch.Generator().manual_seed(8)
+    blocks, causal = [], []
+    for b in range(2):
+        qo, kv = int(pb.lens[b]), int(pb.seq_lens[b])
+        blocks.append((torch.rand(qo, kv, generator=g) < 0.6).flatten())
+        causal.append(torch.tensor([[t <= kv - qo + i for t in range(kv)] for i in range(qo)]).flatten())
+    mask = torch.cat(blocks)
+    mask[:5] = False  # row 0 of request 0 partly masked; fully-masked rows give 0
+    want = _sdpa_reference(a, mask.numpy()).to(torch.float32)
+    got = oracle.bf16_to_f32(_oracle_attn(a, mask.numpy()))
+    np.testing.assert_allclose(got, want.numpy(), rtol=2 ** -8, atol=1e-6)
+    # the causal window written as a custom mask is the default behaviour, bit for bit
+    assert_bits_equal(_oracle_attn(a, torch.cat(causal).numpy()), _oracle_attn(a), "causal mask")
+
+
+def test_attention_closed_forms():
+    # one visible position: output is that v row exactly; lse is the scaled score
+    a = wl.attn_batch([0], [1], Hq=2, Hkv=1, D=16, page_size=4, seed=9)
+    out, lse = _oracle_attn(a, return_lse=True)
+    k, v = _gather_kv(a["cache"], a["batch"], 0)
+    assert_bits_equal(out[0], N(v[0].to(torch.bfloat16).repeat(2, 1)), "single position")
+    s = (a["q"][0].to(torch.float64) * k[0]).sum(-1) / 4.0
+    np.testing.assert_allclose(lse[0], s.numpy(), rtol=1e-12)
+    # identical keys: uniform weights, output = mean of v, lse = s + log(n)
+    a = wl.attn_batch([40], [1], Hq=1, Hkv=1, D=16, page_size=8, seed=10)
+    pb = a["batch"]
+    for pg in pb.kv_indices.tolist():
+        a["cache"][pg, 0] = a["cache"][pb.kv_indices[0], 0, 0]
+    out, lse = _oracle_attn(a, return_lse=True)
+    k, v = _gather_kv(a["cache"], pb, 0)
+    want = v[:, 0].mean(0)
+    np.testing.assert_allclose(oracle.bf16_to_f32(out[0, 0]), want.numpy(), rtol=2 ** -8, atol=1e-7)
+    s = float((a["q"][0, 0].to(torch.float64) * k[0, 0]).sum()) / 4.0
+    assert abs(lse[0, 0] - (s + math.log(41))) < 1e-9
+
+
+def test_attention_page_permutation_invariant():
+    # moving pages (data and table entry together) does not change the result
+    a = wl.attn_batch([50, 17], [3, 2], Hq=4, Hkv=2, D=32, page_size=4, seed=11)
+    pb = a["batch"]
+    base = _oracle_attn(a)
+    perm = torch.randperm(a["cache"].shape[0], generator=torch.Generator().manual_seed(12))
+    cache2 = torch.empty_like(a["cache"])
+    cache2[perm] = a["cache"]
+    a2 = dict(a, cache=cache2)
+    pb.kv_indices = perm[pb.kv_indices.long()].to(torch.int32)
+    assert_bits_equal(_oracle_attn(a2), base, "page permutation")
