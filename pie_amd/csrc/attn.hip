@@ -84,14 +84,33 @@ __device__ __forceinline__ int64_t kv_offset(const PagedKV& kv, int page0, int t
 }
 
 constexpr int kTileTokens = 32;  // kv tokens per wave iteration (two 16-token MFMA subtiles)
-constexpr int kPad = 16;         // LDS row padding (elements) against bank conflicts
+
+// XOR swizzle of the 16-byte chunks of LDS row r (rows of D bf16, no padding): the 16 rows one
+// transpose read touches land on distinct chunks, so its 64 lanes hit every bank at most twice.
+template <int D>
+__device__ __forceinline__ int chunk_swizzle(int r) {
+  return D == 64 ? (r >> 1) & 7 : r & 15;
+}
+
+// Wait until this wave's LDS reads have returned (a transpose read must finish before a load
+// into the same LDS tile is issued).
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt((63 << 14) | (0 << 8) | (7 << 4) | 15);
+}
+
+// Wait until at most n vector-memory operations of this wave are outstanding (loads into LDS
+// included); exp and lgkm counters are not waited on.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(((N >> 4) << 14) | (15 << 8) | (7 << 4) | (N & 15));
+}
 
 // One wave's running state for 16 query rows over a stream of 32-token kv tiles.
 template <int D>
 struct WaveAttn {
   static constexpr int NS = D / 32;  // MFMA k-steps over the head dim
   static constexpr int NB = D / 16;  // 16-dim output blocks
-  static constexpr int PITCH = D + kPad;
   u32x4_t qb[NS];     // B operand: query row n, dims 8(4s+g)..+8
   f32x4_t o[NB];      // C layout: rows 4g+i, dim 16nb+n
   float m;            // running max (exp2 domain) of row n, same in all four lane groups
@@ -104,10 +123,29 @@ struct WaveAttn {
     l = 0.f;
   }
 
-  // One 32-token tile: ka = K A-operands of the two subtiles (already loaded), ok[u][i] says
-  // whether token 16u+4g+i is visible to row n, vt = the tile's V rows in LDS ([32][PITCH]).
-  __device__ __forceinline__ void tile(const u32x4_t (&ka)[2][NS], const bool (&ok)[2][4],
-                                       const uint16_t* vt, float scale_log2, int lane) {
+  // The PV B-operands of a 32-token tile from the wave's LDS tile vt ([32][D], chunk-swizzled):
+  // for each 16-dim block, lane 16g + 4j + q of two transpose reads addresses row (16h + 4g + j),
+  // dims 16nb + 4q..+3, which sit in logical chunk 2nb + q/2 of that row.
+  __device__ __forceinline__ void read_v(const uint16_t* vt, int lane, u32x4_t (&vb)[NB]) const {
+    const int g = lane >> 4, j = (lane >> 2) & 3, q = lane & 3;
+    const int r0 = 4 * g + j, r1 = r0 + 16;
+    const uint16_t* b0 = vt + r0 * D + 4 * (q & 1);
+    const uint16_t* b1 = vt + r1 * D + 4 * (q & 1);
+    const int z0 = chunk_swizzle<D>(r0), z1 = chunk_swizzle<D>(r1);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int lc = 2 * nb + (q >> 1);
+      const uint2 lo = lds_read_tr16(b0 + 8 * (lc ^ z0));
+      const uint2 hi = lds_read_tr16(b1 + 8 * (lc ^ z1));
+      vb[nb] = u32x4_t{lo.x, lo.y, hi.x, hi.y};
+    }
+  }
+
+  // One 32-token tile: ka = K A-operands of the two subtiles, bit 16u+t of vis[u] says whether
+  // token 16u+t is visible, vb = the V B-operands (read_v).
+  __device__ __forceinline__ void tile(const u32x4_t (&ka)[2][NS], const uint64_t (&vis)[2],
+                                       const u32x4_t (&vb)[NB], float scale_log2, int lane) {
+    const int g = lane >> 4;
     float s[2][4];
     #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -115,7 +153,7 @@ struct WaveAttn {
       #pragma unroll
       for (int st = 0; st < NS; ++st) acc = mfma_16x16x32(ka[u][st], qb[st], acc);
       #pragma unroll
-      for (int i = 0; i < 4; ++i) s[u][i] = ok[u][i] ? acc[i] * scale_log2 : -INFINITY;
+      for (int i = 0; i < 4; ++i) s[u][i] = ((vis[u] >> (4 * g + i)) & 1ull) ? acc[i] * scale_log2 : -INFINITY;
     }
     float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
@@ -132,25 +170,17 @@ struct WaveAttn {
     l = l * alpha + psum;
     m = m_new;
     // O rows 4g+i take the factor of row 4g+i (held by lane 4g+i of every group)
-    const int g = lane >> 4;
     float a[4];
     #pragma unroll
     for (int i = 0; i < 4; ++i) a[i] = lane_read(alpha, 4 * g + i);
     const u32x4_t pa = {pack_bf2(p[0][0], p[0][1]), pack_bf2(p[0][2], p[0][3]),
                         pack_bf2(p[1][0], p[1][1]), pack_bf2(p[1][2], p[1][3])};
-    // tr16 source addresses: lane 16g + 4j + q reads row (16h + 4g + j), dims 16nb + 4q..+3
-    const int j = (lane >> 2) & 3, q = lane & 3;
-    const uint16_t* r0 = vt + (4 * g + j) * PITCH + 4 * q;
-    const uint16_t* r1 = r0 + 16 * PITCH;
-    #pragma unroll
+#pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      const uint2 lo = lds_read_tr16(r0 + 16 * nb);
-      const uint2 hi = lds_read_tr16(r1 + 16 * nb);
-      const u32x4_t vb = {lo.x, lo.y, hi.x, hi.y};
       f32x4_t c = o[nb];
       #pragma unroll
       for (int i = 0; i < 4; ++i) c[i] *= a[i];
-      o[nb] = mfma_16x16x32(pa, vb, c);
+      o[nb] = mfma_16x16x32(pa, vb[nb], c);
     }
   }
 
@@ -158,6 +188,59 @@ struct WaveAttn {
   __device__ __forceinline__ float row_sum(int lane) const {
     float t = l + lane_read(l, lane ^ 16);
     return t + lane_read(t, lane ^ 32);
+  }
+};
+
+// Page ids of a window of logical pages, staged in LDS once per work group.
+constexpr int kPageWin = 512;
+
+// Element offset of token t (its logical page lp = t / P lies in the staged window starting at
+// lp0) for kv head h, branch-free; ok = false (and page 0 addressed) if the page id is out of
+// range.
+__device__ __forceinline__ uint64_t kv_offset_lds(const PagedKV& kv, const int32_t* ptab, int lp0,
+                                                  int t, int h, bool& ok) {
+  const int lp = (int)kv.pdiv.div((uint32_t)t);
+  const int slot = t - lp * kv.page_size;
+  const int page = ptab[lp - lp0];
+  ok = (unsigned)page < (unsigned)kv.num_pages;
+  const uint32_t pg = ok ? (uint32_t)page : 0u;
+  return (uint64_t)pg * (uint32_t)kv.page_stride + (uint64_t)(uint32_t)slot * (uint32_t)kv.slot_stride +
+         (uint64_t)(uint32_t)h * (uint32_t)kv.head_stride;
+}
+
+// One wave's loads for a 32-token tile: the K MFMA operands of both subtiles with their
+// visibility ballots (registers), and the V rows, which go from HBM straight into the wave's
+// LDS tile ([32][D], chunk-swizzled) without passing through registers. Tokens at or past `end`
+// and tokens on out-of-range pages are invisible; their loads are clamped to valid addresses
+// (an invisible row gets probability 0).
+template <int D>
+struct KVTile {
+  static constexpr int NS = D / 32, CH = D / 8, RPI = 64 / CH, NVL = kTileTokens / RPI;
+  u32x4_t ka[2][NS];
+  uint64_t vis[2];
+
+  __device__ __forceinline__ void load(const PagedKV& kv, const int32_t* ptab, int lp0, int t0,
+                                       int end, int kvh, int lane, uint16_t* vt) {
+    const int n = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < NVL; ++i) {
+      const int r = RPI * i + lane / CH;
+      bool ok;
+      const uint64_t off = kv_offset_lds(kv, ptab, lp0, min(t0 + r, end - 1), kvh, ok);
+      const int lc = (lane % CH) ^ chunk_swizzle<D>(r);
+      __builtin_amdgcn_global_load_lds(kv.v + off + 8 * lc,
+                                       (__attribute__((address_space(3))) void*)(vt + RPI * i * D),
+                                       16, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int tok = t0 + 16 * u + n;
+      bool ok;
+      const uint16_t* kp = kv.k + kv_offset_lds(kv, ptab, lp0, min(tok, end - 1), kvh, ok);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) ka[u][s] = ld16v(kp + 8 * (4 * s + g));
+      vis[u] = __builtin_amdgcn_ballot_w64(tok < end && ok);
+    }
   }
 };
 
@@ -183,15 +266,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     float scale_log2, int splits, uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs,
     float* __restrict__ part_o, float* __restrict__ part_lse) {
   using W = WaveAttn<D>;
-  constexpr int PITCH = W::PITCH;
-  constexpr int kVtile = kTileTokens * PITCH;                     // elements per wave
+  constexpr int kVtile = kTileTokens * D;  // elements of one wave's V tile
   constexpr int kSmem = (4 * kVtile * 2 > 4 * 16 * (D + 2) * 4) ? 4 * kVtile * 2 : 4 * 16 * (D + 2) * 4;
   __shared__ __attribute__((aligned(16))) char smem[kSmem];
 
   const int slot = blockIdx.x;
   const int b = slot / splits;
   const int kvh = blockIdx.y;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int kv_len = kv_length(kv, b);
   int kv0, kv1;
@@ -211,41 +293,49 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     }
   }
   uint16_t* vt = reinterpret_cast<uint16_t*>(smem) + w * kVtile;
-  constexpr int CH = D / 8;              // 16-byte chunks per row
-  constexpr int RPI = 64 / CH;           // rows per load instruction
-  constexpr int NVL = kTileTokens / RPI; // V load instructions per tile
-  for (int t0 = kv0 + kTileTokens * w; t0 < kv1; t0 += 4 * kTileTokens) {
-    u32x4_t ka[2][W::NS];
-    bool ok[2][4];
-    #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int tok = t0 + 16 * u + n;
-      const int64_t off = kv_offset(kv, page0, min(tok, kv1 - 1), kvh);
-      const uint16_t* kp = kv.k + (off < 0 ? 0 : off);
-      #pragma unroll
-      for (int s = 0; s < W::NS; ++s) ka[u][s] = ld16v(kp + 8 * (4 * s + g));
-      // token 16u+n is visible if inside [t0, kv1) with a valid page (decode has no causal
-      // cut: the query is the last position); row n's lanes need tokens 16u+4g+i
-      const uint64_t vis = __builtin_amdgcn_ballot_w64(tok < kv1 && off >= 0);
-      #pragma unroll
-      for (int i = 0; i < 4; ++i) ok[u][i] = (vis >> (4 * g + i)) & 1ull;
+  __shared__ int32_t ptab[kPageWin];
+  // kv tokens per page window: the pages any such run spans fit in kPageWin
+  const int win = max(kTileTokens, (kPageWin - 2) * kv.page_size / kTileTokens * kTileTokens);
+  for (int wt0 = kv0; wt0 < kv1; wt0 += win) {
+    const int wt1 = min(kv1, wt0 + win);
+    const int lp0 = (int)kv.pdiv.div((uint32_t)wt0);
+    const int npg = (int)kv.pdiv.div((uint32_t)(wt1 - 1)) - lp0 + 1;
+    __syncthreads();  // the previous window's lookups are done
+    for (int i = threadIdx.x; i < npg; i += 256) ptab[i] = kv.indices[page0 + lp0 + i];
+    __syncthreads();
+    // each wave takes every fourth tile; the next tile's loads are issued before the current
+    // tile's MFMA/softmax work so HBM latency overlaps compute
+    // Each wave takes every fourth tile. Two tile slots alternate (no register copies, which
+    // would force a wait on the in-flight loads): the next tile's loads are issued before the
+    // current tile's MFMA/softmax work, so HBM latency overlaps compute.
+    int t0 = wt0 + kTileTokens * w;
+    if (t0 < wt1) {
+      // Two K register slots alternate (no copies, which would force waits on loads in
+      // flight); V has one LDS tile. Each step: wait for the current tile's loads, move its V
+      // from LDS into registers, issue the next tile's loads (V into the now free LDS tile),
+      // then run the current tile's MFMA/softmax work while they stream in.
+      KVTile<D> ta, tb;
+      u32x4_t vb[W::NB];
+      ta.load(kv, ptab, lp0, t0, wt1, kvh, lane, vt);
+      for (;;) {
+        wait_vmcnt<0>();
+        st.read_v(vt, lane, vb);
+        wait_lgkmcnt0();
+        const bool more_b = t0 + 4 * kTileTokens < wt1;
+        if (more_b) tb.load(kv, ptab, lp0, t0 + 4 * kTileTokens, wt1, kvh, lane, vt);
+        st.tile(ta.ka, ta.vis, vb, scale_log2, lane);
+        if (!more_b) break;
+        t0 += 4 * kTileTokens;
+        wait_vmcnt<0>();
+        st.read_v(vt, lane, vb);
+        wait_lgkmcnt0();
+        const bool more_a = t0 + 4 * kTileTokens < wt1;
+        if (more_a) ta.load(kv, ptab, lp0, t0 + 4 * kTileTokens, wt1, kvh, lane, vt);
+        st.tile(tb.ka, tb.vis, vb, scale_log2, lane);
+        if (!more_a) break;
+        t0 += 4 * kTileTokens;
+      }
     }
-    u32x4_t vv[NVL];
-    bool vok[NVL];
-    #pragma unroll
-    for (int i = 0; i < NVL; ++i) {
-      const int r = RPI * i + lane / CH;
-      const int64_t off = kv_offset(kv, page0, min(t0 + r, kv1 - 1), kvh);
-      vok[i] = off >= 0;
-      vv[i] = ld16v(kv.v + (off < 0 ? 0 : off) + 8 * (lane % CH));
-    }
-    #pragma unroll
-    for (int i = 0; i < NVL; ++i) {
-      const int r = RPI * i + lane / CH;
-      const u32x4_t z = {0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4_t*>(vt + r * PITCH + 8 * (lane % CH)) = vok[i] ? vv[i] : z;
-    }
-    st.tile(ka, ok, vt, scale_log2, lane);
   }
   const float lsum = st.row_sum(lane);
 
@@ -260,6 +350,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     #pragma unroll
     for (int i = 0; i < 4; ++i) os[(w * 16 + 4 * g + i) * D + 16 * nb + n] = st.o[nb][i];
   __syncthreads();
+  constexpr int CH = D / 8;
   for (int u = threadIdx.x; u < G * CH; u += 256) {
     const int row = u / CH, c = u % CH;
     float M = -INFINITY;

@@ -486,6 +486,7 @@ int main(int argc, char** argv) {
     case_attn_decode(2, 4, 4, 64, 4, 0, 50, 2);       // G = 1, page 4, an empty request possible
     case_attn_decode(2, 6, 1, 256, 8, 30, 300, 0);    // G = 6, D = 256, library's split count
     case_attn_decode(2, 16, 1, 128, 5, 20, 700, 5);   // G = 16, page size 5
+    case_attn_decode(2, 4, 2, 64, 1, 600, 1500, 1);   // page size 1: several page-table windows
   }
   if (all || c == "qkfused") {
     case_qk_fused(5, 4, 2, 128);  // fused kernel

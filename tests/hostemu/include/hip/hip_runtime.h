@@ -5,7 +5,7 @@
 // Emulated: thread/block indices, __shared__ (function-local statics: blocks run one after
 // another), __syncthreads (block barrier), DPP row_ror / quad_perm, readlane, readfirstlane
 // (wave barriers), ballot, ds_bpermute, MFMA 16x16x32 bf16, ds_read_b64_tr_b16 (wave-wide
-// gathers), the fp builtins used, hipLaunchKernelGGL and the few runtime calls made.
+// gathers), global_load_lds (a per-lane copy), the fp builtins used, hipLaunchKernelGGL and the few runtime calls made.
 #pragma once
 
 #include <barrier>
@@ -170,6 +170,13 @@ auto ds_read_tr16_b64(P p) {
   return out;
 }
 
+// global_load_lds_dwordx4: each lane copies `size` bytes from its own global address to
+// lds_base + offset + lane * size.
+template <typename G, typename L>
+inline void global_load_lds(G src, L lds_base, unsigned size, int offset, int) {
+  memcpy((char*)(void*)lds_base + offset + (size_t)ctx->lane * size, (const void*)src, size);
+}
+
 template <typename K, typename... A>
 void launch(K kernel, dim3 grid, dim3 block, A... args) {
   const unsigned nt = block.x * block.y * block.z;
@@ -215,6 +222,8 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 #define __builtin_amdgcn_ds_bpermute emu::bpermute
 #define __builtin_amdgcn_mfma_f32_16x16x32_bf16 emu::mfma_16x16x32_bf16
 #define __builtin_amdgcn_ds_read_tr16_b64_v4i16 emu::ds_read_tr16_b64
+#define __builtin_amdgcn_global_load_lds emu::global_load_lds
+#define __builtin_amdgcn_s_waitcnt(x) ((void)(x))
 #define __builtin_amdgcn_rcpf(x) (1.0f / (x))
 #define hipLaunchKernelGGL(k, g, b, shm, st, ...) emu::launch(k, dim3(g), dim3(b), __VA_ARGS__)
 

@@ -69,6 +69,17 @@ def test_decode_vs_oracle(dev, layout, Hq, Hkv, D, P, splits):
     _tight(got, want, "decode")
 
 
+def test_decode_page_size_one_long_context(dev):
+    """Page size 1: a 1500-token context spans several 510-page windows of the staged table."""
+    a = wl.attn_batch(torch.tensor([1499, 700, 3]), torch.ones(3, dtype=torch.int32), Hq=8, Hkv=2,
+                      D=128, page_size=1, seed=90)
+    for splits in (1, 2):
+        got = _decode(dev, a, splits)
+        want = _want(a)
+        assert_bf16_close(N(got), want, what=f"P=1 splits {splits}")
+        _tight(got, want, f"P=1 splits {splits}")
+
+
 def test_decode_uniform_keys_average_visible_rows(dev):
     """Every key equal: the output is the plain mean of exactly the request's kv_len v rows."""
     a = wl.attn_batch(torch.tensor([0, 15, 16, 17, 300, 511]), torch.ones(6, dtype=torch.int32),
