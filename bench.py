@@ -310,6 +310,25 @@ def _ops_attention(dev, run):
         q, out = q0.clone(), torch.empty_like(q0)
         return lambda: w.run(q, cache, out=out)
     res = [run(f"attn decode B=256 ctx U[128,4096] (splits {w._plan['splits']})", nbytes, make)]
+    del cache, w
+    # causal prefill over configuration 3's ragged batch: MFMA-bound, reported as TFLOP/s of
+    # the useful (causal-window) QK^T and PV flops
+    a = wl.attn_prefill_cfg()
+    pb = a["batch"]
+    cache, q0 = a["cache"].to(dev), a["q"].to(dev)
+    wp = attention.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    wp.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev),
+            pb.kv_last_page_len.to(dev), 32, 8, 128, 16, causal=True)
+    flops = wl.attn_flops(pb, 32, 128)
+
+    def make_p():
+        q, out = q0.clone(), torch.empty_like(q0)
+        return lambda: wp.run(q, cache, out=out)
+    e = run(f"attn prefill causal cfg3 T={q0.shape[0]}", wl.attn_bytes(pb, 32, 8, 128), make_p)
+    e["flops"] = flops
+    e["tflops"] = round(flops / e["us"] / 1e6, 1)
+    e["mfma_frac"] = round(flops / e["us"] / 1e6 / 2500.0, 3)
+    res.append(e)
     del cache, ws
     return res
 

@@ -292,6 +292,41 @@ int pie_hip_attention_decode(const pie_bf16* q, int64_t q_tok_stride, int64_t q_
                              pie_bf16* out, int64_t o_tok_stride, int64_t o_head_stride,
                              void* stream);
 
+
+/*
+ * Paged attention, prefill form: ragged query tokens per request (qo_indptr [B+1]), each
+ * request's query tokens being its last qo_len positions. Query token i of request b attends
+ * kv position t < kv_len when: mode 0 always (flashinfer's default, causal=False), mode 1
+ * t <= kv_len - qo_len + i (causal=True), mode 2 custom_mask[off_b + i*kv_len + t] != 0 (bytes;
+ * per request a row-major [qo_len, kv_len] block, blocks concatenated in request order, as
+ * pie/src/pie_worker/batching.py:335-386 builds it). Cache addressing, heads and scale as in
+ * the decode form. Rows that see nothing are 0.
+ * Replaces flashinfer.BatchPrefillWithPagedKVCacheWrapper.plan/.run as Pie calls them:
+ *   pie/src/pie_worker/model/llama3.py:307-309 (construction), :779-790 (plan with the custom
+ *   mask), :689 (run); API restated in pie/src/flashinfer_metal/ops.py:163-223.
+ *
+ * pie_hip_attention_prefill_plan runs on the host over host copies of qo_indptr, kv_indptr and
+ * kv_last_page_len and writes the work list (`plan`, int32 words; *num_items work groups per kv
+ * head; for mode 2 the mask block offsets at word plan[3], and *mask_bytes = the mask's size).
+ * The caller copies the plan to device memory and passes it, num_items and plan[3] to the run.
+ */
+int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
+                                   const int32_t* kv_last_page_len, int64_t batch,
+                                   int64_t page_size, int64_t num_qo_heads, int64_t num_kv_heads,
+                                   int32_t mode, int32_t* plan, int64_t plan_capacity,
+                                   int64_t* plan_words, int64_t* num_items, int64_t* mask_bytes);
+int pie_hip_attention_prefill(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                              const pie_bf16* k_cache, const pie_bf16* v_cache,
+                              int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                              int64_t num_pages, const int32_t* qo_indptr,
+                              const int32_t* kv_indptr, const int32_t* kv_indices,
+                              const int32_t* kv_last_page_len, int64_t num_qo_heads,
+                              int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                              float sm_scale, int32_t mode, const uint8_t* custom_mask,
+                              const int32_t* plan, int64_t num_items, int64_t mask_offsets_word,
+                              pie_bf16* out, int64_t o_tok_stride, int64_t o_head_stride,
+                              void* stream);
+
 #ifdef __cplusplus
 }
 #endif

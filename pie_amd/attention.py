@@ -6,6 +6,8 @@ capture plans once per batch-size bin and replays with new page tables, :340-414
 The API is flashinfer 0.6.1's, restated in pie/src/flashinfer_metal/ops.py:163-282.
 
     BatchDecodeWithPagedKVCacheWrapper   one query token per request  -> pie_hip_attention_decode
+    BatchPrefillWithPagedKVCacheWrapper  ragged query tokens, causal /
+                                         custom-mask / full visibility -> pie_hip_attention_prefill
 
 ``plan`` runs on the host and allocates nothing on the device; ``run`` launches kernels on the
 current stream and allocates only its output (unless ``out=`` is given), so it can be captured.
@@ -17,6 +19,8 @@ from __future__ import annotations
 
 import ctypes as C
 import math
+
+import numpy as np
 from typing import Optional, Tuple, Union
 
 import torch
@@ -24,7 +28,7 @@ import torch
 from . import _lib
 from .ops import _cache_desc, _check, _stream
 
-__all__ = ["BatchDecodeWithPagedKVCacheWrapper"]
+__all__ = ["BatchDecodeWithPagedKVCacheWrapper", "BatchPrefillWithPagedKVCacheWrapper"]
 
 _BF16 = torch.bfloat16
 _CUS: dict = {}
@@ -156,6 +160,130 @@ class BatchDecodeWithPagedKVCacheWrapper:
                   p["last_page_len"].data_ptr(), B, Hq, Hkv, D, P, float(p["sm_scale"]),
                   p["splits"], ws.data_ptr(), ws.numel() * ws.element_size(), out.data_ptr(),
                   out.stride(0), out.stride(1), _stream(q))
+        return out
+
+    forward = run
+
+    def end_forward(self) -> None:
+        pass
+
+
+class BatchPrefillWithPagedKVCacheWrapper:
+    """flashinfer.BatchPrefillWithPagedKVCacheWrapper: attention of ragged query tokens (the last
+    qo_len positions of each request) over the request's pages (llama3.py:307-309, :779-790,
+    :689). Visibility: the custom mask when given (Pie always passes one, batching.py:226-228),
+    else causal=True's window, else every cached position (flashinfer's default)."""
+
+    def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD",
+                 use_cuda_graph: bool = False, **_ignored) -> None:
+        if kv_layout not in ("NHD", "HND"):
+            raise ValueError(f"kv_layout must be 'NHD' or 'HND', got {kv_layout!r}")
+        if use_cuda_graph:
+            raise NotImplementedError("BatchPrefillWithPagedKVCacheWrapper: use_cuda_graph "
+                                      "(Pie captures only decode)")
+        self._workspace = float_workspace_buffer
+        self._kv_layout = kv_layout
+        self._plan = None
+
+    def plan(self, qo_indptr: torch.Tensor, paged_kv_indptr: torch.Tensor,
+             paged_kv_indices: torch.Tensor, paged_kv_last_page_len: torch.Tensor,
+             num_qo_heads: int, num_kv_heads: int, head_dim_qk: int, page_size: int,
+             head_dim_vo: Optional[int] = None, custom_mask: Optional[torch.Tensor] = None,
+             packed_custom_mask: Optional[torch.Tensor] = None, causal: bool = False,
+             pos_encoding_mode: str = "NONE", use_fp16_qk_reduction: bool = False,
+             sm_scale: Optional[float] = None, window_left: int = -1,
+             logits_soft_cap: Optional[float] = None, rope_scale: Optional[float] = None,
+             rope_theta: Optional[float] = None, q_data_type=torch.float16, kv_data_type=None,
+             non_blocking: bool = True, **_ignored) -> None:
+        name = "BatchPrefillWithPagedKVCacheWrapper.plan"
+        _unsupported(name, pos_encoding_mode, window_left, logits_soft_cap)
+        if head_dim_vo not in (None, head_dim_qk):
+            raise NotImplementedError(f"{name}: head_dim_vo {head_dim_vo} != head_dim_qk")
+        if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:
+            raise ValueError(f"{name}: num_qo_heads {num_qo_heads} is not a multiple of "
+                             f"num_kv_heads {num_kv_heads}")
+        dev = self._workspace.device
+        batch = qo_indptr.numel() - 1
+        if paged_kv_indptr.numel() != batch + 1 or paged_kv_last_page_len.numel() != batch:
+            raise ValueError(f"{name}: qo_indptr, paged_kv_indptr and paged_kv_last_page_len "
+                             "disagree on the batch size")
+        # host copies of the small index arrays (flashinfer's plan reads them on the host too)
+        qo_h = qo_indptr.to("cpu", torch.int32).contiguous()
+        kv_h = paged_kv_indptr.to("cpu", torch.int32).contiguous()
+        ll_h = paged_kv_last_page_len.to("cpu", torch.int32).contiguous()
+        mask = custom_mask
+        if mask is None and packed_custom_mask is not None:
+            bits = (packed_custom_mask.to(torch.uint8).unsqueeze(-1)
+                    >> torch.arange(8, dtype=torch.uint8, device=packed_custom_mask.device)) & 1
+            mask = bits.flatten().bool()
+        mode = 2 if mask is not None else (1 if causal else 0)
+        G = num_qo_heads // num_kv_heads
+        T = int(qo_h[-1]) if batch else 0
+        cap = 16 + 2 * (T * G // 128 + batch + 1) + 2 * batch + 2
+        plan = np.zeros(cap, dtype=np.int32)
+        words, items, mbytes = C.c_int64(0), C.c_int64(0), C.c_int64(0)
+        _lib.call("pie_hip_attention_prefill_plan", qo_h.data_ptr(), kv_h.data_ptr(), ll_h.data_ptr(),
+                  batch, page_size, num_qo_heads, num_kv_heads, mode, plan.ctypes.data, cap,
+                  C.byref(words), C.byref(items), C.byref(mbytes))
+        if mode == 2:
+            if mask.dtype not in (torch.bool, torch.uint8):
+                raise ValueError(f"{name}: custom_mask must be bool, got {mask.dtype}")
+            mask = mask.reshape(-1)
+            if mask.numel() < mbytes.value:
+                raise ValueError(f"{name}: custom_mask has {mask.numel()} entries, the batch needs "
+                                 f"{mbytes.value} (sum of qo_len * kv_len)")
+            mask = mask.to(dev).contiguous()
+        nbytes = words.value * 4
+        ws_bytes = self._workspace.numel() * self._workspace.element_size()
+        if nbytes > ws_bytes:
+            raise ValueError(f"{name}: the plan needs {nbytes} bytes of workspace, have {ws_bytes}")
+        plan_d = self._workspace.view(torch.uint8)[:nbytes].view(torch.int32)
+        plan_d.copy_(torch.from_numpy(plan[: words.value]), non_blocking=False)
+        tables = [t if t.device == dev else t.to(dev) for t in
+                  (qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len)]
+        self._plan = dict(qo_indptr=tables[0], indptr=tables[1], indices=tables[2],
+                          last_page_len=tables[3], batch=batch, T=T, Hq=num_qo_heads,
+                          Hkv=num_kv_heads, D=head_dim_qk, P=page_size, mode=mode, mask=mask,
+                          plan=plan_d, items=items.value, moff_word=int(plan[3]),
+                          sm_scale=(1.0 / math.sqrt(head_dim_qk)) if sm_scale is None else sm_scale)
+
+    begin_forward = plan
+
+    def run(self, q: torch.Tensor,
+            paged_kv_cache: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]], *args,
+            q_scale=None, k_scale=None, v_scale=None, out: Optional[torch.Tensor] = None,
+            lse: Optional[torch.Tensor] = None, return_lse: bool = False, **_ignored):
+        name = "BatchPrefillWithPagedKVCacheWrapper.run"
+        p = self._plan
+        if p is None:
+            raise RuntimeError(f"{name}: plan() must be called before run()")
+        if return_lse or lse is not None:
+            raise NotImplementedError(f"{name}: lse output")
+        if q_scale not in (None, 1.0) or k_scale not in (None, 1.0) or v_scale not in (None, 1.0):
+            raise NotImplementedError(f"{name}: quantisation scales")
+        _check(name, _BF16, q=q)
+        _check(name, torch.int32, qo_indptr=p["qo_indptr"], indptr=p["indptr"],
+               indices=p["indices"], last_page_len=p["last_page_len"])
+        T, Hq, Hkv, D = p["T"], p["Hq"], p["Hkv"], p["D"]
+        if q.dim() != 3 or tuple(q.shape) != (T, Hq, D) or q.stride(2) != 1:
+            raise ValueError(f"{name}: q must be [{T}, {Hq}, {D}] with unit inner stride, got "
+                             f"{tuple(q.shape)}")
+        kp, vp, npages, ps, ss, hs, P = _cache_desc(paged_kv_cache, self._kv_layout, Hkv, D, name)
+        if P != p["P"]:
+            raise ValueError(f"{name}: cache page size {P} != planned {p['P']}")
+        if out is None:
+            out = torch.empty((T, Hq, D), dtype=_BF16, device=q.device)
+        else:
+            _check(name, _BF16, out=out)
+            if tuple(out.shape) != (T, Hq, D) or out.stride(2) != 1:
+                raise ValueError(f"{name}: out must be [{T}, {Hq}, {D}]")
+        mask = p["mask"]
+        _lib.call("pie_hip_attention_prefill", q.data_ptr(), q.stride(0), q.stride(1), kp, vp, ps,
+                  ss, hs, npages, p["qo_indptr"].data_ptr(), p["indptr"].data_ptr(),
+                  p["indices"].data_ptr(), p["last_page_len"].data_ptr(), Hq, Hkv, D, P,
+                  float(p["sm_scale"]), p["mode"], mask.data_ptr() if mask is not None else None,
+                  p["plan"].data_ptr(), p["items"], p["moff_word"], out.data_ptr(), out.stride(0),
+                  out.stride(1), _stream(q))
         return out
 
     forward = run

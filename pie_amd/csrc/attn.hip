@@ -22,7 +22,10 @@
 // rounded to bf16 for the second product as flashinfer does; everything else is fp32.
 #include <math.h>
 
+#include <string.h>
+
 #include <algorithm>
+#include <vector>
 
 #include "common.h"
 
@@ -141,9 +144,9 @@ struct WaveAttn {
     }
   }
 
-  // One 32-token tile: ka = K A-operands of the two subtiles, bit 16u+t of vis[u] says whether
-  // token 16u+t is visible, vb = the V B-operands (read_v).
-  __device__ __forceinline__ void tile(const u32x4_t (&ka)[2][NS], const uint64_t (&vis)[2],
+  // One 32-token tile: ka = K A-operands of the two subtiles, vb = the V B-operands (read_v),
+  // bit 4u+i of vmask says whether this lane's row n sees token 16u+4g+i.
+  __device__ __forceinline__ void tile(const u32x4_t (&ka)[2][NS], uint32_t vmask,
                                        const u32x4_t (&vb)[NB], float scale_log2, int lane) {
     const int g = lane >> 4;
     float s[2][4];
@@ -153,7 +156,7 @@ struct WaveAttn {
       #pragma unroll
       for (int st = 0; st < NS; ++st) acc = mfma_16x16x32(ka[u][st], qb[st], acc);
       #pragma unroll
-      for (int i = 0; i < 4; ++i) s[u][i] = ((vis[u] >> (4 * g + i)) & 1ull) ? acc[i] * scale_log2 : -INFINITY;
+      for (int i = 0; i < 4; ++i) s[u][i] = ((vmask >> (4 * u + i)) & 1u) ? acc[i] * scale_log2 : -INFINITY;
     }
     float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
@@ -218,6 +221,12 @@ struct KVTile {
   static constexpr int NS = D / 32, CH = D / 8, RPI = 64 / CH, NVL = kTileTokens / RPI;
   u32x4_t ka[2][NS];
   uint64_t vis[2];
+
+  // Row-independent visibility in tile()'s vmask form: bit 4u+i = token 16u+4g+i.
+  __device__ __forceinline__ uint32_t vmask(int lane) const {
+    const int g = lane >> 4;
+    return (uint32_t)((vis[0] >> (4 * g)) & 15u) | ((uint32_t)((vis[1] >> (4 * g)) & 15u) << 4);
+  }
 
   __device__ __forceinline__ void load(const PagedKV& kv, const int32_t* ptab, int lp0, int t0,
                                        int end, int kvh, int lane, uint16_t* vt) {
@@ -323,7 +332,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         wait_lgkmcnt0();
         const bool more_b = t0 + 4 * kTileTokens < wt1;
         if (more_b) tb.load(kv, ptab, lp0, t0 + 4 * kTileTokens, wt1, kvh, lane, vt);
-        st.tile(ta.ka, ta.vis, vb, scale_log2, lane);
+        st.tile(ta.ka, ta.vmask(lane), vb, scale_log2, lane);
         if (!more_b) break;
         t0 += 4 * kTileTokens;
         wait_vmcnt<0>();
@@ -331,7 +340,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         wait_lgkmcnt0();
         const bool more_a = t0 + 4 * kTileTokens < wt1;
         if (more_a) ta.load(kv, ptab, lp0, t0 + 4 * kTileTokens, wt1, kvh, lane, vt);
-        st.tile(tb.ka, tb.vis, vb, scale_log2, lane);
+        st.tile(tb.ka, tb.vmask(lane), vb, scale_log2, lane);
         if (!more_a) break;
         t0 += 4 * kTileTokens;
       }
@@ -413,6 +422,166 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(int B, int Hq, int split
   #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] *= inv;
   st16(out + (int64_t)b * o_ts + (int64_t)hq * o_hs + 8 * c, pack8(acc));
+}
+
+
+// ------------------------------------------------------------------------------ prefill
+// Work item: request b, first packed query row row0 (row R = query token R / G, head R % G of
+// the kv head's group). A work group of 4 waves owns kPrefillRows rows (32 per wave, two MFMA
+// row tiles) and streams the request's kv tokens in 32-token tiles: the four waves load each K
+// and V tile cooperatively straight into LDS (global_load_lds, chunk-swizzled, double-buffered),
+// then every wave reads the K and V MFMA operands it needs into registers before the next
+// tile's loads are issued, and runs both row tiles against them.
+// Visibility: mode 0 every cached position, 1 causal (t <= kv_len - qo_len + i), 2 the custom
+// mask (bytes, per request a row-major [qo_len, kv_len] block at mask + mask_off[b]).
+constexpr int kPrefillRows = 128;
+constexpr int kPlanHeader = 16;  // plan words before the items: [0] items, [1] batch, [2] rows per item
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(
+    const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv,
+    const int32_t* __restrict__ qo_indptr, int G, float scale_log2, const int32_t* __restrict__ plan,
+    int mode, const uint8_t* __restrict__ mask, const int64_t* __restrict__ mask_off,
+    uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
+  using W = WaveAttn<D>;
+  constexpr int NS = W::NS, NB = W::NB, CH = D / 8, RPI = 64 / CH;
+  constexpr int TILE = kTileTokens * D;  // elements of one K or V tile
+  constexpr int kSmemLoop = 2 * 2 * TILE * 2;
+  constexpr int kSmemOut = kPrefillRows * D * 2;
+  constexpr int kSmem = kSmemLoop > kSmemOut ? kSmemLoop : kSmemOut;
+  __shared__ __attribute__((aligned(16))) char smem[kSmem];
+  __shared__ int32_t ptab[kPageWin];
+
+  const int32_t* item = plan + kPlanHeader + 2 * blockIdx.x;
+  const int b = item[0], row0 = item[1];
+  const int kvh = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int q0 = qo_indptr[b], qo_len = qo_indptr[b + 1] - q0;
+  const int kv_len = kv_length(kv, b);
+  const int rows = qo_len * G;
+  const int page0 = kv.indptr[b];
+
+  // this lane's query rows (row n of each of the wave's two row tiles)
+  W st[2];
+  int lim[2], tok[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    st[rt].init();
+    const int R = row0 + 32 * w + 16 * rt + n;
+    const bool valid = R < rows;
+    const int i = valid ? R / G : 0, hg = valid ? R - i * G : 0;
+    tok[rt] = i;
+    lim[rt] = !valid ? -1 : mode == 1 ? min(kv_len - qo_len + i, kv_len - 1) : kv_len - 1;
+    const uint16_t* qp = q + (int64_t)(q0 + i) * q_ts + (int64_t)(kvh * G + hg) * q_hs;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const u32x4_t z = {0u, 0u, 0u, 0u};
+      st[rt].qb[s] = valid ? ld16v(qp + 8 * (4 * s + g)) : z;
+    }
+  }
+  // kv positions any row of this work group can see
+  const int last_row = min(rows, row0 + kPrefillRows) - 1;
+  const int kv_end = mode == 1 ? min(kv_len, kv_len - qo_len + last_row / G + 1) : kv_len;
+  const uint8_t* mrow[2] = {nullptr, nullptr};
+  if (mode == 2) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) mrow[rt] = mask + mask_off[b] + (int64_t)tok[rt] * kv_len;
+  }
+
+  uint16_t* kt = reinterpret_cast<uint16_t*>(smem);  // [2 buffers][K, V][32][D]
+  const int win = max(kTileTokens, (kPageWin - 2) * kv.page_size / kTileTokens * kTileTokens);
+  for (int wt0 = 0; wt0 < kv_end; wt0 += win) {
+    const int wt1 = min(kv_end, wt0 + win);
+    const int lp0 = (int)kv.pdiv.div((uint32_t)wt0);
+    const int npg = (int)kv.pdiv.div((uint32_t)(wt1 - 1)) - lp0 + 1;
+    __syncthreads();  // the previous window's lookups are done
+    for (int i = threadIdx.x; i < npg; i += 256) ptab[i] = kv.indices[page0 + lp0 + i];
+    __syncthreads();
+    // wave w loads rows 8w..8w+7 of the K and V tiles
+    auto issue = [&](int t0, int buf) {
+      uint16_t* kd = kt + buf * 2 * TILE;
+#pragma unroll
+      for (int i = 0; i < 8 / RPI; ++i) {
+        const int r = 8 * w + RPI * i + lane / CH;
+        bool ok;
+        const uint64_t off = kv_offset_lds(kv, ptab, lp0, min(t0 + r, wt1 - 1), kvh, ok);
+        const int lc = (lane % CH) ^ chunk_swizzle<D>(r);
+        __builtin_amdgcn_global_load_lds(kv.k + off + 8 * lc,
+                                         (__attribute__((address_space(3))) void*)(kd + (8 * w + RPI * i) * D),
+                                         16, 0, 0);
+        __builtin_amdgcn_global_load_lds(kv.v + off + 8 * lc,
+                                         (__attribute__((address_space(3))) void*)(kd + TILE + (8 * w + RPI * i) * D),
+                                         16, 0, 0);
+      }
+    };
+    int buf = 0;
+    issue(wt0, 0);
+    for (int t0 = wt0; t0 < wt1; t0 += kTileTokens) {
+      wait_vmcnt<0>();
+      __syncthreads();  // every wave's part of this tile has landed
+      const uint16_t* kd = kt + buf * 2 * TILE;
+      u32x4_t ka[2][NS];
+      u32x4_t vb[NB];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int r = 16 * u + n;
+        const int z = chunk_swizzle<D>(r);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) ka[u][s] = *reinterpret_cast<const u32x4_t*>(kd + r * D + 8 * ((4 * s + g) ^ z));
+      }
+      st[0].read_v(kd + TILE, lane, vb);
+      // tokens of this tile on valid pages (bit r = token t0 + r)
+      bool pok = false;
+      if (lane < kTileTokens && t0 + lane < wt1) kv_offset_lds(kv, ptab, lp0, t0 + lane, kvh, pok);
+      const uint64_t tv = __builtin_amdgcn_ballot_w64(pok);
+      wait_lgkmcnt0();
+      if (t0 + kTileTokens < wt1) issue(t0 + kTileTokens, buf ^ 1);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        uint32_t vm = 0;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 16 * u + 4 * g + i, t = t0 + r;
+            bool vis = t <= lim[rt] && ((tv >> r) & 1ull);
+            if (mode == 2 && vis) vis = mrow[rt][t] != 0;
+            vm |= (uint32_t)vis << (4 * u + i);
+          }
+        st[rt].tile(ka, vm, vb, scale_log2, lane);
+      }
+      buf ^= 1;
+    }
+  }
+
+  // normalise and stage the bf16 rows in LDS ([kPrefillRows][D]), then write 16-byte chunks
+  float inv[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const float L = st[rt].row_sum(lane);
+    inv[rt] = L > 0.f ? 1.f / L : 0.f;
+  }
+  __syncthreads();
+  uint16_t* ot = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float f = lane_read(inv[rt], 4 * g + i);
+      const int row = 32 * w + 16 * rt + 4 * g + i;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) ot[row * D + 16 * nb + n] = to_bf1(st[rt].o[nb][i] * f);
+    }
+  __syncthreads();
+  for (int u = threadIdx.x; u < kPrefillRows * CH; u += 256) {
+    const int row = u / CH, c = u % CH;
+    const int R = row0 + row;
+    if (R >= rows) continue;
+    const int i = R / G, hg = R - i * G;
+    st16(out + (int64_t)(q0 + i) * o_ts + (int64_t)(kvh * G + hg) * o_hs + 8 * c,
+         *reinterpret_cast<const uint4*>(ot + row * D + 8 * c));
+  }
 }
 
 }  // namespace pie
@@ -517,4 +686,114 @@ extern "C" int pie_hip_attention_decode(
                                 o_tok_stride, o_head_stride, po, pl); break;
   }
   return check_launch("attention_decode");
+}
+
+// Host: the prefill work list. Reads host copies of qo_indptr, kv_indptr and kv_last_page_len
+// (as flashinfer's plan does); lists (request, first row) items of kPrefillRows packed rows,
+// those that see the most kv positions first, and for mode 2 the byte offset of every
+// request's [qo_len, kv_len] mask block (int64, 8-byte aligned in the plan).
+extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
+                                              const int32_t* kv_last_page_len, int64_t batch,
+                                              int64_t page_size, int64_t num_qo_heads,
+                                              int64_t num_kv_heads, int32_t mode, int32_t* plan,
+                                              int64_t plan_capacity, int64_t* plan_words,
+                                              int64_t* num_items, int64_t* mask_bytes) {
+  PIE_REQUIRE(qo_indptr && kv_indptr && kv_last_page_len && plan && plan_words && num_items && mask_bytes,
+              "prefill_plan: null argument");
+  PIE_REQUIRE(batch >= 0 && batch < (1 << 24) && page_size > 0 && num_kv_heads > 0 &&
+                  num_qo_heads % num_kv_heads == 0 && mode >= 0 && mode <= 2,
+              "prefill_plan: bad batch %lld / page_size %lld / heads %lld,%lld / mode %d",
+              (long long)batch, (long long)page_size, (long long)num_qo_heads,
+              (long long)num_kv_heads, mode);
+  const int64_t G = num_qo_heads / num_kv_heads;
+  struct Item { int32_t b, row0; int64_t work; };
+  std::vector<Item> items;
+  std::vector<int64_t> moff((size_t)batch, 0);
+  int64_t mtotal = 0;
+  for (int64_t b = 0; b < batch; ++b) {
+    const int64_t qo = (int64_t)qo_indptr[b + 1] - qo_indptr[b];
+    const int64_t np = (int64_t)kv_indptr[b + 1] - kv_indptr[b];
+    PIE_REQUIRE(qo >= 0 && np >= 0, "prefill_plan: indptr decreases at request %lld", (long long)b);
+    const int64_t kv = np > 0 ? (np - 1) * page_size + kv_last_page_len[b] : 0;
+    PIE_REQUIRE(kv >= 0 && kv < (1ll << 31) && qo * G < (1ll << 31),
+                "prefill_plan: request %lld too long", (long long)b);
+    moff[(size_t)b] = mtotal;
+    mtotal += qo * kv;
+    for (int64_t r0 = 0; r0 < qo * G; r0 += kPrefillRows) {
+      const int64_t last = std::min(qo * G, r0 + kPrefillRows) - 1;
+      const int64_t seen = mode == 1 ? std::max<int64_t>(0, std::min(kv, kv - qo + last / G + 1)) : kv;
+      items.push_back(Item{(int32_t)b, (int32_t)r0, seen});
+    }
+  }
+  std::stable_sort(items.begin(), items.end(), [](const Item& x, const Item& y) { return x.work > y.work; });
+  int64_t words = kPlanHeader + 2 * (int64_t)items.size();
+  words = (words + 1) / 2 * 2;  // int64 mask offsets start 8-byte aligned
+  const int64_t moff_word = words;
+  if (mode == 2) words += 2 * batch;
+  *plan_words = words;
+  *num_items = (int64_t)items.size();
+  *mask_bytes = mtotal;
+  PIE_REQUIRE(words <= plan_capacity, "prefill_plan: needs %lld words, capacity %lld",
+              (long long)words, (long long)plan_capacity);
+  for (int i = 0; i < kPlanHeader; ++i) plan[i] = 0;
+  plan[0] = (int32_t)items.size();
+  plan[1] = (int32_t)batch;
+  plan[2] = kPrefillRows;
+  plan[3] = (int32_t)moff_word;
+  int32_t* p = plan + kPlanHeader;
+  for (const Item& it : items) { *p++ = it.b; *p++ = it.row0; }
+  if (mode == 2) memcpy(plan + moff_word, moff.data(), sizeof(int64_t) * (size_t)batch);
+  return PIE_HIP_OK;
+}
+
+template <int D>
+static void launch_prefill(hipStream_t st, dim3 grid, const uint16_t* q, int64_t q_ts, int64_t q_hs,
+                           const PagedKV& kv, const int32_t* qo_indptr, int G, float sl2,
+                           const int32_t* plan, int mode, const uint8_t* mask, const int64_t* moff,
+                           uint16_t* out, int64_t o_ts, int64_t o_hs) {
+  hipLaunchKernelGGL(attn_prefill_kernel<D>, grid, dim3(256), 0, st, q, q_ts, q_hs, kv, qo_indptr, G, sl2,
+                     plan, mode, mask, moff, out, o_ts, o_hs);
+}
+
+extern "C" int pie_hip_attention_prefill(
+    const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride, const pie_bf16* k_cache,
+    const pie_bf16* v_cache, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+    int64_t num_pages, const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+    const int32_t* kv_last_page_len, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
+    int64_t page_size, float sm_scale, int32_t mode, const uint8_t* custom_mask,
+    const int32_t* plan, int64_t num_items, int64_t mask_offsets_word, pie_bf16* out,
+    int64_t o_tok_stride, int64_t o_head_stride, void* stream) {
+  PagedKV kv;
+  int rc = paged_kv_desc(&kv, k_cache, v_cache, page_stride, slot_stride, head_stride, num_pages,
+                         kv_indptr, kv_indices, kv_last_page_len, page_size, head_dim,
+                         "attention_prefill");
+  if (rc) return rc;
+  PIE_REQUIRE(q && out && plan && qo_indptr, "attention_prefill: null q, out, plan or qo_indptr");
+  PIE_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
+              "attention_prefill: head_dim %lld not in {64, 128, 256}", (long long)head_dim);
+  PIE_REQUIRE(num_kv_heads > 0 && num_kv_heads <= 65535 && num_qo_heads % num_kv_heads == 0,
+              "attention_prefill: num_qo_heads %lld not a multiple of num_kv_heads %lld",
+              (long long)num_qo_heads, (long long)num_kv_heads);
+  PIE_REQUIRE(mode >= 0 && mode <= 2 && (mode != 2 || (custom_mask && mask_offsets_word > 0 &&
+                                                       mask_offsets_word % 2 == 0)),
+              "attention_prefill: mode %d needs a custom mask and its plan offsets", mode);
+  PIE_REQUIRE(num_items >= 0 && num_items < (1ll << 31), "attention_prefill: bad item count");
+  PIE_REQUIRE(aligned16(q) && aligned16(out) && q_tok_stride % 8 == 0 && q_head_stride % 8 == 0 &&
+                  o_tok_stride % 8 == 0 && o_head_stride % 8 == 0,
+              "attention_prefill: q/out pointers and strides must be 16-byte aligned");
+  if (num_items == 0) return PIE_HIP_OK;
+  const int G = (int)(num_qo_heads / num_kv_heads);
+  const float sl2 = sm_scale * 1.4426950408889634f;
+  const int64_t* moff = mode == 2 ? reinterpret_cast<const int64_t*>(plan + mask_offsets_word) : nullptr;
+  const dim3 grid((unsigned)num_items, (unsigned)num_kv_heads);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (head_dim) {
+    case 64: launch_prefill<64>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
+                                mode, custom_mask, moff, out, o_tok_stride, o_head_stride); break;
+    case 128: launch_prefill<128>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
+                                  mode, custom_mask, moff, out, o_tok_stride, o_head_stride); break;
+    default: launch_prefill<256>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
+                                 mode, custom_mask, moff, out, o_tok_stride, o_head_stride); break;
+  }
+  return check_launch("attention_prefill");
 }

@@ -34,7 +34,7 @@ HOT_PATH = (
     "apply_rope_with_cos_sin_cache_inplace",
 )
 # flashinfer's attention wrapper classes (llama3.py:293-313)
-ATTENTION = ("BatchDecodeWithPagedKVCacheWrapper",)
+ATTENTION = ("BatchDecodeWithPagedKVCacheWrapper", "BatchPrefillWithPagedKVCacheWrapper")
 
 
 class _Namespace(types.ModuleType):

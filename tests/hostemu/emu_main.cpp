@@ -42,7 +42,7 @@ void oracle_rope_cs(uint16_t*, int64_t, int64_t, uint16_t*, int64_t, int64_t, co
                     int64_t, int64_t, int64_t, int, const float*, int64_t, int64_t);
 void oracle_attention(const uint16_t*, int64_t, int64_t, const uint16_t*, const uint16_t*, int64_t,
                       int64_t, int64_t, const int32_t*, const int32_t*, const int32_t*, const int32_t*,
-                      const uint8_t*, const int64_t*, int64_t, int64_t, int64_t, int64_t, int64_t, double,
+                      const uint8_t*, const int64_t*, int, int64_t, int64_t, int64_t, int64_t, int64_t, double,
                       uint16_t*, int64_t, int64_t, double*);
 void oracle_seq_lens(const int32_t*, const int32_t*, int64_t, int64_t, int32_t*);
 void oracle_batch_indices_positions(const int32_t*, const int32_t*, int64_t, int64_t, int32_t*, int32_t*);
@@ -385,7 +385,7 @@ static void case_attn_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int6
   std::vector<int32_t> qo(B + 1);
   for (int64_t b = 0; b <= B; ++b) qo[b] = (int32_t)b;
   oracle_attention(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, qo.data(), ip.p,
-                   idx.p, ll.p, nullptr, nullptr, B, Hq, Hkv, D, P, 1.0 / sqrt((double)D), want.p, Hq * D,
+                   idx.p, ll.p, nullptr, nullptr, 1, B, Hq, Hkv, D, P, 1.0 / sqrt((double)D), want.p, Hq * D,
                    D, nullptr);
   printf("  splits %lld\n", (long long)splits);
   check_close("decode attention", out.p, want.p, B * Hq * D);
@@ -393,6 +393,67 @@ static void case_attn_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int6
   // shows as an error of ~1/kv_len; rounding P to bf16 stays well below 1/256
   float worst = 0.f;
   for (int64_t i = 0; i < B * Hq * D; ++i) {
+    const float w = bf2f(want[i]);
+    worst = fmaxf(worst, fabsf(bf2f(out[i]) - w) / (1.f / 256 + fabsf(w) / 128));
+  }
+  printf("  max |err| / (1/256 + |want|/128) = %.3f\n", worst);
+  failures += !(worst <= 1.f);
+}
+
+// Paged prefill attention: requests with ctx in [0, cmax] cached tokens and qo in [0, qmax] new
+// query tokens; mode 0 full, 1 causal, 2 a random custom mask.
+static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int cmax, int qmax,
+                              int mode) {
+  printf("attn_prefill B=%lld Hq=%lld Hkv=%lld D=%lld P=%lld ctx<=%d qo<=%d mode=%d\n", (long long)B,
+         (long long)Hq, (long long)Hkv, (long long)D, (long long)P, cmax, qmax, mode);
+  std::vector<int32_t> qo(B + 1, 0), indptr(B + 1, 0), last(B), kvl(B);
+  std::uniform_int_distribution<int> dc(0, cmax), dq(0, qmax);
+  for (int64_t b = 0; b < B; ++b) {
+    const int n = dq(rng);
+    kvl[b] = dc(rng) + n;
+    qo[b + 1] = qo[b] + n;
+    const int np = (kvl[b] + P - 1) / P;
+    indptr[b + 1] = indptr[b] + np;
+    last[b] = np ? kvl[b] - (np - 1) * (int)P : 0;
+  }
+  const int64_t T = qo[B], pages = std::max<int64_t>(indptr[B], 1);
+  Buf<int32_t> qi(B + 1), ip(B + 1), idx(pages), ll(B);
+  std::vector<int32_t> perm(pages);
+  for (int64_t i = 0; i < pages; ++i) perm[i] = (int32_t)i;
+  std::shuffle(perm.begin(), perm.end(), rng);
+  for (int64_t i = 0; i < pages; ++i) idx[i] = perm[i];
+  for (int64_t b = 0; b <= B; ++b) { ip[b] = indptr[b]; qi[b] = qo[b]; }
+  for (int64_t b = 0; b < B; ++b) ll[b] = last[b];
+  const int64_t page_elems = 2 * P * Hkv * D;
+  Buf<uint16_t> cache(pages * page_elems), q(std::max<int64_t>(T, 1) * Hq * D), out(std::max<int64_t>(T, 1) * Hq * D),
+      want(std::max<int64_t>(T, 1) * Hq * D);
+  fill_normal(cache);
+  fill_normal(q);
+  int64_t mbytes = 0;
+  for (int64_t b = 0; b < B; ++b) mbytes += (int64_t)(qo[b + 1] - qo[b]) * kvl[b];
+  Buf<uint8_t> mask(std::max<int64_t>(mbytes, 1));
+  std::vector<int64_t> moff(B, 0);
+  for (int64_t b = 1; b < B; ++b) moff[b] = moff[b - 1] + (int64_t)(qo[b] - qo[b - 1]) * kvl[b - 1];
+  std::bernoulli_distribution bit(0.7);
+  for (int64_t i = 0; i < mbytes; ++i) mask[i] = bit(rng) ? 1 : 0;
+  const int64_t cap = 16 + 2 * (T * Hq / 64 + 2 * B + 2) + 2 * B + 2;
+  Buf<int32_t> plan(cap);
+  int64_t words = 0, items = 0, mb = 0;
+  rc_ok(pie_hip_attention_prefill_plan(qi.p, ip.p, ll.p, B, P, Hq, Hkv, mode, plan.p, cap, &words, &items, &mb),
+        "prefill_plan");
+  if (mode == 2 && mb != mbytes) { printf("  mask bytes %lld != %lld\n", (long long)mb, (long long)mbytes); ++failures; }
+  rc_ok(pie_hip_attention_prefill(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, pages,
+                                  qi.p, ip.p, idx.p, ll.p, Hq, Hkv, D, P, 1.f / sqrtf((float)D), mode,
+                                  mode == 2 ? mask.p : nullptr, plan.p, items, plan[3], out.p, Hq * D, D,
+                                  nullptr),
+        "attention_prefill");
+  oracle_attention(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, qi.p, ip.p, idx.p,
+                   ll.p, mode == 2 ? mask.p : nullptr, mode == 2 ? moff.data() : nullptr, mode == 1, B, Hq,
+                   Hkv, D, P, 1.0 / sqrt((double)D), want.p, Hq * D, D, nullptr);
+  printf("  T=%lld items=%lld\n", (long long)T, (long long)items);
+  check_close("prefill attention", out.p, want.p, T * Hq * D);
+  float worst = 0.f;
+  for (int64_t i = 0; i < T * Hq * D; ++i) {
     const float w = bf2f(want[i]);
     worst = fmaxf(worst, fabsf(bf2f(out[i]) - w) / (1.f / 256 + fabsf(w) / 128));
   }
@@ -487,6 +548,15 @@ int main(int argc, char** argv) {
     case_attn_decode(2, 6, 1, 256, 8, 30, 300, 0);    // G = 6, D = 256, library's split count
     case_attn_decode(2, 16, 1, 128, 5, 20, 700, 5);   // G = 16, page size 5
     case_attn_decode(2, 4, 2, 64, 1, 600, 1500, 1);   // page size 1: several page-table windows
+  }
+  if (all || c == "prefill") {
+    case_attn_prefill(3, 8, 2, 128, 16, 40, 45, 1);   // causal, chunked prefill over cached context
+    case_attn_prefill(2, 4, 4, 64, 4, 20, 40, 0);     // full (non-causal), G = 1
+    case_attn_prefill(3, 6, 2, 128, 8, 30, 30, 2);    // custom mask, G = 3
+    case_attn_prefill(2, 2, 1, 256, 16, 10, 20, 1);   // D = 256
+    case_attn_prefill(2, 4, 1, 64, 1, 600, 10, 1);    // page size 1: several page-table windows
+    case_attn_prefill(2, 8, 2, 128, 16, 50, 100, 1);  // up to 400 rows: several items per request
+    case_attn_prefill(2, 8, 2, 128, 16, 50, 100, 2);
   }
   if (all || c == "qkfused") {
     case_qk_fused(5, 4, 2, 128);  // fused kernel

@@ -172,3 +172,116 @@ def test_decode_rejects_bad_input(dev):
     with pytest.raises(NotImplementedError):
         w.plan(pb.kv_indptr.to(dev), pb.kv_indices.to(dev), pb.kv_last_page_len.to(dev), 8, 2,
                128, 16, pos_encoding_mode="ROPE_LLAMA")
+
+
+# ----------------------------------------------------------------------------- prefill
+def _prefill(dev, a, causal=True, custom=None, out=None):
+    pb = a["batch"]
+    w = attention.BatchPrefillWithPagedKVCacheWrapper(_workspace(dev), a["layout"])
+    w.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev),
+           pb.kv_last_page_len.to(dev), a["Hq"], a["Hkv"], a["D"], pb.page_size,
+           custom_mask=None if custom is None else torch.as_tensor(custom).to(dev), causal=causal,
+           q_data_type=torch.bfloat16)
+    o = w.run(a["q"].to(dev), a["cache"].to(dev), out=out)
+    torch.cuda.synchronize()
+    return o
+
+
+def _brle_causal_mask(pb):
+    """The mask Pie builds for plain causal requests (batching.py:335-386 with one true run of
+    position+1): per request a [qo_len, kv_len] block, row i true for t <= kv_len - qo_len + i."""
+    blocks = []
+    for b in range(pb.seq_lens.numel()):
+        qo, kv = int(pb.lens[b]), int(pb.seq_lens[b])
+        t = torch.arange(kv)[None, :]
+        i = torch.arange(qo)[:, None]
+        blocks.append((t <= kv - qo + i).flatten())
+    return torch.cat(blocks) if blocks else torch.zeros(0, dtype=torch.bool)
+
+
+@pytest.mark.parametrize("layout", ["NHD", "HND"])
+@pytest.mark.parametrize("Hq,Hkv,D,P", [(32, 8, 128, 16), (8, 8, 64, 16), (8, 2, 256, 8),
+                                        (28, 4, 128, 5), (12, 4, 128, 1)])
+@pytest.mark.parametrize("mode", ["causal", "full", "custom"])
+def test_prefill_vs_oracle(dev, layout, Hq, Hkv, D, P, mode):
+    print(f"prefill Hq={Hq} Hkv={Hkv} D={D} P={P} layout={layout} mode={mode}", flush=True)
+    g = torch.Generator().manual_seed(Hq + D * 3 + P)
+    B = 5
+    ctx = torch.randint(0, 300, (B,), generator=g).to(torch.int32)
+    qo = torch.randint(1, 90, (B,), generator=g).to(torch.int32)
+    ctx[0], qo[1] = 0, 0  # a fresh prefill and a request with no query tokens
+    a = wl.attn_batch(ctx, qo, Hq=Hq, Hkv=Hkv, D=D, page_size=P, seed=int(qo.sum()) % 997,
+                      layout=layout)
+    custom = None
+    if mode == "custom":
+        pb = a["batch"]
+        n = int((pb.lens.to(torch.int64) * pb.seq_lens.to(torch.int64)).sum())
+        custom = (torch.rand(n, generator=g) < 0.5)
+        custom[:7] = False
+    got = _prefill(dev, a, causal=mode == "causal", custom=custom)
+    pb = a["batch"]
+    want = oracle.attention(N(a["q"]), N(a["cache"]), N(pb.qo_indptr), N(pb.kv_indptr),
+                            N(pb.kv_indices), N(pb.kv_last_page_len),
+                            custom_mask=None if custom is None else custom.numpy(),
+                            causal=mode == "causal", layout=layout)
+    assert_bf16_close(N(got), want, what=mode)
+    _tight(got, want, mode)
+
+
+def test_prefill_pie_causal_mask_equals_causal_mode(dev):
+    """Pie always passes a custom mask (batching.py:226-228); for plain causal requests it is the
+    causal window, and the result is bit-identical to causal=True."""
+    a = wl.attn_batch(torch.tensor([0, 40, 333, 7]), torch.tensor([130, 5, 64, 1]), Hq=32, Hkv=8,
+                      D=128, page_size=16, seed=100)
+    by_mask = _prefill(dev, a, custom=_brle_causal_mask(a["batch"]))
+    by_mode = _prefill(dev, a, causal=True)
+    assert torch.equal(by_mask.view(torch.int16), by_mode.view(torch.int16))
+
+
+def test_prefill_decode_rows_match_decode_wrapper(dev):
+    """One query token per request: prefill (causal) and decode agree within bf16 rounding."""
+    a = wl.attn_batch(torch.randint(0, 900, (7,), generator=torch.Generator().manual_seed(3)),
+                      torch.ones(7, dtype=torch.int32), Hq=32, Hkv=8, D=128, page_size=16, seed=101)
+    p = _prefill(dev, a, causal=True)
+    d = _decode(dev, a)
+    _tight(p, N(d), "prefill vs decode")
+
+
+def test_prefill_config3_sampled(dev):
+    """Configuration 3's ragged batch (64 requests, lengths U[1, 2048], fresh causal prefill,
+    Llama-3-8B heads): the full batch runs in one call; four requests are checked against the
+    oracle (each request's rows depend only on its own pages)."""
+    a = wl.attn_prefill_cfg()
+    pb = a["batch"]
+    got = N(_prefill(dev, a, causal=True))
+    cache = N(a["cache"])
+    lens = pb.lens.tolist()
+    pick = [b for b in np.random.default_rng(1).permutation(len(lens)) if lens[b] <= 1100][:4]
+    for b in pick:
+        b = int(b)
+        q0, q1 = int(pb.qo_indptr[b]), int(pb.qo_indptr[b + 1])
+        ind = pb.kv_indices[int(pb.kv_indptr[b]):int(pb.kv_indptr[b + 1])]
+        want = oracle.attention(N(a["q"][q0:q1]), cache, np.array([0, q1 - q0], np.int32),
+                                np.array([0, ind.numel()], np.int32), N(ind),
+                                N(pb.kv_last_page_len[b:b + 1]))
+        assert_bf16_close(got[q0:q1], want, what=f"request {b} (len {q1 - q0})")
+        _tight(got[q0:q1], want, f"request {b}")
+
+
+def test_prefill_rejects_bad_input(dev):
+    a = wl.attn_batch([5, 0], [3, 4], Hq=8, Hkv=2, D=128, page_size=16, seed=102)
+    pb = a["batch"]
+    w = attention.BatchPrefillWithPagedKVCacheWrapper(_workspace(dev), "NHD")
+    with pytest.raises(RuntimeError):
+        w.run(a["q"].to(dev), a["cache"].to(dev))
+    w.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev),
+           pb.kv_last_page_len.to(dev), 8, 2, 128, 16, causal=True)
+    with pytest.raises(ValueError):
+        w.run(a["q"].to(dev)[:3], a["cache"].to(dev))  # wrong token count
+    with pytest.raises(ValueError):
+        w.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev),
+               pb.kv_last_page_len.to(dev), 8, 2, 128, 16,
+               custom_mask=torch.ones(3, dtype=torch.bool, device=dev))  # mask too short
+    with pytest.raises(NotImplementedError):
+        w.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev),
+               pb.kv_last_page_len.to(dev), 8, 2, 128, 16, window_left=128)

@@ -112,8 +112,11 @@ def test_integration_installs_flashinfer_namespace():
         assert fi is mod
         for n in integration.HOT_PATH:
             assert getattr(fi, n) is getattr(ops, n)
+        from pie_amd import attention
+        for n in integration.ATTENTION:
+            assert getattr(fi, n) is getattr(attention, n)
         with pytest.raises(AttributeError):
-            fi.BatchPrefillWithPagedKVCacheWrapper  # not served here, and no real flashinfer
+            fi.sampling  # not served here, and no real flashinfer
         assert integration.install() is mod  # idempotent
     finally:
         integration.uninstall()
