@@ -313,7 +313,7 @@ int pie_hip_attention_decode(const pie_bf16* q, int64_t q_tok_stride, int64_t q_
 int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
                                    const int32_t* kv_last_page_len, int64_t batch,
                                    int64_t page_size, int64_t num_qo_heads, int64_t num_kv_heads,
-                                   int32_t mode, int32_t* plan, int64_t plan_capacity,
+                                   int64_t head_dim, int32_t mode, int32_t* plan, int64_t plan_capacity,
                                    int64_t* plan_words, int64_t* num_items, int64_t* mask_bytes);
 int pie_hip_attention_prefill(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
                               const pie_bf16* k_cache, const pie_bf16* v_cache,

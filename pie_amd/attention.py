@@ -219,11 +219,11 @@ class BatchPrefillWithPagedKVCacheWrapper:
         mode = 2 if mask is not None else (1 if causal else 0)
         G = num_qo_heads // num_kv_heads
         T = int(qo_h[-1]) if batch else 0
-        cap = 16 + 2 * (T * G // 128 + batch + 1) + 2 * batch + 2
+        cap = 16 + 2 * (T * G // 64 + batch + 1) + 2 * batch + 2
         plan = np.zeros(cap, dtype=np.int32)
         words, items, mbytes = C.c_int64(0), C.c_int64(0), C.c_int64(0)
         _lib.call("pie_hip_attention_prefill_plan", qo_h.data_ptr(), kv_h.data_ptr(), ll_h.data_ptr(),
-                  batch, page_size, num_qo_heads, num_kv_heads, mode, plan.ctypes.data, cap,
+                  batch, page_size, num_qo_heads, num_kv_heads, head_dim_qk, mode, plan.ctypes.data, cap,
                   C.byref(words), C.byref(items), C.byref(mbytes))
         if mode == 2:
             if mask.dtype not in (torch.bool, torch.uint8):

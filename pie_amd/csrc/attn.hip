@@ -144,20 +144,24 @@ struct WaveAttn {
     }
   }
 
-  // One 32-token tile: ka = K A-operands of the two subtiles, vb = the V B-operands (read_v),
-  // bit 4u+i of vmask says whether this lane's row n sees token 16u+4g+i.
-  __device__ __forceinline__ void tile(const u32x4_t (&ka)[2][NS], uint32_t vmask,
-                                       const u32x4_t (&vb)[NB], float scale_log2, int lane) {
-    const int g = lane >> 4;
-    float s[2][4];
-    #pragma unroll
+  // Scores of a 32-token tile in the exp2 domain: s[u][i] = row n . token 16u+4g+i, -inf where
+  // bit 4u+i of vmask is clear.
+  __device__ __forceinline__ void scores(const u32x4_t (&ka)[2][NS], uint32_t vmask, float scale_log2,
+                                         float (&s)[2][4]) const {
+#pragma unroll
     for (int u = 0; u < 2; ++u) {
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-      #pragma unroll
+#pragma unroll
       for (int st = 0; st < NS; ++st) acc = mfma_16x16x32(ka[u][st], qb[st], acc);
-      #pragma unroll
+#pragma unroll
       for (int i = 0; i < 4; ++i) s[u][i] = ((vmask >> (4 * u + i)) & 1u) ? acc[i] * scale_log2 : -INFINITY;
     }
+  }
+
+  // Online-softmax step: updates m and l, returns the tile's probabilities as the PV A-operand
+  // (bf16) and in a[i] the factor by which O row 4g+i must be rescaled.
+  __device__ __forceinline__ u32x4_t softmax(const float (&s)[2][4], int lane, float (&a)[4]) {
+    const int g = lane >> 4;
     float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
     mx = fmaxf(mx, lane_read(mx, lane ^ 16));
@@ -166,25 +170,36 @@ struct WaveAttn {
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = fast_exp2(m - m_use);
     float p[2][4], psum = 0.f;
-    #pragma unroll
+#pragma unroll
     for (int u = 0; u < 2; ++u)
-      #pragma unroll
+#pragma unroll
       for (int i = 0; i < 4; ++i) { p[u][i] = fast_exp2(s[u][i] - m_use); psum += p[u][i]; }
     l = l * alpha + psum;
     m = m_new;
     // O rows 4g+i take the factor of row 4g+i (held by lane 4g+i of every group)
-    float a[4];
-    #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = lane_read(alpha, 4 * g + i);
-    const u32x4_t pa = {pack_bf2(p[0][0], p[0][1]), pack_bf2(p[0][2], p[0][3]),
-                        pack_bf2(p[1][0], p[1][1]), pack_bf2(p[1][2], p[1][3])};
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      f32x4_t c = o[nb];
-      #pragma unroll
-      for (int i = 0; i < 4; ++i) c[i] *= a[i];
-      o[nb] = mfma_16x16x32(pa, vb[nb], c);
-    }
+    for (int i = 0; i < 4; ++i) a[i] = lane_read(alpha, 4 * g + i);
+    return u32x4_t{pack_bf2(p[0][0], p[0][1]), pack_bf2(p[0][2], p[0][3]),
+                   pack_bf2(p[1][0], p[1][1]), pack_bf2(p[1][2], p[1][3])};
+  }
+
+  // O block nb = O block nb * a + P V_nb.
+  __device__ __forceinline__ void pv(const u32x4_t& pa, const u32x4_t& vb, const float (&a)[4], int nb) {
+    f32x4_t c = o[nb];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] *= a[i];
+    o[nb] = mfma_16x16x32(pa, vb, c);
+  }
+
+  // One 32-token tile: ka = K A-operands of the two subtiles, vb = the V B-operands (read_v),
+  // bit 4u+i of vmask says whether this lane's row n sees token 16u+4g+i.
+  __device__ __forceinline__ void tile(const u32x4_t (&ka)[2][NS], uint32_t vmask,
+                                       const u32x4_t (&vb)[NB], float scale_log2, int lane) {
+    float s[2][4], a[4];
+    scores(ka, vmask, scale_log2, s);
+    const u32x4_t pa = softmax(s, lane, a);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) pv(pa, vb[nb], a, nb);
   }
 
   // Row n's total probability mass (sum of the four lane groups' partials).
@@ -427,24 +442,30 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(int B, int Hq, int split
 
 // ------------------------------------------------------------------------------ prefill
 // Work item: request b, first packed query row row0 (row R = query token R / G, head R % G of
-// the kv head's group). A work group of 4 waves owns kPrefillRows rows (32 per wave, two MFMA
-// row tiles) and streams the request's kv tokens in 32-token tiles: the four waves load each K
+// the kv head's group). A work group of 4 waves owns prefill_rows<D> rows (one or two 16-row
+// MFMA row tiles per wave) and streams the request's kv tokens in 32-token tiles: the four waves load each K
 // and V tile cooperatively straight into LDS (global_load_lds, chunk-swizzled, double-buffered),
 // then every wave reads the K and V MFMA operands it needs into registers before the next
 // tile's loads are issued, and runs both row tiles against them.
 // Visibility: mode 0 every cached position, 1 causal (t <= kv_len - qo_len + i), 2 the custom
 // mask (bytes, per request a row-major [qo_len, kv_len] block at mask + mask_off[b]).
-constexpr int kPrefillRows = 128;
+// Query rows per work group: 2 MFMA row tiles per wave (1 for D = 256, whose accumulators
+// would not fit twice).
+template <int D>
+constexpr int prefill_row_tiles() { return D == 256 ? 1 : 2; }
+template <int D>
+constexpr int prefill_rows() { return 64 * prefill_row_tiles<D>(); }
 constexpr int kPlanHeader = 16;  // plan words before the items: [0] items, [1] batch, [2] rows per item
 
 template <int D>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(
+__global__ __launch_bounds__(256, D == 256 ? 1 : 2) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv,
     const int32_t* __restrict__ qo_indptr, int G, float scale_log2, const int32_t* __restrict__ plan,
     int mode, const uint8_t* __restrict__ mask, const int64_t* __restrict__ mask_off,
     uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
   using W = WaveAttn<D>;
   constexpr int NS = W::NS, NB = W::NB, CH = D / 8, RPI = 64 / CH;
+  constexpr int RT = prefill_row_tiles<D>(), kPrefillRows = prefill_rows<D>();
   constexpr int TILE = kTileTokens * D;  // elements of one K or V tile
   constexpr int kSmemLoop = 2 * 2 * TILE * 2;
   constexpr int kSmemOut = kPrefillRows * D * 2;
@@ -462,13 +483,13 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
   const int rows = qo_len * G;
   const int page0 = kv.indptr[b];
 
-  // this lane's query rows (row n of each of the wave's two row tiles)
-  W st[2];
-  int lim[2], tok[2];
+  // this lane's query rows (row n of each of the wave's row tiles)
+  W st[RT];
+  int lim[RT], tok[RT];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int rt = 0; rt < RT; ++rt) {
     st[rt].init();
-    const int R = row0 + 32 * w + 16 * rt + n;
+    const int R = row0 + 16 * RT * w + 16 * rt + n;
     const bool valid = R < rows;
     const int i = valid ? R / G : 0, hg = valid ? R - i * G : 0;
     tok[rt] = i;
@@ -483,62 +504,64 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
   // kv positions any row of this work group can see
   const int last_row = min(rows, row0 + kPrefillRows) - 1;
   const int kv_end = mode == 1 ? min(kv_len, kv_len - qo_len + last_row / G + 1) : kv_len;
-  const uint8_t* mrow[2] = {nullptr, nullptr};
-  if (mode == 2) {
+  const uint8_t* mrow[RT];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) mrow[rt] = mask + mask_off[b] + (int64_t)tok[rt] * kv_len;
-  }
+  for (int rt = 0; rt < RT; ++rt) mrow[rt] = mode == 2 ? mask + mask_off[b] + (int64_t)tok[rt] * kv_len : nullptr;
 
   uint16_t* kt = reinterpret_cast<uint16_t*>(smem);  // [2 buffers][K, V][32][D]
+  constexpr int NL = 8 / RPI;  // load instructions per wave for its 8 rows of a K or V tile
+  // A tile in flight in registers: this wave's rows 8w..8w+7 of K and V (chunk-swizzled as they
+  // will sit in LDS).
+  struct Slot { u32x4_t k[NL], v[NL]; };
   const int win = max(kTileTokens, (kPageWin - 2) * kv.page_size / kTileTokens * kTileTokens);
   for (int wt0 = 0; wt0 < kv_end; wt0 += win) {
     const int wt1 = min(kv_end, wt0 + win);
     const int lp0 = (int)kv.pdiv.div((uint32_t)wt0);
     const int npg = (int)kv.pdiv.div((uint32_t)(wt1 - 1)) - lp0 + 1;
-    __syncthreads();  // the previous window's lookups are done
+    const int ntiles = (wt1 - wt0 + kTileTokens - 1) / kTileTokens;
+    __syncthreads();  // the previous window's lookups and LDS tiles are done
     for (int i = threadIdx.x; i < npg; i += 256) ptab[i] = kv.indices[page0 + lp0 + i];
     __syncthreads();
-    // wave w loads rows 8w..8w+7 of the K and V tiles
-    auto issue = [&](int t0, int buf) {
-      uint16_t* kd = kt + buf * 2 * TILE;
+    auto gload = [&](Slot& sl, int tile) {
+      const int t0 = wt0 + tile * kTileTokens;
 #pragma unroll
-      for (int i = 0; i < 8 / RPI; ++i) {
+      for (int i = 0; i < NL; ++i) {
         const int r = 8 * w + RPI * i + lane / CH;
         bool ok;
         const uint64_t off = kv_offset_lds(kv, ptab, lp0, min(t0 + r, wt1 - 1), kvh, ok);
         const int lc = (lane % CH) ^ chunk_swizzle<D>(r);
-        __builtin_amdgcn_global_load_lds(kv.k + off + 8 * lc,
-                                         (__attribute__((address_space(3))) void*)(kd + (8 * w + RPI * i) * D),
-                                         16, 0, 0);
-        __builtin_amdgcn_global_load_lds(kv.v + off + 8 * lc,
-                                         (__attribute__((address_space(3))) void*)(kd + TILE + (8 * w + RPI * i) * D),
-                                         16, 0, 0);
+        sl.k[i] = ld16v(kv.k + off + 8 * lc);
+        sl.v[i] = ld16v(kv.v + off + 8 * lc);
       }
     };
-    int buf = 0;
-    issue(wt0, 0);
-    for (int t0 = wt0; t0 < wt1; t0 += kTileTokens) {
-      wait_vmcnt<0>();
-      __syncthreads();  // every wave's part of this tile has landed
-      const uint16_t* kd = kt + buf * 2 * TILE;
+    auto lwrite = [&](const Slot& sl, int tile) {
+      uint16_t* kd = kt + (tile & 1) * 2 * TILE;
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        *reinterpret_cast<u32x4_t*>(kd + (8 * w + RPI * i) * D + 8 * lane) = sl.k[i];
+        *reinterpret_cast<u32x4_t*>(kd + TILE + (8 * w + RPI * i) * D + 8 * lane) = sl.v[i];
+      }
+    };
+    auto compute = [&](int tile) {
+      const int t0 = wt0 + tile * kTileTokens;
+      const uint16_t* kd = kt + (tile & 1) * 2 * TILE;
+      // tokens of this tile on valid pages (bit r = token t0 + r)
+      bool pok = false;
+      if (lane < kTileTokens && t0 + lane < wt1) kv_offset_lds(kv, ptab, lp0, t0 + lane, kvh, pok);
+      const uint64_t tv = __builtin_amdgcn_ballot_w64(pok);
       u32x4_t ka[2][NS];
-      u32x4_t vb[NB];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int r = 16 * u + n;
         const int z = chunk_swizzle<D>(r);
 #pragma unroll
-        for (int s = 0; s < NS; ++s) ka[u][s] = *reinterpret_cast<const u32x4_t*>(kd + r * D + 8 * ((4 * s + g) ^ z));
+        for (int s = 0; s < NS; ++s)
+          ka[u][s] = *reinterpret_cast<const u32x4_t*>(kd + r * D + 8 * ((4 * s + g) ^ z));
       }
-      st[0].read_v(kd + TILE, lane, vb);
-      // tokens of this tile on valid pages (bit r = token t0 + r)
-      bool pok = false;
-      if (lane < kTileTokens && t0 + lane < wt1) kv_offset_lds(kv, ptab, lp0, t0 + lane, kvh, pok);
-      const uint64_t tv = __builtin_amdgcn_ballot_w64(pok);
-      wait_lgkmcnt0();
-      if (t0 + kTileTokens < wt1) issue(t0 + kTileTokens, buf ^ 1);
+      u32x4_t pa[RT];
+      float a[RT][4];
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
+      for (int rt = 0; rt < RT; ++rt) {
         uint32_t vm = 0;
 #pragma unroll
         for (int u = 0; u < 2; ++u)
@@ -549,27 +572,67 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
             if (mode == 2 && vis) vis = mrow[rt][t] != 0;
             vm |= (uint32_t)vis << (4 * u + i);
           }
-        st[rt].tile(ka, vm, vb, scale_log2, lane);
+        float sc[2][4];
+        st[rt].scores(ka, vm, scale_log2, sc);
+        pa[rt] = st[rt].softmax(sc, lane, a[rt]);
       }
-      buf ^= 1;
+      // PV: the V operand of each 16-dim block comes straight from LDS (transpose reads)
+      const int j = (lane >> 2) & 3, qq = lane & 3;
+      const int r0 = 4 * g + j, r1 = r0 + 16;
+      const uint16_t* b0 = kd + TILE + r0 * D + 4 * (qq & 1);
+      const uint16_t* b1 = kd + TILE + r1 * D + 4 * (qq & 1);
+      const int z0 = chunk_swizzle<D>(r0), z1 = chunk_swizzle<D>(r1);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int lc = 2 * nb + (qq >> 1);
+        const uint2 lo = lds_read_tr16(b0 + 8 * (lc ^ z0));
+        const uint2 hi = lds_read_tr16(b1 + 8 * (lc ^ z1));
+        const u32x4_t vb = {lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) st[rt].pv(pa[rt], vb, a[rt], nb);
+      }
+    };
+    // Two register slots alternate (no copies, which would force waits on loads in flight):
+    // tile k+3's loads are issued while tile k is computed and land in LDS two steps later.
+    Slot sa, sb;
+    gload(sa, 0);
+    if (ntiles > 1) gload(sb, 1);
+    lwrite(sa, 0);
+    if (ntiles > 2) gload(sa, 2);
+    __syncthreads();
+    for (int k = 0;;) {
+      compute(k);
+      if (k + 1 < ntiles) {
+        lwrite(sb, k + 1);
+        if (k + 3 < ntiles) gload(sb, k + 3);
+      }
+      __syncthreads();
+      if (++k >= ntiles) break;
+      compute(k);
+      if (k + 1 < ntiles) {
+        lwrite(sa, k + 1);
+        if (k + 3 < ntiles) gload(sa, k + 3);
+      }
+      __syncthreads();
+      if (++k >= ntiles) break;
     }
   }
 
   // normalise and stage the bf16 rows in LDS ([kPrefillRows][D]), then write 16-byte chunks
-  float inv[2];
+  float inv[RT];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int rt = 0; rt < RT; ++rt) {
     const float L = st[rt].row_sum(lane);
     inv[rt] = L > 0.f ? 1.f / L : 0.f;
   }
   __syncthreads();
   uint16_t* ot = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float f = lane_read(inv[rt], 4 * g + i);
-      const int row = 32 * w + 16 * rt + 4 * g + i;
+      const int row = 16 * RT * w + 16 * rt + 4 * g + i;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) ot[row * D + 16 * nb + n] = to_bf1(st[rt].o[nb][i] * f);
     }
@@ -689,13 +752,14 @@ extern "C" int pie_hip_attention_decode(
 }
 
 // Host: the prefill work list. Reads host copies of qo_indptr, kv_indptr and kv_last_page_len
-// (as flashinfer's plan does); lists (request, first row) items of kPrefillRows packed rows,
+// (as flashinfer's plan does); lists (request, first row) items of prefill_rows<D> packed rows,
 // those that see the most kv positions first, and for mode 2 the byte offset of every
 // request's [qo_len, kv_len] mask block (int64, 8-byte aligned in the plan).
 extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
                                               const int32_t* kv_last_page_len, int64_t batch,
                                               int64_t page_size, int64_t num_qo_heads,
-                                              int64_t num_kv_heads, int32_t mode, int32_t* plan,
+                                              int64_t num_kv_heads, int64_t head_dim, int32_t mode,
+                                              int32_t* plan,
                                               int64_t plan_capacity, int64_t* plan_words,
                                               int64_t* num_items, int64_t* mask_bytes) {
   PIE_REQUIRE(qo_indptr && kv_indptr && kv_last_page_len && plan && plan_words && num_items && mask_bytes,
@@ -705,7 +769,10 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
               "prefill_plan: bad batch %lld / page_size %lld / heads %lld,%lld / mode %d",
               (long long)batch, (long long)page_size, (long long)num_qo_heads,
               (long long)num_kv_heads, mode);
+  PIE_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
+              "prefill_plan: head_dim %lld not in {64, 128, 256}", (long long)head_dim);
   const int64_t G = num_qo_heads / num_kv_heads;
+  const int64_t kPrefillRows = head_dim == 256 ? prefill_rows<256>() : prefill_rows<128>();
   struct Item { int32_t b, row0; int64_t work; };
   std::vector<Item> items;
   std::vector<int64_t> moff((size_t)batch, 0);
@@ -738,7 +805,7 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
   for (int i = 0; i < kPlanHeader; ++i) plan[i] = 0;
   plan[0] = (int32_t)items.size();
   plan[1] = (int32_t)batch;
-  plan[2] = kPrefillRows;
+  plan[2] = (int32_t)kPrefillRows;
   plan[3] = (int32_t)moff_word;
   int32_t* p = plan + kPlanHeader;
   for (const Item& it : items) { *p++ = it.b; *p++ = it.row0; }
@@ -778,6 +845,8 @@ extern "C" int pie_hip_attention_prefill(
                                                        mask_offsets_word % 2 == 0)),
               "attention_prefill: mode %d needs a custom mask and its plan offsets", mode);
   PIE_REQUIRE(num_items >= 0 && num_items < (1ll << 31), "attention_prefill: bad item count");
+  PIE_REQUIRE(plan[2] == (head_dim == 256 ? prefill_rows<256>() : prefill_rows<128>()),
+              "attention_prefill: the plan was made for another head_dim");
   PIE_REQUIRE(aligned16(q) && aligned16(out) && q_tok_stride % 8 == 0 && q_head_stride % 8 == 0 &&
                   o_tok_stride % 8 == 0 && o_head_stride % 8 == 0,
               "attention_prefill: q/out pointers and strides must be 16-byte aligned");

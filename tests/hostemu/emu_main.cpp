@@ -436,10 +436,10 @@ static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
   for (int64_t b = 1; b < B; ++b) moff[b] = moff[b - 1] + (int64_t)(qo[b] - qo[b - 1]) * kvl[b - 1];
   std::bernoulli_distribution bit(0.7);
   for (int64_t i = 0; i < mbytes; ++i) mask[i] = bit(rng) ? 1 : 0;
-  const int64_t cap = 16 + 2 * (T * Hq / 64 + 2 * B + 2) + 2 * B + 2;
+  const int64_t cap = 16 + 2 * (T * Hq / 32 + 2 * B + 2) + 2 * B + 2;
   Buf<int32_t> plan(cap);
   int64_t words = 0, items = 0, mb = 0;
-  rc_ok(pie_hip_attention_prefill_plan(qi.p, ip.p, ll.p, B, P, Hq, Hkv, mode, plan.p, cap, &words, &items, &mb),
+  rc_ok(pie_hip_attention_prefill_plan(qi.p, ip.p, ll.p, B, P, Hq, Hkv, D, mode, plan.p, cap, &words, &items, &mb),
         "prefill_plan");
   if (mode == 2 && mb != mbytes) { printf("  mask bytes %lld != %lld\n", (long long)mb, (long long)mbytes); ++failures; }
   rc_ok(pie_hip_attention_prefill(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, pages,

@@ -45,7 +45,7 @@ inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
 #define __device__
 #define __host__
 #define __forceinline__ inline
-#define __launch_bounds__(x)
+#define __launch_bounds__(...)
 #define __shared__ static
 
 namespace emu {
