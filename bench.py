@@ -153,6 +153,8 @@ def measure_ops(dev, cold_iters=20, only=None):
         res.extend(_ops_variants(dev, run))
     if want("attn"):
         res.extend(_ops_attention(dev, run))
+    if want("sample"):
+        res.extend(_ops_sampling(dev, run))
     if want("cfg5"):
         res.extend(measure_chain(dev, flush, cold_iters))
     del scratch
@@ -333,6 +335,31 @@ def _ops_attention(dev, run):
     return res
 
 
+def _ops_sampling(dev, run):
+    """The sampling path at Llama-3 vocabulary (128256) for 256 decode rows: safe_scaled_softmax
+    on bf16 logits, and top-k + top-p sampling on fp32 probabilities. Bytes: one read (and for the
+    softmax one write) of the rows; the sampler's later passes re-read rows from L2/MALL."""
+    import torch
+    from pie_amd import sampling
+    B, V = 256, 128256
+    g = torch.Generator().manual_seed(0)
+    logits0 = (torch.randn(B, V, generator=g) * 3).to(torch.bfloat16).to(dev)
+    temps = torch.full((B,), 0.8, device=dev)
+    probs0 = torch.softmax(logits0.float(), -1)
+    k = torch.full((B,), 50, dtype=torch.int32, device=dev)
+    p = torch.full((B,), 0.9, device=dev)
+
+    def make_softmax():
+        x, out = logits0.clone(), torch.empty_like(logits0)
+        return lambda: sampling.safe_scaled_softmax(x, temps, out=out)
+
+    def make_sample():
+        pr = probs0.clone()
+        return lambda: sampling.top_k_top_p_sampling_from_probs(pr, k, p, seed=1, offset=0)
+    return [run(f"safe_scaled_softmax bf16 [{B},{V}]", 2 * B * V * 2, make_softmax),
+            run(f"top_k_top_p sampling fp32 [{B},{V}] (k 50, p 0.9)", B * V * 4, make_sample)]
+
+
 def _back_to_back(fn, n, reps=5):
     """µs per call over n back-to-back calls between two events (median of reps)."""
     import torch
@@ -384,7 +411,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", choices=["all", "main", "ops", "copy", "chain"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--op", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "variants", "attn"], default=None,
+    ap.add_argument("--op", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "variants", "attn", "sample"], default=None,
                     help="with --only ops: measure one configuration")
     args = ap.parse_args()
     if args.gpus != 1:

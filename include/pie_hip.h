@@ -327,6 +327,38 @@ int pie_hip_attention_prefill(const pie_bf16* q, int64_t q_tok_stride, int64_t q
                               pie_bf16* out, int64_t o_tok_stride, int64_t o_head_stride,
                               void* stream);
 
+
+/*
+ * Sampling from probabilities, one draw per row: flashinfer.sampling.sampling_from_probs (mode 0),
+ * top_p_ (1), top_k_ (2), min_p_ (3) and top_k_top_p_sampling_from_probs (4) as Pie calls them
+ * (pie/src/pie_worker/model/common.py:316-344; API restated in
+ * pie/src/flashinfer_metal/sampling.py:19-79).
+ * probs: fp32 [prob_rows, prob_stride], non-negative (NaN and p <= 0 are never drawn). Output
+ * row r uses probs row row_indices[r] (NULL: row r; an index outside [0, prob_rows) gives -1). Kept set: top_p keeps token i iff the mass of
+ * strictly more probable tokens is below top_p times the row's (top-k set's) mass; top_k keeps i
+ * iff fewer than k tokens are strictly more probable (k <= 0 or k >= vocab keeps all); min_p keeps
+ * p_i >= min_p * max p. Per-row parameters come from the arrays when non-NULL, else the scalars.
+ * The draw is the first kept index (in index order) whose running kept mass exceeds u times the
+ * kept mass, u = uniforms[r] when non-NULL, else Philox4x32-10 of (seed, offset, r). Masses are
+ * summed in 64-bit fixed point (2^-40), so results do not depend on thread order.
+ * out: int32 [batch]; a row with nothing kept gives -1.
+ */
+int pie_hip_sample(const float* probs, int64_t prob_stride, int64_t prob_rows, int64_t vocab,
+                   int64_t batch, const int32_t* row_indices, int32_t mode, const int32_t* top_k,
+                   int32_t top_k_scalar, const float* top_p, float top_p_scalar,
+                   const float* min_p, float min_p_scalar, const double* uniforms, uint64_t seed,
+                   uint64_t offset, int32_t* out, void* stream);
+
+/*
+ * safe_scaled_softmax of pie/src/pie_worker/model/common.py:38-59, :68-188 (the Triton kernel Pie
+ * runs on GPUs): per row, softmax(logits / T) with fp32 math, or the one-hot of the first maximum
+ * when T < greedy_threshold (greedy decoding). logits and out are fp32 (is_bf16 = 0) or bf16
+ * (is_bf16 = 1), out in the logits' dtype; temperatures: fp32 [batch]. out may alias logits.
+ */
+int pie_hip_scaled_softmax(const void* logits, int32_t is_bf16, int64_t stride, int64_t batch,
+                           int64_t vocab, const float* temperatures, float greedy_threshold,
+                           void* out, int64_t out_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,8 @@ Each function cites the reference behaviour it restates (paths in the zyma98/pie
   rope / inv_freq_*       pie/src/flashinfer_metal/kernels/metal_rope.metal:26-107
   append                  pie/src/flashinfer_metal/kernels/metal_append_paged_kv_cache.metal:23-107
   seq_lens, batch_indices_positions   pie/src/flashinfer_metal/ops.py:392-436
+  scaled_softmax          pie/src/pie_worker/model/common.py:38-59, :68-188 (safe_scaled_softmax)
+  sample                  flashinfer.sampling.*_sampling_from_probs as called at common.py:316-344
   attention               flashinfer Batch{Prefill,Decode}WithPagedKVCacheWrapper.run, restated in
                           pie/src/flashinfer_metal/ops.py:163-282 and
                           kernels/metal_attention_simdgroup_opt.metal:120-470; custom masks as
@@ -81,6 +83,9 @@ def _load():
         "oracle_attention": (None, [_u16p, i64, i64, C.c_void_p, C.c_void_p, i64, i64, i64,
                                     _i32p, _i32p, _i32p, _i32p, C.c_void_p, C.c_void_p, C.c_int, i64, i64,
                                     i64, i64, i64, C.c_double, _u16p, i64, i64, C.c_void_p]),
+        "oracle_scaled_softmax": (None, [_f32p, i64, i64, _f32p, C.c_double, _f64p]),
+        "oracle_sample": (None, [_f32p, i64, i64, i64, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+                                 _f64p, _i32p, C.c_void_p]),
         "oracle_f32_to_bf16": (C.c_uint16, [C.c_float]),
         "oracle_f64_to_bf16": (C.c_uint16, [C.c_double]),
     }
@@ -329,3 +334,31 @@ def attention(q: np.ndarray, cache: np.ndarray, qo_indptr, kv_indptr, kv_indices
         None if off is None else off.ctypes.data, 1 if causal else 0, B, Hq, Hkv, D, P, scale, out, Hq * D, D,
         lse.ctypes.data)
     return (out, lse) if return_lse else out
+
+
+def scaled_softmax(logits: np.ndarray, temperatures, greedy_threshold: float = 1e-5) -> np.ndarray:
+    """logits [B, V] (float32 values) -> float64 probabilities (one-hot rows for T < threshold)."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    B, V = x.shape
+    out = np.empty((B, V), dtype=np.float64)
+    _load().oracle_scaled_softmax(x, B, V, np.ascontiguousarray(temperatures, np.float32),
+                                  greedy_threshold, out)
+    return out
+
+
+SAMPLE_MODES = {"plain": 0, "top_p": 1, "top_k": 2, "min_p": 3, "top_k_top_p": 4}
+
+
+def sample(probs: np.ndarray, mode: str, uniforms, top_k=None, top_p=None, min_p=None):
+    """Inverse-CDF draw (index order) over each row's kept set; returns (samples int32 [B],
+    kept bool [B, V])."""
+    p = np.ascontiguousarray(probs, dtype=np.float32)
+    B, V = p.shape
+    arr = lambda a, dt: None if a is None else np.ascontiguousarray(np.broadcast_to(a, (B,)), dt)
+    tk, tp, mp = arr(top_k, np.int32), arr(top_p, np.float32), arr(min_p, np.float32)
+    out = np.empty(B, dtype=np.int32)
+    kept = np.empty((B, V), dtype=np.uint8)
+    ptr = lambda a: None if a is None else a.ctypes.data
+    _load().oracle_sample(p, B, V, V, SAMPLE_MODES[mode], ptr(tk), ptr(tp), ptr(mp),
+                          np.ascontiguousarray(uniforms, np.float64), out, kept.ctypes.data)
+    return out, kept.astype(bool)

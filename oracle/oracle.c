@@ -26,6 +26,11 @@
  *                      in pie/src/flashinfer_metal/ops.py:163-282 and
  *                      kernels/metal_attention_simdgroup_opt.metal:120-470 (causal window),
  *                      custom masks as built at pie/src/pie_worker/batching.py:335-386
+ *   scaled_softmax     safe_scaled_softmax, pie/src/pie_worker/model/common.py:38-59 (torch
+ *                      form) and :68-188 (the Triton kernel Pie runs on GPUs)
+ *   sample             flashinfer.sampling.{sampling,top_p,top_k,min_p,top_k_top_p}_sampling_from_probs
+ *                      as called at common.py:316-344; restated (with a simplified top-k and a
+ *                      boundary-excluding top-p) in pie/src/flashinfer_metal/sampling.py:19-79
  */
 #include <math.h>
 #include <stdlib.h>
@@ -368,4 +373,112 @@ void oracle_attention(const uint16_t* q, int64_t q_ts, int64_t q_hs, const uint1
     free(s);
     free(acc);
   }
+}
+
+/* ------------------------------------------------------------------ sampling path
+ * scaled_softmax: row r of logits (fp32 values given as float) -> probs, float64 math.
+ * temperature < greedy_threshold: one-hot at the first maximum; otherwise softmax(x / T).     */
+void oracle_scaled_softmax(const float* x, int64_t B, int64_t V, const float* temps, double greedy,
+                           double* out) {
+  for (int64_t r = 0; r < B; ++r) {
+    const float* xr = x + r * V;
+    double* o = out + r * V;
+    int64_t am = 0;
+    for (int64_t i = 1; i < V; ++i)
+      if (xr[i] > xr[am]) am = i;
+    if ((double)temps[r] < greedy) {
+      for (int64_t i = 0; i < V; ++i) o[i] = i == am ? 1.0 : 0.0;
+      continue;
+    }
+    const double T = temps[r];
+    const double m = (double)xr[am] / T;
+    double s = 0;
+    for (int64_t i = 0; i < V; ++i) s += exp((double)xr[i] / T - m);
+    for (int64_t i = 0; i < V; ++i) o[i] = exp((double)xr[i] / T - m) / s;
+  }
+}
+
+/* Kept set of one row (flashinfer's filter semantics), kept[i] = 1/0:
+ *   mode 0 every p > 0; 1 top_p: keep i iff sum_{p_j > p_i} p_j < top_p * sum_j p_j (the most
+ *   probable tokens always stay, which matters only for top_p <= 0);
+ *   2 top_k: keep i iff #{j : p_j > p_i} < k (all tokens tied with the k-th largest stay;
+ *   k <= 0 or k >= V keeps all); 3 min_p: keep i iff p_i >= min_p * max_j p_j;
+ *   4 top_k then top_p inside the top-k set (the top-p mass rule over that set).
+ * Only p > 0 is ever kept; negative or NaN probabilities count as 0.                           */
+static double pval(float p) { return p > 0.f ? (double)p : 0.0; }
+
+typedef struct { double p; int64_t i; } PI;
+static int cmp_desc(const void* x, const void* y) {
+  const double a = ((const PI*)x)->p, b = ((const PI*)y)->p;
+  return a < b ? 1 : a > b ? -1 : 0;
+}
+
+/* Sorts the positive probabilities once (descending) and applies the rules group by group of
+ * equal values, so ties share one decision; O(V log V).                                     */
+static void kept_set(const float* p, int64_t V, int mode, int32_t k, double top_p, double min_p,
+                     unsigned char* kept) {
+  PI* s = (PI*)malloc(sizeof(PI) * (size_t)(V > 0 ? V : 1));
+  int64_t n = 0;
+  for (int64_t i = 0; i < V; ++i) {
+    kept[i] = 0;
+    if (pval(p[i]) > 0) { s[n].p = pval(p[i]); s[n].i = i; ++n; }
+  }
+  qsort(s, (size_t)n, sizeof(PI), cmp_desc);
+  int64_t m = n;  /* s[0..m) is the current kept set, most probable first */
+  if ((mode == 2 || mode == 4) && k > 0 && k < n) {
+    const double tau = s[k - 1].p;
+    m = k;
+    while (m < n && s[m].p == tau) ++m;
+  }
+  if (mode == 1 || mode == 4) {
+    double tot = 0;
+    for (int64_t j = 0; j < m; ++j) tot += s[j].p;
+    double above = 0;
+    int64_t j = 0, keep = 0;
+    while (j < m) {
+      int64_t e = j;
+      double g = 0;
+      while (e < m && s[e].p == s[j].p) { g += s[e].p; ++e; }
+      if (above < top_p * tot || j == 0) keep = e; /* the most probable tokens always stay */
+      else break;
+      above += g;
+      j = e;
+    }
+    m = keep;
+  }
+  if (mode == 3) {
+    const double thr = n > 0 ? min_p * s[0].p : 0;
+    int64_t e = 0;
+    while (e < m && s[e].p >= thr) ++e;
+    m = e;
+  }
+  for (int64_t j = 0; j < m; ++j) kept[s[j].i] = 1;
+  free(s);
+}
+
+/* Inverse-CDF draw in index order over the kept set: the first kept index whose running kept
+ * mass exceeds u * (total kept mass); -1 if nothing is kept. kept_out (optional) receives the
+ * kept set, row-major [B, V].                                                                   */
+void oracle_sample(const float* probs, int64_t B, int64_t V, int64_t stride, int mode,
+                   const int32_t* top_k, const float* top_p, const float* min_p, const double* u,
+                   int32_t* out, unsigned char* kept_out) {
+  unsigned char* kept = (unsigned char*)malloc((size_t)(V > 0 ? V : 1));
+  for (int64_t r = 0; r < B; ++r) {
+    const float* p = probs + r * stride;
+    kept_set(p, V, mode, top_k ? top_k[r] : 0, top_p ? top_p[r] : 1.0, min_p ? min_p[r] : 0.0, kept);
+    if (kept_out) memcpy(kept_out + r * V, kept, (size_t)V);
+    double tot = 0;
+    for (int64_t i = 0; i < V; ++i) if (kept[i]) tot += pval(p[i]);
+    const double target = u[r] * tot;
+    int32_t pick = -1, last = -1;
+    double run = 0;
+    for (int64_t i = 0; i < V; ++i) {
+      if (!kept[i]) continue;
+      last = (int32_t)i;
+      run += pval(p[i]);
+      if (run > target) { pick = (int32_t)i; break; }
+    }
+    out[r] = pick >= 0 ? pick : last;
+  }
+  free(kept);
 }

@@ -15,6 +15,7 @@ LIB_PATH = Path(os.environ.get("PIE_HIP_LIB", _PKG / "libpie_hip.so"))
 HEADER = _PKG.parent / "include" / "pie_hip.h"
 
 i64, i32, f32, vp = C.c_int64, C.c_int, C.c_float, C.c_void_p
+u64 = C.c_uint64
 
 # name -> argtypes (restype is int for all but pie_hip_last_error)
 SIGNATURES: dict[str, list] = {
@@ -51,6 +52,8 @@ SIGNATURES: dict[str, list] = {
                                        vp],
     "pie_hip_attention_prefill": [vp, i64, i64, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, i64,
                                   i64, i64, i64, f32, i32, vp, vp, i64, i64, vp, i64, i64, vp],
+    "pie_hip_sample": [vp, i64, i64, i64, i64, vp, i32, vp, i32, vp, f32, vp, f32, vp, u64, u64, vp, vp],
+    "pie_hip_scaled_softmax": [vp, i32, i64, i64, i64, vp, f32, vp, i64, vp],
     "pie_hip_get_seq_lens": [vp, vp, i64, i64, vp, vp],
     "pie_hip_get_batch_indices_positions": [vp, vp, i64, i64, vp, vp, vp],
 }

@@ -7,7 +7,8 @@ The model files choose their kernel namespace at import time
     else:                  import flashinfer as ops
 
 ``install()`` registers a module named ``flashinfer`` whose hot-path functions are this
-package's gfx950 kernels, as are the paged-attention wrappers. Every other attribute (sampling, ...) is
+package's gfx950 kernels, as are the paged-attention wrappers and the ``flashinfer.sampling``
+submodule (Pie's samplers, pie/src/pie_worker/model/common.py:13-28). Every other attribute is
 looked up in the real flashinfer package when one is importable, and raises AttributeError
 otherwise. Call it before the model modules are imported; it is idempotent.
 """
@@ -17,7 +18,7 @@ import importlib
 import sys
 import types
 
-from . import attention, ops
+from . import attention, ops, sampling
 
 # flashinfer names this package serves (the calls at llama3.py:660-755, qwen3.py:665-684,
 # gemma2.py:608, gpt_oss.py:671-678).
@@ -46,6 +47,7 @@ class _Namespace(types.ModuleType):
             setattr(self, n, getattr(ops, n))
         for n in ATTENTION:
             setattr(self, n, getattr(attention, n))
+        self.sampling = sampling  # `from flashinfer.sampling import ...` (common.py:13-28)
 
     def __getattr__(self, item):
         fb = self.__dict__.get("_fallback")
@@ -68,6 +70,8 @@ def install(name: str = "flashinfer") -> types.ModuleType:
             fallback = None
     mod = _Namespace(name, fallback)
     sys.modules[name] = mod
+    mod._saved_sampling = sys.modules.get(name + ".sampling")
+    sys.modules[name + ".sampling"] = sampling
     return mod
 
 
@@ -75,6 +79,10 @@ def uninstall(name: str = "flashinfer") -> None:
     """Undo install(): restore the real module (if any)."""
     cur = sys.modules.get(name)
     if isinstance(cur, _Namespace):
+        if cur._saved_sampling is not None:
+            sys.modules[name + ".sampling"] = cur._saved_sampling
+        else:
+            sys.modules.pop(name + ".sampling", None)
         if cur._fallback is not None:
             sys.modules[name] = cur._fallback
         else:

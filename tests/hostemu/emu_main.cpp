@@ -3,7 +3,7 @@
 // the results with the CPU oracle (oracle/oracle.c). TEST INFRASTRUCTURE.
 //
 //   emu_main <case>    case = norm | qk | silu | embed | rope | fused | decode | index | qkfused |
-//                      variants | fastdiv | attn | all | big
+//                      variants | fastdiv | attn | prefill | sample | all | big
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -44,6 +44,9 @@ void oracle_attention(const uint16_t*, int64_t, int64_t, const uint16_t*, const 
                       int64_t, int64_t, const int32_t*, const int32_t*, const int32_t*, const int32_t*,
                       const uint8_t*, const int64_t*, int, int64_t, int64_t, int64_t, int64_t, int64_t, double,
                       uint16_t*, int64_t, int64_t, double*);
+void oracle_sample(const float*, int64_t, int64_t, int64_t, int, const int32_t*, const float*, const float*,
+                   const double*, int32_t*, unsigned char*);
+void oracle_scaled_softmax(const float*, int64_t, int64_t, const float*, double, double*);
 void oracle_seq_lens(const int32_t*, const int32_t*, int64_t, int64_t, int32_t*);
 void oracle_batch_indices_positions(const int32_t*, const int32_t*, int64_t, int64_t, int32_t*, int32_t*);
 }
@@ -461,6 +464,61 @@ static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
   failures += !(worst <= 1.f);
 }
 
+// ---------------------------------------------------------------------------- sampling
+// Probabilities are multiples of 2^-30 (exact in the kernel's 2^-40 fixed point and in float64),
+// so kept sets and draws must match the oracle exactly; ties are forced in some rows.
+static void case_sample(int64_t B, int64_t V, int mode, bool row_map) {
+  printf("sample B=%lld V=%lld mode=%d rows=%d\n", (long long)B, (long long)V, mode, (int)row_map);
+  Buf<float> probs(B * V);
+  std::uniform_int_distribution<int> dq(0, 1 << 12);
+  for (int64_t r = 0; r < B; ++r) {
+    double tot = 0;
+    for (int64_t i = 0; i < V; ++i) { probs[r * V + i] = (float)dq(rng); tot += probs[r * V + i]; }
+    if (r % 3 == 1) for (int64_t i = 0; i < V; i += 7) probs[r * V + i] = probs[r * V];  // ties
+    if (r % 4 == 2) probs[r * V + 3] = 0.f;
+    for (int64_t i = 0; i < V; ++i) probs[r * V + i] = (float)(ldexp(floor(probs[r * V + i] / tot * 1073741824.0), -30));
+  }
+  Buf<int32_t> rows(B), topk(B), out(B), want(B);
+  Buf<float> topp(B), minp(B);
+  Buf<double> u(B);
+  std::uniform_real_distribution<double> du(0.0, 1.0);
+  std::uniform_int_distribution<int> dk(1, (int)V + 2);
+  for (int64_t r = 0; r < B; ++r) {
+    rows[r] = row_map ? (int32_t)((r * 5 + 1) % B) : (int32_t)r;
+    topk[r] = r == 0 ? 0 : dk(rng);
+    topp[r] = (float)du(rng);
+    minp[r] = (float)du(rng) * 0.5f;
+    u[r] = du(rng);
+  }
+  rc_ok(pie_hip_sample(probs.p, V, B, V, B, row_map ? rows.p : nullptr, mode, topk.p, 0, topp.p, 0.f, minp.p, 0.f,
+                       u.p, 0, 0, out.p, nullptr), "sample");
+  Buf<float> mapped(B * V);
+  for (int64_t r = 0; r < B; ++r) memcpy(mapped.p + r * V, probs.p + (int64_t)rows[r] * V, V * 4);
+  oracle_sample(mapped.p, B, V, V, mode, topk.p, topp.p, minp.p, u.p, want.p, nullptr);
+  check_equal("sample", out.p, want.p, B);
+}
+
+static void case_softmax(int64_t B, int64_t V, bool bf16) {
+  printf("scaled_softmax B=%lld V=%lld bf16=%d\n", (long long)B, (long long)V, (int)bf16);
+  Buf<float> x(B * V), temps(B), out(B * V);
+  Buf<uint16_t> xb(B * V), ob(B * V);
+  std::normal_distribution<float> d(0.f, 3.f);
+  for (int64_t i = 0; i < B * V; ++i) { xb[i] = f2bf(d(rng)); x[i] = bf2f(xb[i]); }
+  for (int64_t r = 0; r < B; ++r) temps[r] = r == 0 ? 0.f : 0.3f + 0.4f * (float)r;
+  if (bf16) rc_ok(pie_hip_scaled_softmax(xb.p, 1, V, B, V, temps.p, 1e-5f, ob.p, V, nullptr), "softmax");
+  else rc_ok(pie_hip_scaled_softmax(x.p, 0, V, B, V, temps.p, 1e-5f, out.p, V, nullptr), "softmax");
+  std::vector<double> want(B * V);
+  oracle_scaled_softmax(x.p, B, V, temps.p, 1e-5, want.data());
+  size_t bad = 0;
+  for (int64_t i = 0; i < B * V; ++i) {
+    const double g = bf16 ? bf2f(ob[i]) : out[i];
+    if (!(fabs(g - want[i]) <= 1e-2 * fabs(want[i]) + 1e-7)) ++bad;
+  }
+  printf("  %-40s %s (%zu / %lld outside 1e-2 rel + 1e-7 abs)\n", "scaled_softmax", bad ? "FAIL" : "ok", bad,
+         (long long)(B * V));
+  failures += bad != 0;
+}
+
 static void case_index(int64_t B) {
   printf("index helpers B=%lld\n", (long long)B);
   Paged pg = make_paged(B, 16, 0, 100, 0, 9);
@@ -548,6 +606,12 @@ int main(int argc, char** argv) {
     case_attn_decode(2, 6, 1, 256, 8, 30, 300, 0);    // G = 6, D = 256, library's split count
     case_attn_decode(2, 16, 1, 128, 5, 20, 700, 5);   // G = 16, page size 5
     case_attn_decode(2, 4, 2, 64, 1, 600, 1500, 1);   // page size 1: several page-table windows
+  }
+  if (all || c == "sample") {
+    for (int mode = 0; mode <= 4; ++mode) case_sample(5, 301, mode, mode == 4);
+    case_sample(3, 4099, 4, false);  // several 4096-element scan tiles
+    case_softmax(3, 1000, false);
+    case_softmax(3, 777, true);
   }
   if (all || c == "prefill") {
     case_attn_prefill(3, 8, 2, 128, 16, 40, 45, 1);   // causal, chunked prefill over cached context

@@ -25,6 +25,7 @@ struct dim3 {
 struct uint2 { unsigned x, y; };
 struct uint4 { unsigned x, y, z, w; };
 struct float2 { float x, y; };
+struct float4 { float x, y, z, w; };
 inline uint4 make_uint4(unsigned a, unsigned b, unsigned c, unsigned d) { return uint4{a, b, c, d}; }
 inline float2 make_float2(float a, float b) { return float2{a, b}; }
 
@@ -230,5 +231,11 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 inline float __uint_as_float(unsigned u) { float f; memcpy(&f, &u, 4); return f; }
 inline int min(int a, int b) { return a < b ? a : b; }
 inline int max(int a, int b) { return a > b ? a : b; }
+inline unsigned max(unsigned a, unsigned b) { return a > b ? a : b; }
+// Atomics on block-shared memory (emulated threads of one block run concurrently).
+inline unsigned atomicAdd(unsigned* p, unsigned v) { return __atomic_fetch_add(p, v, __ATOMIC_RELAXED); }
+inline unsigned long long atomicAdd(unsigned long long* p, unsigned long long v) {
+  return __atomic_fetch_add(p, v, __ATOMIC_RELAXED);
+}
 inline float rsqrtf(float x) { return 1.0f / sqrtf(x); }
 inline unsigned __umulhi(unsigned a, unsigned b) { return (unsigned)(((unsigned long long)a * b) >> 32); }

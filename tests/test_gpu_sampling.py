@@ -1,0 +1,159 @@
+"""GPU parity of the sampling path: Pie's safe_scaled_softmax (fp32 and bf16 logits, greedy
+rows) against the float64 oracle, and the five flashinfer samplers. With caller-given uniforms
+and probabilities on a 2^-30 grid (exact in the kernel's fixed point and in float64) every draw
+must equal the oracle's exactly; with the kernel's own Philox numbers the draws must follow the
+kept-set distribution (chi-square over 40k draws with a fixed seed) and stay inside the kept set
+at full vocabulary size (Llama-3 128256, Qwen3 151936)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from pie_amd import sampling
+from tests._util import assert_bf16_close
+
+pytestmark = pytest.mark.gpu
+N = oracle.to_np
+SAMPLERS = {
+    "plain": lambda p, **kw: sampling.sampling_from_probs(p, **kw),
+    "top_p": lambda p, top_p, **kw: sampling.top_p_sampling_from_probs(p, top_p, **kw),
+    "top_k": lambda p, top_k, **kw: sampling.top_k_sampling_from_probs(p, top_k, **kw),
+    "min_p": lambda p, min_p, **kw: sampling.min_p_sampling_from_probs(p, min_p, **kw),
+    "top_k_top_p": lambda p, top_k, top_p, **kw: sampling.top_k_top_p_sampling_from_probs(
+        p, top_k, top_p, **kw),
+}
+
+
+def _grid_probs(B, V, seed, ties=True):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randint(0, 4097, (B, V), generator=g).double() ** 2
+    if ties:
+        w[1::3, ::7] = w[1::3, :1]  # many tokens tied with one value
+        w[2::4, 3] = 0
+    p = w / w.sum(-1, keepdim=True)
+    return (torch.floor(p * 2**30) / 2**30).float()
+
+
+def _params(B, V, seed):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randint(1, V + 3, (B,), generator=g).to(torch.int32)
+    k[0] = 0
+    return dict(top_k=k, top_p=torch.rand(B, generator=g) * 0.98 + 0.01,
+                min_p=torch.rand(B, generator=g) * 0.5,
+                u=torch.rand(B, generator=g, dtype=torch.float64))
+
+
+def _call(mode, probs, prm, **kw):
+    args = {"plain": {}, "top_p": {"top_p": prm["top_p"]}, "top_k": {"top_k": prm["top_k"]},
+            "min_p": {"min_p": prm["min_p"]},
+            "top_k_top_p": {"top_k": prm["top_k"], "top_p": prm["top_p"]}}[mode]
+    return SAMPLERS[mode](probs, **args, **kw)
+
+
+@pytest.mark.parametrize("mode", list(SAMPLERS))
+@pytest.mark.parametrize("V", [301, 4099, 32000])
+def test_sample_exact_vs_oracle(dev, mode, V):
+    print(f"sample mode={mode} V={V}", flush=True)
+    B = 24
+    probs = _grid_probs(B, V, V + len(mode))
+    prm = _params(B, V, V)
+    dp = {k: v.to(dev) for k, v in prm.items()}
+    got = _call(mode, probs.to(dev), dp, uniforms=dp["u"]).cpu().numpy()
+    want, kept = oracle.sample(probs.numpy(), mode, prm["u"].numpy(), top_k=prm["top_k"].numpy(),
+                               top_p=prm["top_p"].numpy(), min_p=prm["min_p"].numpy())
+    assert (got == want).all(), f"rows {np.nonzero(got != want)[0][:5]}: {got[got != want][:5]} vs {want[got != want][:5]}"
+    assert kept[np.arange(B), got].all()
+
+
+def test_sample_scalar_params_and_row_indices(dev):
+    B, V = 16, 1000
+    probs = _grid_probs(B, V, 5)
+    u = torch.rand(12, generator=torch.Generator().manual_seed(6), dtype=torch.float64)
+    idx = torch.tensor([3, 3, 0, 15, 7, 7, 7, 1, 2, 9, 11, 4], dtype=torch.int32)
+    got = sampling.top_k_top_p_sampling_from_probs(probs.to(dev), 50, 0.7, indices=idx.to(dev),
+                                                   uniforms=u.to(dev)).cpu().numpy()
+    want, _ = oracle.sample(probs[idx.long()].numpy(), "top_k_top_p", u.numpy(), top_k=50, top_p=0.7)
+    assert (got == want).all()
+
+
+def test_sample_distribution_with_philox(dev):
+    """40k draws of one 8-token distribution per mode, fixed seed: chi-square against the
+    renormalised kept set (p-value above 1e-4 for every mode)."""
+    from scipy.stats import chisquare
+    p = torch.tensor([0.02, 0.3, 0.05, 0.2, 0.13, 0.1, 0.15, 0.05])
+    n = 40000
+    probs = p.repeat(n, 1).to(dev)
+    for mode in SAMPLERS:
+        prm = dict(top_k=4, top_p=0.6, min_p=0.3, u=None)
+        got = _call(mode, probs, prm, seed=1234, offset=7).cpu().numpy()
+        _, kept = oracle.sample(p[None].numpy(), mode, [0.5], top_k=4, top_p=0.6, min_p=0.3)
+        kept = kept[0]
+        assert kept[got].all(), mode
+        counts = np.bincount(got, minlength=8)[kept]
+        expect = p.numpy()[kept].astype(np.float64)
+        expect = expect / expect.sum() * n
+        pv = chisquare(counts, expect).pvalue
+        assert pv > 1e-4, f"{mode}: p-value {pv}, counts {counts}, expected {expect}"
+
+
+def test_sample_reproducible_by_seed_and_offset(dev):
+    probs = _grid_probs(64, 5000, 9).to(dev)
+    a = sampling.sampling_from_probs(probs, seed=42, offset=3)
+    b = sampling.sampling_from_probs(probs, seed=42, offset=3)
+    c = sampling.sampling_from_probs(probs, seed=42, offset=4)
+    assert torch.equal(a, b) and not torch.equal(a, c)
+    g = torch.Generator().manual_seed(77)
+    d, e = sampling.sampling_from_probs(probs, generator=g), sampling.sampling_from_probs(probs, generator=g)
+    assert not torch.equal(d, e)  # the generator's offset advances
+
+
+@pytest.mark.parametrize("V", [128256, 151936])
+def test_sample_full_vocab_kept_sets(dev, V):
+    """Full vocabulary, softmax of N(0, 3) logits (as after the LM head): every mode's draws stay
+    in the oracle's kept set, and with given uniforms equal the oracle's draw except where the
+    fp32 probabilities' 2^-40 rounding moves a boundary (none expected here)."""
+    B = 32
+    g = torch.Generator().manual_seed(V)
+    logits = torch.randn(B, V, generator=g) * 3
+    probs = torch.softmax(logits.double(), -1).float()
+    prm = _params(B, V, 11)
+    prm["top_k"] = torch.randint(1, 200, (B,), generator=g).to(torch.int32)
+    dp = {k: v.to(dev) for k, v in prm.items()}
+    for mode in SAMPLERS:
+        got = _call(mode, probs.to(dev), dp, uniforms=dp["u"]).cpu().numpy()
+        want, kept = oracle.sample(probs.numpy(), mode, prm["u"].numpy(), top_k=prm["top_k"].numpy(),
+                                   top_p=prm["top_p"].numpy(), min_p=prm["min_p"].numpy())
+        assert kept[np.arange(B), got].all(), mode
+        assert (got == want).mean() >= 0.9, f"{mode}: {(got == want).mean()}"
+        free = _call(mode, probs.to(dev), dp, seed=5, offset=0).cpu().numpy()
+        assert kept[np.arange(B), free].all(), f"{mode} (Philox)"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_safe_scaled_softmax(dev, dtype):
+    B, V = 8, 128256
+    g = torch.Generator().manual_seed(21)
+    logits = (torch.randn(B, V, generator=g) * 4).to(dtype)
+    temps = torch.tensor([0.0, 1e-6, 0.3, 0.7, 1.0, 1.0, 1.7, 5.0])
+    got = sampling.safe_scaled_softmax(logits.to(dev), temps.to(dev))
+    want = oracle.scaled_softmax(logits.float().numpy(), temps.numpy())
+    gotf = got.float().cpu().numpy().astype(np.float64)
+    assert (gotf[:2] == want[:2]).all(), "greedy rows are exact one-hots"
+    rel = 2 ** -7 if dtype == torch.bfloat16 else 1e-5
+    bad = np.abs(gotf - want) > rel * np.abs(want) + 1e-30
+    assert not bad.any(), f"{bad.sum()} entries off, first {np.argwhere(bad)[:3]}"
+    np.testing.assert_allclose(gotf[2:].sum(-1), 1.0, rtol=2e-2 if dtype == torch.bfloat16 else 1e-5)
+
+
+def test_sampling_chain_like_pie(dev):
+    """Pie's order (common.py:226-283): softmax with temperatures, then a sampler per group."""
+    B, V = 6, 32000
+    logits = torch.randn(B, V, generator=torch.Generator().manual_seed(3)).to(dev) * 2
+    temps = torch.tensor([0.0, 0.8, 0.8, 1.0, 1.2, 0.5], device=dev)
+    probs = sampling.safe_scaled_softmax(logits, temps)
+    tok = sampling.top_k_top_p_sampling_from_probs(probs, 40, 0.9, seed=1, offset=0)
+    assert tok.dtype == torch.int32 and tok.shape == (B,)
+    assert int(tok[0]) == int(logits[0].argmax())  # greedy row
+    assert ((tok >= 0) & (tok < V)).all()

@@ -115,9 +115,13 @@ def test_integration_installs_flashinfer_namespace():
         from pie_amd import attention
         for n in integration.ATTENTION:
             assert getattr(fi, n) is getattr(attention, n)
+        from pie_amd import sampling
+        assert fi.sampling is sampling
+        from flashinfer.sampling import top_k_top_p_sampling_from_probs  # Pie's import form
+        assert top_k_top_p_sampling_from_probs is sampling.top_k_top_p_sampling_from_probs
         with pytest.raises(AttributeError):
-            fi.sampling  # not served here, and no real flashinfer
+            fi.BatchAttentionWithAttentionSinkWrapper  # not served here, and no real flashinfer
         assert integration.install() is mod  # idempotent
     finally:
         integration.uninstall()
-    assert "flashinfer" not in sys.modules
+    assert "flashinfer" not in sys.modules and "flashinfer.sampling" not in sys.modules

@@ -560,3 +560,71 @@ def test_attention_page_permutation_invariant():
     a2 = dict(a, cache=cache2)
     pb.kv_indices = perm[pb.kv_indices.long()].to(torch.int32)
     assert_bits_equal(_oracle_attn(a2), base, "page permutation")
+
+
+# ----------------------------------------------------------------------------- sampling path
+def _hf_kept(scores: torch.Tensor, mode: str, k=None, p=None, m=None) -> torch.Tensor:
+    """Kept sets from transformers' logits warpers (a local library routine): top-p keeps the
+    smallest most-probable set reaching p, top-k the k best (ties at the k-th value stay), min-p
+    tokens with prob >= m * max."""
+    from transformers.generation.logits_process import (MinPLogitsWarper, TopKLogitsWarper,
+                                                        TopPLogitsWarper)
+    lg = torch.log(scores)
+    if mode == "top_p":
+        lg = TopPLogitsWarper(top_p=p)(None, lg)
+    elif mode == "top_k":
+        lg = TopKLogitsWarper(top_k=k)(None, lg)
+    elif mode == "min_p":
+        lg = MinPLogitsWarper(min_p=m)(None, lg)
+    return torch.isfinite(lg)
+
+
+@pytest.mark.parametrize("mode", ["top_p", "top_k", "min_p"])
+def test_sample_kept_sets_vs_transformers_warpers(mode):
+    g = torch.Generator().manual_seed(31)
+    for trial in range(20):
+        V = int(torch.randint(5, 300, (1,), generator=g))
+        probs = torch.rand(1, V, generator=g, dtype=torch.float64) ** 3
+        probs /= probs.sum()
+        k = int(torch.randint(1, V + 3, (1,), generator=g))
+        p = float(torch.rand(1, generator=g)) * 0.98 + 0.01
+        m = float(torch.rand(1, generator=g)) * 0.9
+        want = _hf_kept(probs, mode, k=k, p=p, m=m)[0].numpy()
+        _, kept = oracle.sample(probs.float().numpy(), mode, [0.5], top_k=[k], top_p=[p], min_p=[m])
+        assert (kept[0] == want).all(), f"{mode} trial {trial}: V={V} k={k} p={p} m={m}"
+
+
+def test_sample_closed_forms():
+    probs = np.array([[0.1, 0.4, 0.2, 0.3]], np.float32)
+    # plain inverse CDF in index order: cumulative 0.1, 0.5, 0.7, 1.0
+    for u, want in ((0.0, 0), (0.05, 0), (0.1, 1), (0.49, 1), (0.5, 2), (0.69, 2), (0.7, 3), (0.99, 3)):
+        assert oracle.sample(probs, "plain", [u])[0][0] == want, u
+    # top_k = 1 and tiny top_p are greedy; top_k >= V and top_p = 1 keep everything
+    for u in (0.0, 0.3, 0.99):
+        assert oracle.sample(probs, "top_k", [u], top_k=[1])[0][0] == 1
+        assert oracle.sample(probs, "top_p", [u], top_p=[1e-6])[0][0] == 1
+    assert oracle.sample(probs, "top_k", [0.5], top_k=[9])[1].all()
+    assert oracle.sample(probs, "top_p", [0.5], top_p=[1.0])[1].all()
+    # top_p 0.6: 0.4 (mass above 0 < 0.6) and 0.3 (above 0.4 < 0.6) stay, 0.2 (above 0.7) goes
+    assert (oracle.sample(probs, "top_p", [0.5], top_p=[0.6])[1][0] == [False, True, False, True]).all()
+    # min_p 0.6: threshold 0.24 keeps 0.4 and 0.3
+    assert (oracle.sample(probs, "min_p", [0.5], min_p=[0.6])[1][0] == [False, True, False, True]).all()
+    # top_k 3 then top_p 0.5 inside {0.4, 0.3, 0.2} (mass 0.9, threshold 0.45): 0.4 and 0.3 stay
+    assert (oracle.sample(probs, "top_k_top_p", [0.5], top_k=[3], top_p=[0.5])[1][0]
+            == [False, True, False, True]).all()
+    # ties at the k-th value all stay
+    tied = np.array([[0.3, 0.2, 0.2, 0.2, 0.1]], np.float32)
+    assert (oracle.sample(tied, "top_k", [0.5], top_k=[2])[1][0] == [True, True, True, True, False]).all()
+
+
+def test_scaled_softmax_vs_torch_reference():
+    """Against Pie's own torch form (_safe_scaled_softmax_impl_torch, common.py:38-59) in fp64."""
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(4, 500, generator=g) * 4
+    temps = torch.tensor([0.0, 0.5, 1.0, 2.5])
+    safe = torch.where(temps[:, None] < 1e-5, 1.0, temps[:, None].double())
+    soft = torch.softmax(x.double() / safe, -1)
+    greedy = F.one_hot(x.argmax(-1), 500).double()
+    want = torch.where(temps[:, None] < 1e-5, greedy, soft)
+    np.testing.assert_allclose(oracle.scaled_softmax(x.numpy(), temps.numpy()), want.numpy(),
+                               rtol=1e-12, atol=1e-300)
