@@ -102,8 +102,20 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, SampleShared& sh) 
 template <typename F>
 __device__ __forceinline__ void for_row(const float* p, int V, bool vec, F&& f) {
   if (vec) {
+    // four 16-byte loads in flight per thread before any is used
     const int nv = V >> 2;
-    for (int i = threadIdx.x; i < nv; i += kSampThreads) {
+    int i = threadIdx.x;
+    for (; i + 3 * kSampThreads < nv; i += 4 * kSampThreads) {
+      float4 x[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) x[k] = *reinterpret_cast<const float4*>(p + 4 * (i + k * kSampThreads));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int j = 4 * (i + k * kSampThreads);
+        f(j, x[k].x); f(j + 1, x[k].y); f(j + 2, x[k].z); f(j + 3, x[k].w);
+      }
+    }
+    for (; i < nv; i += kSampThreads) {
       const float4 x = *reinterpret_cast<const float4*>(p + 4 * i);
       f(4 * i, x.x); f(4 * i + 1, x.y); f(4 * i + 2, x.z); f(4 * i + 3, x.w);
     }
@@ -294,60 +306,118 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
 }
 
 // safe_scaled_softmax: probs = softmax(logits / T) per row, or the one-hot of the first maximum
-// when T < greedy_threshold. fp32 math in the exp2 domain; output in the logits' dtype.
+// when T < greedy_threshold. Two passes over the row: (max, first argmax, sum of exp2 relative to
+// a running max) with 16-byte loads, then the normalised write; fp32 math in the exp2 domain,
+// output in the logits' dtype.
+template <bool BF16>
+struct RowIO {
+  static constexpr int E = BF16 ? 8 : 4;  // elements per 16-byte vector
+  __device__ static void load(const void* base, int64_t i, float (&x)[E]) {
+    const uint4 v = ld16(reinterpret_cast<const char*>(base) + i * (BF16 ? 2 : 4));
+    if (BF16) unpack8(v, x);
+    else { x[0] = __uint_as_float(v.x); x[1] = __uint_as_float(v.y); x[2] = __uint_as_float(v.z); x[3] = __uint_as_float(v.w); }
+  }
+  __device__ static void store(void* base, int64_t i, const float (&x)[E]) {
+    uint4 v;
+    if (BF16) v = pack8(x);
+    else v = make_uint4(__builtin_bit_cast(uint32_t, x[0]), __builtin_bit_cast(uint32_t, x[1]),
+                        __builtin_bit_cast(uint32_t, x[2]), __builtin_bit_cast(uint32_t, x[3]));
+    st_nt(reinterpret_cast<char*>(base) + i * (BF16 ? 2 : 4), v);
+  }
+  __device__ static float get(const void* base, int64_t i) {
+    return BF16 ? bf1(reinterpret_cast<const uint16_t*>(base)[i]) : reinterpret_cast<const float*>(base)[i];
+  }
+  __device__ static void put(void* base, int64_t i, float v) {
+    if (BF16) reinterpret_cast<uint16_t*>(base)[i] = to_bf1(v);
+    else reinterpret_cast<float*>(base)[i] = v;
+  }
+};
+
 template <bool BF16>
 __global__ __launch_bounds__(kSampThreads) void scaled_softmax_kernel(const void* __restrict__ logits,
                                                                       int64_t stride, int V,
                                                                       const float* __restrict__ temps,
                                                                       float greedy, void* __restrict__ out,
-                                                                      int64_t out_stride) {
-  __shared__ float sm[kSampWaves];
+                                                                      int64_t out_stride, int vec) {
+  using IO = RowIO<BF16>;
+  constexpr int E = IO::E;
+  __shared__ float sm[kSampWaves], ss[kSampWaves];
   __shared__ int si[kSampWaves];
   const int r = blockIdx.x;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  auto ld = [&](int i) -> float {
-    return BF16 ? bf1(reinterpret_cast<const uint16_t*>(logits)[(int64_t)r * stride + i])
-                : reinterpret_cast<const float*>(logits)[(int64_t)r * stride + i];
-  };
-  auto st = [&](int i, float v) {
-    if (BF16) reinterpret_cast<uint16_t*>(out)[(int64_t)r * out_stride + i] = to_bf1(v);
-    else reinterpret_cast<float*>(out)[(int64_t)r * out_stride + i] = v;
-  };
-  // max and first argmax
-  float mx = -INFINITY;
+  const char* row = reinterpret_cast<const char*>(logits) + (int64_t)r * stride * (BF16 ? 2 : 4);
+  char* orow = reinterpret_cast<char*>(out) + (int64_t)r * out_stride * (BF16 ? 2 : 4);
+  const float T = temps[r];
+  const bool greedy_row = T < greedy;
+  const float c = greedy_row ? 1.f : 1.4426950408889634f / T;
+  // pass 1: max, first argmax and sum of exp2(x*c - running max) (online rescaling)
+  float mx = -INFINITY, s = 0.f;
   int am = 0x7fffffff;
-  for (int i = threadIdx.x; i < V; i += kSampThreads) {
-    const float x = ld(i);
-    if (x > mx) { mx = x; am = i; }
+  auto visit = [&](float x, int i) {
+    if (x > mx) {
+      s = s * __builtin_amdgcn_exp2f((mx - x) * c);  // mx = -inf first: exp2(-inf) = 0
+      mx = x;
+      am = i;
+    }
+    s += __builtin_amdgcn_exp2f((x - mx) * c);
+  };
+  const int nv = vec ? V / E : 0;
+  int v = threadIdx.x;
+  for (; v + 3 * kSampThreads < nv; v += 4 * kSampThreads) {  // four 16-byte loads in flight
+    float x[4][E];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) IO::load(row, (int64_t)(v + k * kSampThreads) * E, x[k]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int e = 0; e < E; ++e) visit(x[k][e], (v + k * kSampThreads) * E + e);
   }
+  for (; v < nv; v += kSampThreads) {
+    float x[E];
+    IO::load(row, (int64_t)v * E, x);
+#pragma unroll
+    for (int e = 0; e < E; ++e) visit(x[e], v * E + e);
+  }
+  for (int i = nv * E + threadIdx.x; i < V; i += kSampThreads) visit(IO::get(row, i), i);
+  // combine (max, argmax, sum) across the wave, then across waves
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
     const float y = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, __builtin_bit_cast(int, mx)));
+    const float ys = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, __builtin_bit_cast(int, s)));
     const int yi = __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, am);
-    if (y > mx || (y == mx && yi < am)) { mx = y; am = yi; }
+    const float m2 = fmaxf(mx, y);
+    const float s2 = (mx == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f((mx - m2) * c)) +
+                     (y == -INFINITY ? 0.f : ys * __builtin_amdgcn_exp2f((y - m2) * c));
+    if (y > mx || (y == mx && yi < am)) am = yi;
+    mx = m2;
+    s = s2;
   }
-  if (lane == 0) { sm[w] = mx; si[w] = am; }
+  if (lane == 0) { sm[w] = mx; ss[w] = s; si[w] = am; }
   __syncthreads();
-  mx = sm[0]; am = si[0];
-  for (int i = 1; i < kSampWaves; ++i)
-    if (sm[i] > mx || (sm[i] == mx && si[i] < am)) { mx = sm[i]; am = si[i]; }
-  __syncthreads();
-  const float T = temps[r];
-  if (T < greedy) {
-    for (int i = threadIdx.x; i < V; i += kSampThreads) st(i, i == am ? 1.f : 0.f);
-    return;
+  float M = -INFINITY;
+  int A = 0x7fffffff;
+  for (int i = 0; i < kSampWaves; ++i)
+    if (sm[i] > M || (sm[i] == M && si[i] < A)) { M = sm[i]; A = si[i]; }
+  float S = 0.f;
+  for (int i = 0; i < kSampWaves; ++i)
+    if (sm[i] != -INFINITY) S += ss[i] * __builtin_amdgcn_exp2f((sm[i] - M) * c);
+  // pass 2: write
+  const float inv = 1.f / S;
+  const float mc = M * c;
+  for (int v = threadIdx.x; v < nv; v += kSampThreads) {
+    float x[E];
+    if (greedy_row) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) x[e] = (v * E + e) == A ? 1.f : 0.f;
+    } else {
+      IO::load(row, (int64_t)v * E, x);
+#pragma unroll
+      for (int e = 0; e < E; ++e) x[e] = __builtin_amdgcn_exp2f(fmaf(x[e], c, -mc)) * inv;
+    }
+    IO::store(orow, (int64_t)v * E, x);
   }
-  const float c = 1.4426950408889634f / T;
-  const float mc = mx * c;
-  float s = 0.f;
-  for (int i = threadIdx.x; i < V; i += kSampThreads) s += __builtin_amdgcn_exp2f(fmaf(ld(i), c, -mc));
-  s = wave_sum(s);
-  if (lane == 0) sm[w] = s;
-  __syncthreads();
-  float tot = 0.f;
-  for (int i = 0; i < kSampWaves; ++i) tot += sm[i];
-  const float inv = 1.f / tot;
-  for (int i = threadIdx.x; i < V; i += kSampThreads) st(i, __builtin_amdgcn_exp2f(fmaf(ld(i), c, -mc)) * inv);
+  for (int i = nv * E + threadIdx.x; i < V; i += kSampThreads)
+    IO::put(orow, i, greedy_row ? (i == A ? 1.f : 0.f) : __builtin_amdgcn_exp2f(fmaf(IO::get(row, i), c, -mc)) * inv);
 }
 
 }  // namespace pie
@@ -384,11 +454,13 @@ extern "C" int pie_hip_scaled_softmax(const void* logits, int32_t is_bf16, int64
               "scaled_softmax: bad shape");
   if (batch == 0) return PIE_HIP_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t e = is_bf16 ? 8 : 4;  // elements per 16-byte vector
+  const int vec = aligned16(logits) && aligned16(out) && stride % e == 0 && out_stride % e == 0;
   if (is_bf16)
     hipLaunchKernelGGL(scaled_softmax_kernel<true>, dim3((unsigned)batch), dim3(kSampThreads), 0, st, logits,
-                       stride, (int)vocab, temperatures, greedy_threshold, out, out_stride);
+                       stride, (int)vocab, temperatures, greedy_threshold, out, out_stride, vec);
   else
     hipLaunchKernelGGL(scaled_softmax_kernel<false>, dim3((unsigned)batch), dim3(kSampThreads), 0, st, logits,
-                       stride, (int)vocab, temperatures, greedy_threshold, out, out_stride);
+                       stride, (int)vocab, temperatures, greedy_threshold, out, out_stride, vec);
   return check_launch("scaled_softmax");
 }
