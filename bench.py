@@ -331,6 +331,27 @@ def _ops_attention(dev, run):
     e["tflops"] = round(flops / e["us"] / 1e6, 1)
     e["mfma_frac"] = round(flops / e["us"] / 1e6 / 2500.0, 3)
     res.append(e)
+    # the same causal window given as the custom mask Pie always passes (batching.py:226-228)
+    blocks = []
+    for b in range(pb.lens.numel()):
+        qo, kv = int(pb.lens[b]), int(pb.seq_lens[b])
+        blocks.append((torch.arange(kv, device=dev)[None, :] <=
+                       (kv - qo + torch.arange(qo, device=dev))[:, None]).flatten())
+    mask = torch.cat(blocks)
+    del blocks
+    wm = attention.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    wm.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev),
+            pb.kv_last_page_len.to(dev), 32, 8, 128, 16, custom_mask=mask)
+
+    def make_m():
+        q, out = q0.clone(), torch.empty_like(q0)
+        return lambda: wm.run(q, cache, out=out)
+    e = run(f"attn prefill custom causal mask cfg3 T={q0.shape[0]}", wl.attn_bytes(pb, 32, 8, 128), make_m)
+    e["flops"] = flops
+    e["tflops"] = round(flops / e["us"] / 1e6, 1)
+    e["mfma_frac"] = round(flops / e["us"] / 1e6 / 2500.0, 3)
+    res.append(e)
+    del mask
     del cache, ws
     return res
 

@@ -307,14 +307,26 @@ int pie_hip_attention_decode(const pie_bf16* q, int64_t q_tok_stride, int64_t q_
  *
  * pie_hip_attention_prefill_plan runs on the host over host copies of qo_indptr, kv_indptr and
  * kv_last_page_len and writes the work list (`plan`, int32 words; *num_items work groups per kv
- * head; for mode 2 the mask block offsets at word plan[3], and *mask_bytes = the mask's size).
- * The caller copies the plan to device memory and passes it, num_items and plan[3] to the run.
+ * head; for mode 2 the int64 byte offsets of the mask blocks at word plan[3] and of their packed
+ * words at plan[4], *mask_bytes = the mask's size, *mask_words = its packed size in uint32).
+ * The caller copies the plan to device memory. For mode 2, pie_hip_attention_pack_mask (device,
+ * on the stream) packs the byte mask into 32-position words (bit j of word w of query token i =
+ * position 32w+j; 0 past kv_len) in a caller buffer of mask_words uint32, and writes every query
+ * token's visible extent (1 + its last visible position; int32 [num_tokens]) so the run skips kv
+ * tiles no row of a work group can see. The run reads both with the plan, num_items and plan[4]
+ * (mask_offsets_word).
  */
 int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
                                    const int32_t* kv_last_page_len, int64_t batch,
                                    int64_t page_size, int64_t num_qo_heads, int64_t num_kv_heads,
                                    int64_t head_dim, int32_t mode, int32_t* plan, int64_t plan_capacity,
-                                   int64_t* plan_words, int64_t* num_items, int64_t* mask_bytes);
+                                   int64_t* plan_words, int64_t* num_items, int64_t* mask_bytes,
+                                   int64_t* mask_words);
+int pie_hip_attention_pack_mask(const uint8_t* custom_mask, const int32_t* plan,
+                                const int32_t* qo_indptr, const int32_t* kv_indptr,
+                                const int32_t* kv_last_page_len, int64_t batch, int64_t page_size,
+                                int64_t mask_words, int64_t num_tokens, uint32_t* packed_mask,
+                                int32_t* mask_extent, void* stream);
 int pie_hip_attention_prefill(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
                               const pie_bf16* k_cache, const pie_bf16* v_cache,
                               int64_t page_stride, int64_t slot_stride, int64_t head_stride,
@@ -322,8 +334,9 @@ int pie_hip_attention_prefill(const pie_bf16* q, int64_t q_tok_stride, int64_t q
                               const int32_t* kv_indptr, const int32_t* kv_indices,
                               const int32_t* kv_last_page_len, int64_t num_qo_heads,
                               int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
-                              float sm_scale, int32_t mode, const uint8_t* custom_mask,
-                              const int32_t* plan, int64_t num_items, int64_t mask_offsets_word,
+                              float sm_scale, int32_t mode, const uint32_t* packed_mask,
+                              const int32_t* mask_extent, const int32_t* plan, int64_t num_items,
+                              int64_t mask_offsets_word,
                               pie_bf16* out, int64_t o_tok_stride, int64_t o_head_stride,
                               void* stream);
 

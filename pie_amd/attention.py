@@ -219,12 +219,12 @@ class BatchPrefillWithPagedKVCacheWrapper:
         mode = 2 if mask is not None else (1 if causal else 0)
         G = num_qo_heads // num_kv_heads
         T = int(qo_h[-1]) if batch else 0
-        cap = 16 + 2 * (T * G // 64 + batch + 1) + 2 * batch + 2
+        cap = 16 + 2 * (T * G // 64 + batch + 1) + 4 * batch + 8
         plan = np.zeros(cap, dtype=np.int32)
-        words, items, mbytes = C.c_int64(0), C.c_int64(0), C.c_int64(0)
+        words, items, mbytes, mwords = C.c_int64(0), C.c_int64(0), C.c_int64(0), C.c_int64(0)
         _lib.call("pie_hip_attention_prefill_plan", qo_h.data_ptr(), kv_h.data_ptr(), ll_h.data_ptr(),
                   batch, page_size, num_qo_heads, num_kv_heads, head_dim_qk, mode, plan.ctypes.data, cap,
-                  C.byref(words), C.byref(items), C.byref(mbytes))
+                  C.byref(words), C.byref(items), C.byref(mbytes), C.byref(mwords))
         if mode == 2:
             if mask.dtype not in (torch.bool, torch.uint8):
                 raise ValueError(f"{name}: custom_mask must be bool, got {mask.dtype}")
@@ -233,18 +233,32 @@ class BatchPrefillWithPagedKVCacheWrapper:
                 raise ValueError(f"{name}: custom_mask has {mask.numel()} entries, the batch needs "
                                  f"{mbytes.value} (sum of qo_len * kv_len)")
             mask = mask.to(dev).contiguous()
-        nbytes = words.value * 4
+        # workspace layout: [plan words | packed mask words | per-token extents] (mode 2), each
+        # 16-byte aligned
+        nbytes = (words.value * 4 + 15) // 16 * 16
+        mask_off = nbytes
+        ext_off = mask_off + (mwords.value * 4 + 15) // 16 * 16
+        need = ext_off + T * 4 if mode == 2 else nbytes
         ws_bytes = self._workspace.numel() * self._workspace.element_size()
-        if nbytes > ws_bytes:
-            raise ValueError(f"{name}: the plan needs {nbytes} bytes of workspace, have {ws_bytes}")
-        plan_d = self._workspace.view(torch.uint8)[:nbytes].view(torch.int32)
+        if need > ws_bytes:
+            raise ValueError(f"{name}: the plan needs {need} bytes of workspace, have {ws_bytes}")
+        ws8 = self._workspace.view(torch.uint8)
+        plan_d = ws8[: words.value * 4].view(torch.int32)
         plan_d.copy_(torch.from_numpy(plan[: words.value]), non_blocking=False)
         tables = [t if t.device == dev else t.to(dev) for t in
                   (qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len)]
+        packed = extent = None
+        if mode == 2 and mwords.value:
+            packed = ws8[mask_off: mask_off + mwords.value * 4].view(torch.int32)
+            extent = ws8[ext_off: ext_off + T * 4].view(torch.int32)
+            _lib.call("pie_hip_attention_pack_mask", mask.data_ptr(), plan_d.data_ptr(),
+                      tables[0].data_ptr(), tables[1].data_ptr(), tables[3].data_ptr(), batch,
+                      page_size, mwords.value, T, packed.data_ptr(), extent.data_ptr(),
+                      _stream(plan_d))
         self._plan = dict(qo_indptr=tables[0], indptr=tables[1], indices=tables[2],
                           last_page_len=tables[3], batch=batch, T=T, Hq=num_qo_heads,
-                          Hkv=num_kv_heads, D=head_dim_qk, P=page_size, mode=mode, mask=mask,
-                          plan=plan_d, items=items.value, moff_word=int(plan[3]),
+                          Hkv=num_kv_heads, D=head_dim_qk, P=page_size, mode=mode, packed=packed, extent=extent,
+                          plan=plan_d, items=items.value, woff_word=int(plan[4]),
                           sm_scale=(1.0 / math.sqrt(head_dim_qk)) if sm_scale is None else sm_scale)
 
     begin_forward = plan
@@ -277,12 +291,15 @@ class BatchPrefillWithPagedKVCacheWrapper:
             _check(name, _BF16, out=out)
             if tuple(out.shape) != (T, Hq, D) or out.stride(2) != 1:
                 raise ValueError(f"{name}: out must be [{T}, {Hq}, {D}]")
-        mask = p["mask"]
+        packed = p["packed"]
+        if p["mode"] == 2 and packed is None:  # a mask over zero positions: nothing is visible
+            return out.zero_()
         _lib.call("pie_hip_attention_prefill", q.data_ptr(), q.stride(0), q.stride(1), kp, vp, ps,
                   ss, hs, npages, p["qo_indptr"].data_ptr(), p["indptr"].data_ptr(),
                   p["indices"].data_ptr(), p["last_page_len"].data_ptr(), Hq, Hkv, D, P,
-                  float(p["sm_scale"]), p["mode"], mask.data_ptr() if mask is not None else None,
-                  p["plan"].data_ptr(), p["items"], p["moff_word"], out.data_ptr(), out.stride(0),
+                  float(p["sm_scale"]), p["mode"], packed.data_ptr() if packed is not None else None,
+                  p["extent"].data_ptr() if p["extent"] is not None else None,
+                  p["plan"].data_ptr(), p["items"], p["woff_word"], out.data_ptr(), out.stride(0),
                   out.stride(1), _stream(q))
         return out
 

@@ -153,14 +153,21 @@ struct WaveAttn {
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < NS; ++st) acc = mfma_16x16x32(ka[u][st], qb[st], acc);
+      if (vmask == 0xFFu) {  // wave-uniform fast path for fully visible tiles
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[u][i] = ((vmask >> (4 * u + i)) & 1u) ? acc[i] * scale_log2 : -INFINITY;
+        for (int i = 0; i < 4; ++i) s[u][i] = acc[i] * scale_log2;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[u][i] = ((vmask >> (4 * u + i)) & 1u) ? acc[i] * scale_log2 : -INFINITY;
+      }
     }
   }
 
   // Online-softmax step: updates m and l, returns the tile's probabilities as the PV A-operand
-  // (bf16) and in a[i] the factor by which O row 4g+i must be rescaled.
-  __device__ __forceinline__ u32x4_t softmax(const float (&s)[2][4], int lane, float (&a)[4]) {
+  // (bf16) and in a[i] the factor by which O row 4g+i must be rescaled; rescale = false (a
+  // unset) when no row of the wave changed its maximum, so O needs no rescaling (wave-uniform).
+  __device__ __forceinline__ u32x4_t softmax(const float (&s)[2][4], int lane, float (&a)[4],
+                                             bool& rescale) {
     const int g = lane >> 4;
     float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
@@ -176,18 +183,24 @@ struct WaveAttn {
       for (int i = 0; i < 4; ++i) { p[u][i] = fast_exp2(s[u][i] - m_use); psum += p[u][i]; }
     l = l * alpha + psum;
     m = m_new;
-    // O rows 4g+i take the factor of row 4g+i (held by lane 4g+i of every group)
+    rescale = __builtin_amdgcn_ballot_w64(alpha != 1.f) != 0;
+    if (rescale) {
+      // O rows 4g+i take the factor of row 4g+i (held by lane 4g+i of every group)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = lane_read(alpha, 4 * g + i);
+      for (int i = 0; i < 4; ++i) a[i] = lane_read(alpha, 4 * g + i);
+    }
     return u32x4_t{pack_bf2(p[0][0], p[0][1]), pack_bf2(p[0][2], p[0][3]),
                    pack_bf2(p[1][0], p[1][1]), pack_bf2(p[1][2], p[1][3])};
   }
 
-  // O block nb = O block nb * a + P V_nb.
-  __device__ __forceinline__ void pv(const u32x4_t& pa, const u32x4_t& vb, const float (&a)[4], int nb) {
+  // O block nb = O block nb * a + P V_nb (no rescaling when softmax() reported none).
+  __device__ __forceinline__ void pv(const u32x4_t& pa, const u32x4_t& vb, const float (&a)[4], bool rescale,
+                                     int nb) {
     f32x4_t c = o[nb];
+    if (rescale) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) c[i] *= a[i];
+      for (int i = 0; i < 4; ++i) c[i] *= a[i];
+    }
     o[nb] = mfma_16x16x32(pa, vb, c);
   }
 
@@ -196,10 +209,11 @@ struct WaveAttn {
   __device__ __forceinline__ void tile(const u32x4_t (&ka)[2][NS], uint32_t vmask,
                                        const u32x4_t (&vb)[NB], float scale_log2, int lane) {
     float s[2][4], a[4];
+    bool rescale;
     scores(ka, vmask, scale_log2, s);
-    const u32x4_t pa = softmax(s, lane, a);
+    const u32x4_t pa = softmax(s, lane, a, rescale);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) pv(pa, vb[nb], a, nb);
+    for (int nb = 0; nb < NB; ++nb) pv(pa, vb[nb], a, rescale, nb);
   }
 
   // Row n's total probability mass (sum of the four lane groups' partials).
@@ -442,30 +456,39 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(int B, int Hq, int split
 
 // ------------------------------------------------------------------------------ prefill
 // Work item: request b, first packed query row row0 (row R = query token R / G, head R % G of
-// the kv head's group). A work group of 4 waves owns prefill_rows<D> rows (one or two 16-row
-// MFMA row tiles per wave) and streams the request's kv tokens in 32-token tiles: the four waves load each K
-// and V tile cooperatively straight into LDS (global_load_lds, chunk-swizzled, double-buffered),
+// the kv head's group). A work group of prefill_waves<D> waves owns prefill_rows<D> rows
+// (prefill_row_tiles<D> 16-row MFMA row tiles per wave) and streams the request's kv tokens in 32-token tiles: the four waves load each K
+// and V tile cooperatively (three tiles ahead through registers, then into LDS, chunk-swizzled,
+// double-buffered),
 // then every wave reads the K and V MFMA operands it needs into registers before the next
 // tile's loads are issued, and runs both row tiles against them.
 // Visibility: mode 0 every cached position, 1 causal (t <= kv_len - qo_len + i), 2 the custom
-// mask (bytes, per request a row-major [qo_len, kv_len] block at mask + mask_off[b]).
-// Query rows per work group: 2 MFMA row tiles per wave (1 for D = 256, whose accumulators
-// would not fit twice).
+// mask, bit-packed by attn_pack_mask_kernel: query token i of request b reads 32-bit word
+// w (kv positions 32w..32w+31) at packed + word_off[b] + i * ceil(kv_len / 32) + w.
+// Work-group shape: for D = 128, PIE_PREFILL_NW waves of 8 / PIE_PREFILL_NW 16-row MFMA row tiles
+// each; D = 64 uses 4 waves of two tiles (a wave's share of a K/V tile must fill one load
+// instruction), D = 256 4 waves of one tile (its accumulators would not fit twice).
+#ifndef PIE_PREFILL_NW
+#define PIE_PREFILL_NW 4
+#endif
 template <int D>
-constexpr int prefill_row_tiles() { return D == 256 ? 1 : 2; }
+constexpr int prefill_waves() { return D == 128 ? PIE_PREFILL_NW : 4; }
 template <int D>
-constexpr int prefill_rows() { return 64 * prefill_row_tiles<D>(); }
+constexpr int prefill_row_tiles() { return D == 256 ? 1 : D == 128 ? 8 / PIE_PREFILL_NW : 2; }
+template <int D>
+constexpr int prefill_rows() { return 16 * prefill_waves<D>() * prefill_row_tiles<D>(); }
 constexpr int kPlanHeader = 16;  // plan words before the items: [0] items, [1] batch, [2] rows per item
 
 template <int D>
-__global__ __launch_bounds__(256, D == 256 ? 1 : 2) void attn_prefill_kernel(
+__global__ __launch_bounds__(64 * prefill_waves<D>(), D == 256 ? 1 : 2) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv,
     const int32_t* __restrict__ qo_indptr, int G, float scale_log2, const int32_t* __restrict__ plan,
-    int mode, const uint8_t* __restrict__ mask, const int64_t* __restrict__ mask_off,
-    uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
+    int mode, const uint32_t* __restrict__ packed, const int64_t* __restrict__ word_off,
+    const int32_t* __restrict__ extent, uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
   using W = WaveAttn<D>;
   constexpr int NS = W::NS, NB = W::NB, CH = D / 8, RPI = 64 / CH;
   constexpr int RT = prefill_row_tiles<D>(), kPrefillRows = prefill_rows<D>();
+  constexpr int NW = prefill_waves<D>(), NT = 64 * NW;  // waves, threads
   constexpr int TILE = kTileTokens * D;  // elements of one K or V tile
   constexpr int kSmemLoop = 2 * 2 * TILE * 2;
   constexpr int kSmemOut = kPrefillRows * D * 2;
@@ -501,54 +524,96 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void attn_prefill_kernel(
       st[rt].qb[s] = valid ? ld16v(qp + 8 * (4 * s + g)) : z;
     }
   }
-  // kv positions any row of this work group can see
+  // kv positions any row of this work group can see (mode 2: the furthest set mask bit of its
+  // rows' query tokens, from attn_mask_extent_kernel)
   const int last_row = min(rows, row0 + kPrefillRows) - 1;
-  const int kv_end = mode == 1 ? min(kv_len, kv_len - qo_len + last_row / G + 1) : kv_len;
-  const uint8_t* mrow[RT];
+  int kv_end = mode == 1 ? min(kv_len, kv_len - qo_len + last_row / G + 1) : kv_len;
+  if (mode == 2) {
+    __shared__ int wg_extent;
+    if (threadIdx.x == 0) wg_extent = 0;
+    __syncthreads();
+    const int r = row0 + (int)threadIdx.x;
+    if ((int)threadIdx.x < kPrefillRows && r < rows) atomicMax(&wg_extent, extent[q0 + r / G]);
+    __syncthreads();
+    kv_end = min(kv_len, wg_extent);
+  }
+  // mode 2: this lane's rows' mask words; modes 0/1: the last kv position every row of the wave
+  // sees (tiles ending at or before it need no per-element visibility test)
+  const uint32_t* mword[RT];
+  const int nw = (kv_len + 31) / 32;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) mrow[rt] = mode == 2 ? mask + mask_off[b] + (int64_t)tok[rt] * kv_len : nullptr;
+  for (int rt = 0; rt < RT; ++rt) mword[rt] = mode == 2 ? packed + word_off[b] + (int64_t)tok[rt] * nw : nullptr;
+  int wave_lim = 0x7fffffff;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) wave_lim = min(wave_lim, lim[rt] < 0 ? 0x7fffffff : lim[rt]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) wave_lim = min(wave_lim, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, wave_lim));
+  wave_lim = uniform(wave_lim);
+  __shared__ int window_bad;
+  __shared__ uint32_t mwt[2][RT][NT];  // mode 2: mask words of the tiles in LDS, per lane
 
   uint16_t* kt = reinterpret_cast<uint16_t*>(smem);  // [2 buffers][K, V][32][D]
-  constexpr int NL = 8 / RPI;  // load instructions per wave for its 8 rows of a K or V tile
+  constexpr int WR = kTileTokens / NW;  // rows of each K / V tile one wave loads
+  constexpr int NL = WR / RPI;          // load instructions per wave for them
+  static_assert(NL >= 1 && WR % RPI == 0, "tile rows per wave");
   // A tile in flight in registers: this wave's rows 8w..8w+7 of K and V (chunk-swizzled as they
   // will sit in LDS).
-  struct Slot { u32x4_t k[NL], v[NL]; };
+  struct Slot { u32x4_t k[NL], v[NL]; uint32_t mw[RT]; };
   const int win = max(kTileTokens, (kPageWin - 2) * kv.page_size / kTileTokens * kTileTokens);
   for (int wt0 = 0; wt0 < kv_end; wt0 += win) {
     const int wt1 = min(kv_end, wt0 + win);
     const int lp0 = (int)kv.pdiv.div((uint32_t)wt0);
     const int npg = (int)kv.pdiv.div((uint32_t)(wt1 - 1)) - lp0 + 1;
     const int ntiles = (wt1 - wt0 + kTileTokens - 1) / kTileTokens;
+    if (threadIdx.x == 0) window_bad = 0;
     __syncthreads();  // the previous window's lookups and LDS tiles are done
-    for (int i = threadIdx.x; i < npg; i += 256) ptab[i] = kv.indices[page0 + lp0 + i];
+    for (int i = threadIdx.x; i < npg; i += NT) {
+      const int pg = kv.indices[page0 + lp0 + i];
+      ptab[i] = pg;
+      if ((unsigned)pg >= (unsigned)kv.num_pages) window_bad = 1;
+    }
     __syncthreads();
+    const bool all_pages_ok = window_bad == 0;
     auto gload = [&](Slot& sl, int tile) {
       const int t0 = wt0 + tile * kTileTokens;
 #pragma unroll
       for (int i = 0; i < NL; ++i) {
-        const int r = 8 * w + RPI * i + lane / CH;
+        const int r = WR * w + RPI * i + lane / CH;
         bool ok;
         const uint64_t off = kv_offset_lds(kv, ptab, lp0, min(t0 + r, wt1 - 1), kvh, ok);
         const int lc = (lane % CH) ^ chunk_swizzle<D>(r);
         sl.k[i] = ld16v(kv.k + off + 8 * lc);
         sl.v[i] = ld16v(kv.v + off + 8 * lc);
       }
+      if (mode == 2) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) sl.mw[rt] = mword[rt][t0 >> 5];
+      }
     };
     auto lwrite = [&](const Slot& sl, int tile) {
       uint16_t* kd = kt + (tile & 1) * 2 * TILE;
+      if (mode == 2) {  // each lane keeps its own rows' mask words with the tile (no sharing)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) mwt[tile & 1][rt][threadIdx.x] = sl.mw[rt];
+      }
 #pragma unroll
       for (int i = 0; i < NL; ++i) {
-        *reinterpret_cast<u32x4_t*>(kd + (8 * w + RPI * i) * D + 8 * lane) = sl.k[i];
-        *reinterpret_cast<u32x4_t*>(kd + TILE + (8 * w + RPI * i) * D + 8 * lane) = sl.v[i];
+        *reinterpret_cast<u32x4_t*>(kd + (WR * w + RPI * i) * D + 8 * lane) = sl.k[i];
+        *reinterpret_cast<u32x4_t*>(kd + TILE + (WR * w + RPI * i) * D + 8 * lane) = sl.v[i];
       }
     };
     auto compute = [&](int tile) {
       const int t0 = wt0 + tile * kTileTokens;
       const uint16_t* kd = kt + (tile & 1) * 2 * TILE;
-      // tokens of this tile on valid pages (bit r = token t0 + r)
-      bool pok = false;
-      if (lane < kTileTokens && t0 + lane < wt1) kv_offset_lds(kv, ptab, lp0, t0 + lane, kvh, pok);
-      const uint64_t tv = __builtin_amdgcn_ballot_w64(pok);
+      // tokens of this tile on valid pages (bit r = token t0 + r); tested only in windows that
+      // hold an out-of-range page id
+      uint64_t tv = 0xffffffffull;
+      if (!all_pages_ok) {
+        bool pok = false;
+        if (lane < kTileTokens && t0 + lane < wt1) kv_offset_lds(kv, ptab, lp0, t0 + lane, kvh, pok);
+        tv = __builtin_amdgcn_ballot_w64(pok);
+      }
+      const bool full = mode != 2 && all_pages_ok && t0 + kTileTokens - 1 <= wave_lim;
       u32x4_t ka[2][NS];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -560,21 +625,29 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void attn_prefill_kernel(
       }
       u32x4_t pa[RT];
       float a[RT][4];
+      bool rs[RT];
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        uint32_t vm = 0;
+        uint32_t vm = 0xFFu;
+        if (mode == 2) {
+          // bit 16u+4g+i of the row's word is token t0+16u+4g+i
+          const uint32_t mw = mwt[tile & 1][rt][threadIdx.x] & (uint32_t)tv;
+          vm = ((mw >> (4 * g)) & 15u) | (((mw >> (16 + 4 * g)) & 15u) << 4);
+          if (lim[rt] < 0) vm = 0;
+        } else if (!full) {
+          vm = 0;
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+          for (int u = 0; u < 2; ++u)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = 16 * u + 4 * g + i, t = t0 + r;
-            bool vis = t <= lim[rt] && ((tv >> r) & 1ull);
-            if (mode == 2 && vis) vis = mrow[rt][t] != 0;
-            vm |= (uint32_t)vis << (4 * u + i);
-          }
+            for (int i = 0; i < 4; ++i) {
+              const int r = 16 * u + 4 * g + i;
+              vm |= (uint32_t)(t0 + r <= lim[rt] && ((tv >> r) & 1ull)) << (4 * u + i);
+            }
+        }
+        if (__builtin_amdgcn_ballot_w64(vm != 0xFFu) == 0) vm = 0xFFu;  // keep the fast path visible
         float sc[2][4];
         st[rt].scores(ka, vm, scale_log2, sc);
-        pa[rt] = st[rt].softmax(sc, lane, a[rt]);
+        pa[rt] = st[rt].softmax(sc, lane, a[rt], rs[rt]);
       }
       // PV: the V operand of each 16-dim block comes straight from LDS (transpose reads)
       const int j = (lane >> 2) & 3, qq = lane & 3;
@@ -589,7 +662,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void attn_prefill_kernel(
         const uint2 hi = lds_read_tr16(b1 + 8 * (lc ^ z1));
         const u32x4_t vb = {lo.x, lo.y, hi.x, hi.y};
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) st[rt].pv(pa[rt], vb, a[rt], nb);
+        for (int rt = 0; rt < RT; ++rt) st[rt].pv(pa[rt], vb, a[rt], rs[rt], nb);
       }
     };
     // Two register slots alternate (no copies, which would force waits on loads in flight):
@@ -637,7 +710,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void attn_prefill_kernel(
       for (int nb = 0; nb < NB; ++nb) ot[row * D + 16 * nb + n] = to_bf1(st[rt].o[nb][i] * f);
     }
   __syncthreads();
-  for (int u = threadIdx.x; u < kPrefillRows * CH; u += 256) {
+  for (int u = threadIdx.x; u < kPrefillRows * CH; u += NT) {
     const int row = u / CH, c = u % CH;
     const int R = row0 + row;
     if (R >= rows) continue;
@@ -761,8 +834,10 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
                                               int64_t num_kv_heads, int64_t head_dim, int32_t mode,
                                               int32_t* plan,
                                               int64_t plan_capacity, int64_t* plan_words,
-                                              int64_t* num_items, int64_t* mask_bytes) {
-  PIE_REQUIRE(qo_indptr && kv_indptr && kv_last_page_len && plan && plan_words && num_items && mask_bytes,
+                                              int64_t* num_items, int64_t* mask_bytes,
+                                              int64_t* mask_words) {
+  PIE_REQUIRE(qo_indptr && kv_indptr && kv_last_page_len && plan && plan_words && num_items && mask_bytes &&
+                  mask_words,
               "prefill_plan: null argument");
   PIE_REQUIRE(batch >= 0 && batch < (1 << 24) && page_size > 0 && num_kv_heads > 0 &&
                   num_qo_heads % num_kv_heads == 0 && mode >= 0 && mode <= 2,
@@ -775,8 +850,8 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
   const int64_t kPrefillRows = head_dim == 256 ? prefill_rows<256>() : prefill_rows<128>();
   struct Item { int32_t b, row0; int64_t work; };
   std::vector<Item> items;
-  std::vector<int64_t> moff((size_t)batch, 0);
-  int64_t mtotal = 0;
+  std::vector<int64_t> moff((size_t)batch + 1, 0), woff((size_t)batch + 1, 0);
+  int64_t mtotal = 0, wtotal = 0;
   for (int64_t b = 0; b < batch; ++b) {
     const int64_t qo = (int64_t)qo_indptr[b + 1] - qo_indptr[b];
     const int64_t np = (int64_t)kv_indptr[b + 1] - kv_indptr[b];
@@ -785,7 +860,9 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
     PIE_REQUIRE(kv >= 0 && kv < (1ll << 31) && qo * G < (1ll << 31),
                 "prefill_plan: request %lld too long", (long long)b);
     moff[(size_t)b] = mtotal;
+    woff[(size_t)b] = wtotal;
     mtotal += qo * kv;
+    wtotal += qo * ((kv + 31) / 32);
     for (int64_t r0 = 0; r0 < qo * G; r0 += kPrefillRows) {
       const int64_t last = std::min(qo * G, r0 + kPrefillRows) - 1;
       const int64_t seen = mode == 1 ? std::max<int64_t>(0, std::min(kv, kv - qo + last / G + 1)) : kv;
@@ -795,31 +872,90 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
   std::stable_sort(items.begin(), items.end(), [](const Item& x, const Item& y) { return x.work > y.work; });
   int64_t words = kPlanHeader + 2 * (int64_t)items.size();
   words = (words + 1) / 2 * 2;  // int64 mask offsets start 8-byte aligned
-  const int64_t moff_word = words;
-  if (mode == 2) words += 2 * batch;
+  moff[(size_t)batch] = mtotal;
+  woff[(size_t)batch] = wtotal;
+  const int64_t moff_word = words, woff_word = words + 2 * (batch + 1);
+  if (mode == 2) words += 4 * (batch + 1);
   *plan_words = words;
   *num_items = (int64_t)items.size();
   *mask_bytes = mtotal;
+  *mask_words = wtotal;
   PIE_REQUIRE(words <= plan_capacity, "prefill_plan: needs %lld words, capacity %lld",
               (long long)words, (long long)plan_capacity);
   for (int i = 0; i < kPlanHeader; ++i) plan[i] = 0;
   plan[0] = (int32_t)items.size();
   plan[1] = (int32_t)batch;
   plan[2] = (int32_t)kPrefillRows;
-  plan[3] = (int32_t)moff_word;
+  plan[3] = (int32_t)moff_word;  // mode 2: int64 byte offsets of the mask blocks [batch + 1]
+  plan[4] = (int32_t)woff_word;  // mode 2: int64 offsets of the packed mask words [batch + 1]
   int32_t* p = plan + kPlanHeader;
   for (const Item& it : items) { *p++ = it.b; *p++ = it.row0; }
-  if (mode == 2) memcpy(plan + moff_word, moff.data(), sizeof(int64_t) * (size_t)batch);
+  if (mode == 2) {
+    memcpy(plan + moff_word, moff.data(), sizeof(int64_t) * (size_t)(batch + 1));
+    memcpy(plan + woff_word, woff.data(), sizeof(int64_t) * (size_t)(batch + 1));
+  }
   return PIE_HIP_OK;
 }
 
 template <int D>
 static void launch_prefill(hipStream_t st, dim3 grid, const uint16_t* q, int64_t q_ts, int64_t q_hs,
                            const PagedKV& kv, const int32_t* qo_indptr, int G, float sl2,
-                           const int32_t* plan, int mode, const uint8_t* mask, const int64_t* moff,
-                           uint16_t* out, int64_t o_ts, int64_t o_hs) {
-  hipLaunchKernelGGL(attn_prefill_kernel<D>, grid, dim3(256), 0, st, q, q_ts, q_hs, kv, qo_indptr, G, sl2,
-                     plan, mode, mask, moff, out, o_ts, o_hs);
+                           const int32_t* plan, int mode, const uint32_t* packed, const int64_t* woff,
+                           const int32_t* extent, uint16_t* out, int64_t o_ts, int64_t o_hs) {
+  hipLaunchKernelGGL(attn_prefill_kernel<D>, grid, dim3(64 * prefill_waves<D>()), 0, st, q, q_ts, q_hs, kv,
+                     qo_indptr, G, sl2, plan, mode, packed, woff, extent, out, o_ts, o_hs);
+}
+
+// Visible extent of every query token under the packed mask: 1 + the last kv position whose bit
+// is set (0 if none). One thread per query token, scanning its words from the end.
+__global__ __launch_bounds__(256) void attn_mask_extent_kernel(const uint32_t* __restrict__ packed,
+                                                               const int32_t* __restrict__ plan,
+                                                               const int32_t* __restrict__ qo_indptr,
+                                                               PagedKV kv, int B, int T,
+                                                               int32_t* __restrict__ extent) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= T) return;
+  const int64_t* woff = reinterpret_cast<const int64_t*>(plan + plan[4]);
+  int lo = 0, hi = B - 1;  // the request holding query token j
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (qo_indptr[mid] <= j) lo = mid; else hi = mid - 1;
+  }
+  const int b = lo, i = j - qo_indptr[b];
+  const int nw = (kv_length(kv, b) + 31) / 32;
+  const uint32_t* row = packed + woff[b] + (int64_t)i * nw;
+  int e = 0;
+  for (int w = nw - 1; w >= 0; --w)
+    if (row[w]) { e = 32 * w + 32 - __builtin_clz(row[w]); break; }
+  extent[j] = e;
+}
+
+// Bit-packs the custom mask: one thread per 32-bit word (query token i of request b, kv
+// positions 32w..32w+31; bit j = mask byte of position 32w+j, 0 past kv_len).
+__global__ __launch_bounds__(256) void attn_pack_mask_kernel(const uint8_t* __restrict__ mask,
+                                                             const int32_t* __restrict__ plan,
+                                                             const int32_t* __restrict__ qo_indptr,
+                                                             PagedKV kv, int B, int64_t total,
+                                                             uint32_t* __restrict__ packed) {
+  const int64_t gw = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gw >= total) return;
+  const int64_t* moff = reinterpret_cast<const int64_t*>(plan + plan[3]);
+  const int64_t* woff = reinterpret_cast<const int64_t*>(plan + plan[4]);
+  int lo = 0, hi = B - 1;  // the request whose word range holds gw
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (woff[mid] <= gw) lo = mid; else hi = mid - 1;
+  }
+  const int b = lo;
+  const int kv_len = kv_length(kv, b);
+  const int64_t nw = (kv_len + 31) / 32;
+  const int64_t local = gw - woff[b];
+  const int64_t i = local / nw, w = local - i * nw;
+  const uint8_t* src = mask + moff[b] + i * kv_len + 32 * w;
+  const int n = (int)min((int64_t)32, (int64_t)kv_len - 32 * w);
+  uint32_t bits = 0;
+  for (int j = 0; j < n; ++j) bits |= (uint32_t)(src[j] != 0) << j;
+  packed[gw] = bits;
 }
 
 extern "C" int pie_hip_attention_prefill(
@@ -827,8 +963,8 @@ extern "C" int pie_hip_attention_prefill(
     const pie_bf16* v_cache, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
     int64_t num_pages, const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
     const int32_t* kv_last_page_len, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
-    int64_t page_size, float sm_scale, int32_t mode, const uint8_t* custom_mask,
-    const int32_t* plan, int64_t num_items, int64_t mask_offsets_word, pie_bf16* out,
+    int64_t page_size, float sm_scale, int32_t mode, const uint32_t* packed_mask,
+    const int32_t* mask_extent, const int32_t* plan, int64_t num_items, int64_t mask_offsets_word, pie_bf16* out,
     int64_t o_tok_stride, int64_t o_head_stride, void* stream) {
   PagedKV kv;
   int rc = paged_kv_desc(&kv, k_cache, v_cache, page_stride, slot_stride, head_stride, num_pages,
@@ -841,9 +977,9 @@ extern "C" int pie_hip_attention_prefill(
   PIE_REQUIRE(num_kv_heads > 0 && num_kv_heads <= 65535 && num_qo_heads % num_kv_heads == 0,
               "attention_prefill: num_qo_heads %lld not a multiple of num_kv_heads %lld",
               (long long)num_qo_heads, (long long)num_kv_heads);
-  PIE_REQUIRE(mode >= 0 && mode <= 2 && (mode != 2 || (custom_mask && mask_offsets_word > 0 &&
+  PIE_REQUIRE(mode >= 0 && mode <= 2 && (mode != 2 || (packed_mask && mask_extent && mask_offsets_word > 0 &&
                                                        mask_offsets_word % 2 == 0)),
-              "attention_prefill: mode %d needs a custom mask and its plan offsets", mode);
+              "attention_prefill: mode %d needs the packed mask and its plan offsets", mode);
   PIE_REQUIRE(num_items >= 0 && num_items < (1ll << 31), "attention_prefill: bad item count");
   PIE_REQUIRE(plan[2] == (head_dim == 256 ? prefill_rows<256>() : prefill_rows<128>()),
               "attention_prefill: the plan was made for another head_dim");
@@ -853,16 +989,41 @@ extern "C" int pie_hip_attention_prefill(
   if (num_items == 0) return PIE_HIP_OK;
   const int G = (int)(num_qo_heads / num_kv_heads);
   const float sl2 = sm_scale * 1.4426950408889634f;
-  const int64_t* moff = mode == 2 ? reinterpret_cast<const int64_t*>(plan + mask_offsets_word) : nullptr;
+  const int64_t* woff = mode == 2 ? reinterpret_cast<const int64_t*>(plan + mask_offsets_word) : nullptr;
   const dim3 grid((unsigned)num_items, (unsigned)num_kv_heads);
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (head_dim) {
     case 64: launch_prefill<64>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
-                                mode, custom_mask, moff, out, o_tok_stride, o_head_stride); break;
+                                mode, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride); break;
     case 128: launch_prefill<128>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
-                                  mode, custom_mask, moff, out, o_tok_stride, o_head_stride); break;
+                                  mode, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride); break;
     default: launch_prefill<256>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
-                                 mode, custom_mask, moff, out, o_tok_stride, o_head_stride); break;
+                                 mode, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride); break;
   }
   return check_launch("attention_prefill");
+}
+
+extern "C" int pie_hip_attention_pack_mask(const uint8_t* custom_mask, const int32_t* plan,
+                                           const int32_t* qo_indptr, const int32_t* kv_indptr,
+                                           const int32_t* kv_last_page_len, int64_t batch,
+                                           int64_t page_size, int64_t mask_words, int64_t num_tokens,
+                                           uint32_t* packed_mask, int32_t* mask_extent, void* stream) {
+  PIE_REQUIRE(custom_mask && plan && qo_indptr && kv_indptr && kv_last_page_len && packed_mask && mask_extent,
+              "attention_pack_mask: null argument");
+  PIE_REQUIRE(num_tokens >= 0 && num_tokens < (1ll << 31), "attention_pack_mask: bad token count");
+  PIE_REQUIRE(batch > 0 && batch < (1 << 24) && page_size > 0 && mask_words >= 0,
+              "attention_pack_mask: bad batch %lld / page_size %lld / words %lld", (long long)batch,
+              (long long)page_size, (long long)mask_words);
+  PagedKV kv{};
+  kv.indptr = kv_indptr;
+  kv.last_len = kv_last_page_len;
+  kv.page_size = (int32_t)page_size;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (mask_words > 0)
+    hipLaunchKernelGGL(attn_pack_mask_kernel, dim3((unsigned)((mask_words + 255) / 256)), dim3(256), 0, st,
+                       custom_mask, plan, qo_indptr, kv, (int)batch, mask_words, packed_mask);
+  if (num_tokens > 0)
+    hipLaunchKernelGGL(attn_mask_extent_kernel, dim3((unsigned)((num_tokens + 255) / 256)), dim3(256), 0, st,
+                       packed_mask, plan, qo_indptr, kv, (int)batch, (int)num_tokens, mask_extent);
+  return check_launch("attention_pack_mask");
 }

@@ -406,7 +406,7 @@ static void case_attn_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int6
 // Paged prefill attention: requests with ctx in [0, cmax] cached tokens and qo in [0, qmax] new
 // query tokens; mode 0 full, 1 causal, 2 a random custom mask.
 static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int cmax, int qmax,
-                              int mode) {
+                              int mode, bool causal_mask = false) {
   printf("attn_prefill B=%lld Hq=%lld Hkv=%lld D=%lld P=%lld ctx<=%d qo<=%d mode=%d\n", (long long)B,
          (long long)Hq, (long long)Hkv, (long long)D, (long long)P, cmax, qmax, mode);
   std::vector<int32_t> qo(B + 1, 0), indptr(B + 1, 0), last(B), kvl(B);
@@ -439,15 +439,29 @@ static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
   for (int64_t b = 1; b < B; ++b) moff[b] = moff[b - 1] + (int64_t)(qo[b] - qo[b - 1]) * kvl[b - 1];
   std::bernoulli_distribution bit(0.7);
   for (int64_t i = 0; i < mbytes; ++i) mask[i] = bit(rng) ? 1 : 0;
-  const int64_t cap = 16 + 2 * (T * Hq / 32 + 2 * B + 2) + 2 * B + 2;
+  if (causal_mask)  // random bits inside the causal window only: extents shorter than kv_len
+    for (int64_t b = 0; b < B; ++b) {
+      const int64_t qn = qo[b + 1] - qo[b];
+      for (int64_t i = 0; i < qn; ++i)
+        for (int64_t t = 0; t < kvl[b]; ++t)
+          if (t > kvl[b] - qn + i) mask[moff[b] + i * kvl[b] + t] = 0;
+    }
+  const int64_t cap = 16 + 2 * (T * Hq / 32 + 2 * B + 2) + 4 * B + 8;
   Buf<int32_t> plan(cap);
-  int64_t words = 0, items = 0, mb = 0;
-  rc_ok(pie_hip_attention_prefill_plan(qi.p, ip.p, ll.p, B, P, Hq, Hkv, D, mode, plan.p, cap, &words, &items, &mb),
+  int64_t words = 0, items = 0, mb = 0, mw = 0;
+  rc_ok(pie_hip_attention_prefill_plan(qi.p, ip.p, ll.p, B, P, Hq, Hkv, D, mode, plan.p, cap, &words, &items, &mb,
+                                       &mw),
         "prefill_plan");
   if (mode == 2 && mb != mbytes) { printf("  mask bytes %lld != %lld\n", (long long)mb, (long long)mbytes); ++failures; }
+  Buf<uint32_t> packed(std::max<int64_t>(mw, 1));
+  Buf<int32_t> extent(std::max<int64_t>(T, 1));
+  if (mode == 2)
+    rc_ok(pie_hip_attention_pack_mask(mask.p, plan.p, qi.p, ip.p, ll.p, B, P, mw, T, packed.p, extent.p, nullptr),
+          "pack_mask");
   rc_ok(pie_hip_attention_prefill(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, pages,
                                   qi.p, ip.p, idx.p, ll.p, Hq, Hkv, D, P, 1.f / sqrtf((float)D), mode,
-                                  mode == 2 ? mask.p : nullptr, plan.p, items, plan[3], out.p, Hq * D, D,
+                                  mode == 2 ? packed.p : nullptr, mode == 2 ? extent.p : nullptr, plan.p, items,
+                                  plan[4], out.p, Hq * D, D,
                                   nullptr),
         "attention_prefill");
   oracle_attention(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, qi.p, ip.p, idx.p,
@@ -621,6 +635,7 @@ int main(int argc, char** argv) {
     case_attn_prefill(2, 4, 1, 64, 1, 600, 10, 1);    // page size 1: several page-table windows
     case_attn_prefill(2, 8, 2, 128, 16, 50, 100, 1);  // up to 400 rows: several items per request
     case_attn_prefill(2, 8, 2, 128, 16, 50, 100, 2);
+    case_attn_prefill(3, 8, 2, 128, 16, 20, 120, 2, true);  // masks within the causal window
   }
   if (all || c == "qkfused") {
     case_qk_fused(5, 4, 2, 128);  // fused kernel
