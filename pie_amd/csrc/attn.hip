@@ -95,6 +95,14 @@ __device__ __forceinline__ int chunk_swizzle(int r) {
   return D == 64 ? (r >> 1) & 7 : r & 15;
 }
 
+// Swizzle of V rows, read by ds_read_b64_tr_b16: a transpose read takes two 16-byte chunks
+// (one pair) from each of 16 rows, and every 8 consecutive rows must hit different 32-byte bank
+// groups, so the pair index is XORed with r mod 8 (D = 64 keeps the row-pair scheme above).
+template <int D>
+__device__ __forceinline__ int v_swizzle(int r) {
+  return D == 64 ? chunk_swizzle<64>(r) : (r & 7) << 1;
+}
+
 // Wait until this wave's LDS reads have returned (a transpose read must finish before a load
 // into the same LDS tile is issued).
 __device__ __forceinline__ void wait_lgkmcnt0() {
@@ -134,7 +142,7 @@ struct WaveAttn {
     const int r0 = 4 * g + j, r1 = r0 + 16;
     const uint16_t* b0 = vt + r0 * D + 4 * (q & 1);
     const uint16_t* b1 = vt + r1 * D + 4 * (q & 1);
-    const int z0 = chunk_swizzle<D>(r0), z1 = chunk_swizzle<D>(r1);
+    const int z0 = v_swizzle<D>(r0), z1 = v_swizzle<D>(r1);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const int lc = 2 * nb + (q >> 1);
@@ -265,7 +273,7 @@ struct KVTile {
       const int r = RPI * i + lane / CH;
       bool ok;
       const uint64_t off = kv_offset_lds(kv, ptab, lp0, min(t0 + r, end - 1), kvh, ok);
-      const int lc = (lane % CH) ^ chunk_swizzle<D>(r);
+      const int lc = (lane % CH) ^ v_swizzle<D>(r);
       __builtin_amdgcn_global_load_lds(kv.v + off + 8 * lc,
                                        (__attribute__((address_space(3))) void*)(vt + RPI * i * D),
                                        16, 0, 0);
@@ -581,9 +589,8 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), D == 256 ? 1 : 2) void att
         const int r = WR * w + RPI * i + lane / CH;
         bool ok;
         const uint64_t off = kv_offset_lds(kv, ptab, lp0, min(t0 + r, wt1 - 1), kvh, ok);
-        const int lc = (lane % CH) ^ chunk_swizzle<D>(r);
-        sl.k[i] = ld16v(kv.k + off + 8 * lc);
-        sl.v[i] = ld16v(kv.v + off + 8 * lc);
+        sl.k[i] = ld16v(kv.k + off + 8 * ((lane % CH) ^ chunk_swizzle<D>(r)));
+        sl.v[i] = ld16v(kv.v + off + 8 * ((lane % CH) ^ v_swizzle<D>(r)));
       }
       if (mode == 2) {
 #pragma unroll
@@ -654,7 +661,7 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), D == 256 ? 1 : 2) void att
       const int r0 = 4 * g + j, r1 = r0 + 16;
       const uint16_t* b0 = kd + TILE + r0 * D + 4 * (qq & 1);
       const uint16_t* b1 = kd + TILE + r1 * D + 4 * (qq & 1);
-      const int z0 = chunk_swizzle<D>(r0), z1 = chunk_swizzle<D>(r1);
+      const int z0 = v_swizzle<D>(r0), z1 = v_swizzle<D>(r1);
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const int lc = 2 * nb + (qq >> 1);
