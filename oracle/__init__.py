@@ -81,7 +81,7 @@ def _load():
         "oracle_rope_cs": (None, [_u16p, i64, i64, _u16p, i64, i64, _i32p, i64, i64, i64, i64,
                                   C.c_int, _f32p, i64, i64]),
         "oracle_attention": (None, [_u16p, i64, i64, C.c_void_p, C.c_void_p, i64, i64, i64,
-                                    _i32p, _i32p, _i32p, _i32p, C.c_void_p, C.c_void_p, C.c_int, i64, i64,
+                                    _i32p, _i32p, _i32p, _i32p, C.c_void_p, C.c_void_p, C.c_int, i64, i64, i64,
                                     i64, i64, i64, C.c_double, _u16p, i64, i64, C.c_void_p]),
         "oracle_scaled_softmax": (None, [_f32p, i64, i64, _f32p, C.c_double, _f64p]),
         "oracle_sample": (None, [_f32p, i64, i64, i64, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -294,12 +294,13 @@ def batch_indices_positions(append_indptr, seq_lens_, nnz: int, fill: int = -1):
 
 def attention(q: np.ndarray, cache: np.ndarray, qo_indptr, kv_indptr, kv_indices, last_page_len,
               custom_mask=None, sm_scale: float | None = None, layout: str = "NHD",
-              return_lse: bool = False, causal: bool = True):
+              return_lse: bool = False, causal: bool = True, window_left: int = -1):
     """Paged attention over cache [pages, 2, P, Hkv, D] (NHD) or [pages, 2, Hkv, P, D] (HND).
     q [T, Hq, D] bf16 bits -> out [T, Hq, D] bf16 bits (and lse [T, Hq] float64, natural log).
     custom_mask: flat bool/uint8, per request a row-major [qo_len, kv_len] block, concatenated
     in request order; None means the causal window t <= kv_len - qo_len + i (causal=True) or
-    every cached position (causal=False)."""
+    every cached position (causal=False); window_left >= 0 also hides positions before
+    kv_len - qo_len + i - window_left (flashinfer's sliding window)."""
     q = np.ascontiguousarray(q, dtype=np.uint16)
     assert cache.flags.c_contiguous and cache.dtype == np.uint16
     T, Hq, D = q.shape
@@ -331,7 +332,8 @@ def attention(q: np.ndarray, cache: np.ndarray, qo_indptr, kv_indptr, kv_indices
         q, Hq * D, D, base, base + P * Hkv * D * 2, ps, ss, hs, qo_indptr, kv_indptr,
         np.ascontiguousarray(kv_indices, np.int32), last,
         None if mask_arr is None else mask_arr.ctypes.data,
-        None if off is None else off.ctypes.data, 1 if causal else 0, B, Hq, Hkv, D, P, scale, out, Hq * D, D,
+        None if off is None else off.ctypes.data, 1 if causal else 0, window_left, B, Hq, Hkv, D, P,
+        scale, out, Hq * D, D,
         lse.ctypes.data)
     return (out, lse) if return_lse else out
 

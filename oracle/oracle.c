@@ -319,6 +319,7 @@ void oracle_batch_indices_positions(const int32_t* indptr, const int32_t* seq_le
  *                 the layout decode_brle_batch writes, batching.py:335-386)
  *   causal:       t <= kv_len - qo_len + i                  (metal_attention...:176, 243)
  *   neither:      every t < kv_len (flashinfer's prefill default, causal=False)
+ * and, with window_left >= 0 (flashinfer's sliding window), also t >= kv_len - qo_len + i - window_left.
  * Head h reads kv head h / (Hq/Hkv). Scores are q.k * sm_scale in float64, softmax in float64,
  * output rounded once to bf16. A row with no allowed position gives 0 and lse = -inf.
  * Token t of request b lives in page kv_indices[kv_indptr[b] + t/P], slot t%P; k and v are
@@ -328,7 +329,7 @@ void oracle_attention(const uint16_t* q, int64_t q_ts, int64_t q_hs, const uint1
                       const uint16_t* vc, int64_t page_stride, int64_t slot_stride,
                       int64_t head_stride, const int32_t* qo_indptr, const int32_t* kv_indptr,
                       const int32_t* kv_indices, const int32_t* last_len, const uint8_t* mask,
-                      const int64_t* mask_off, int causal, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                      const int64_t* mask_off, int causal, int64_t window_left, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
                       int64_t P, double sm_scale, uint16_t* out, int64_t o_ts, int64_t o_hs,
                       double* lse) {
   const int64_t G = Hq / Hkv;
@@ -345,6 +346,7 @@ void oracle_attention(const uint16_t* q, int64_t q_ts, int64_t q_hs, const uint1
         double mx = -INFINITY;
         for (int64_t t = 0; t < kv_len; ++t) {
           int ok = mask ? mask[mask_off[b] + i * kv_len + t] != 0 : (!causal || t <= kv_len - qo_len + i);
+          if (window_left >= 0 && t < kv_len - qo_len + i - window_left) ok = 0;
           if (!ok) { s[t] = -INFINITY; continue; }
           const int64_t page = kv_indices[kv_indptr[b] + t / P];
           const uint16_t* kv = kc + page * page_stride + (t % P) * slot_stride + kh * head_stride;

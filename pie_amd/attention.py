@@ -12,8 +12,9 @@ The API is flashinfer 0.6.1's, restated in pie/src/flashinfer_metal/ops.py:163-2
 ``plan`` runs on the host and allocates nothing on the device; ``run`` launches kernels on the
 current stream and allocates only its output (unless ``out=`` is given), so it can be captured.
 Split requests keep their partial results in the caller's workspace buffer, as flashinfer does.
-Unsupported options (positional encodings inside attention, sliding windows, soft caps, lse
-output) raise instead of being ignored.
+``window_left`` (flashinfer's sliding window, which OLMo-3 plans per layer) is supported; the
+options Pie's models do not use (positional encodings inside attention, logit soft caps, lse
+output, fp8 scales) raise instead of being ignored.
 """
 from __future__ import annotations
 
@@ -41,13 +42,10 @@ def _num_cus(device: torch.device) -> int:
     return _CUS[idx]
 
 
-def _unsupported(name: str, pos_encoding_mode="NONE", window_left=-1, logits_soft_cap=None,
-                 rope_scale=None, rope_theta=None):
+def _unsupported(name: str, pos_encoding_mode="NONE", logits_soft_cap=None):
     if pos_encoding_mode not in ("NONE", None):
         raise NotImplementedError(f"{name}: pos_encoding_mode={pos_encoding_mode!r} (RoPE is "
                                   "applied before the append, as Pie does)")
-    if window_left not in (-1, None):
-        raise NotImplementedError(f"{name}: sliding windows (window_left={window_left})")
     if logits_soft_cap not in (None, 0, 0.0):
         raise NotImplementedError(f"{name}: logits_soft_cap={logits_soft_cap}")
 
@@ -85,7 +83,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
              rope_scale: Optional[float] = None, rope_theta: Optional[float] = None,
              non_blocking: bool = True, **_ignored) -> None:
         name = "BatchDecodeWithPagedKVCacheWrapper.plan"
-        _unsupported(name, pos_encoding_mode, window_left, logits_soft_cap)
+        _unsupported(name, pos_encoding_mode, logits_soft_cap)
+        window_left = -1 if window_left is None or window_left < 0 else int(window_left)
         if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:
             raise ValueError(f"{name}: num_qo_heads {num_qo_heads} is not a multiple of "
                              f"num_kv_heads {num_kv_heads}")
@@ -121,7 +120,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
                                               for t in (indptr, indices, last_page_len))
         self._plan = dict(indptr=indptr, indices=indices, last_page_len=last_page_len,
                           batch=batch, Hq=num_qo_heads, Hkv=num_kv_heads, D=head_dim,
-                          P=page_size, splits=s,
+                          P=page_size, splits=s, window_left=window_left,
                           sm_scale=(1.0 / math.sqrt(head_dim)) if sm_scale is None else sm_scale)
 
     begin_forward = plan
@@ -158,7 +157,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
         _lib.call("pie_hip_attention_decode", q.data_ptr(), q.stride(0), q.stride(1), kp, vp, ps,
                   ss, hs, npages, p["indptr"].data_ptr(), p["indices"].data_ptr(),
                   p["last_page_len"].data_ptr(), B, Hq, Hkv, D, P, float(p["sm_scale"]),
-                  p["splits"], ws.data_ptr(), ws.numel() * ws.element_size(), out.data_ptr(),
+                  p["window_left"], p["splits"], ws.data_ptr(), ws.numel() * ws.element_size(),
+                  out.data_ptr(),
                   out.stride(0), out.stride(1), _stream(q))
         return out
 
@@ -196,7 +196,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
              rope_theta: Optional[float] = None, q_data_type=torch.float16, kv_data_type=None,
              non_blocking: bool = True, **_ignored) -> None:
         name = "BatchPrefillWithPagedKVCacheWrapper.plan"
-        _unsupported(name, pos_encoding_mode, window_left, logits_soft_cap)
+        _unsupported(name, pos_encoding_mode, logits_soft_cap)
+        window_left = -1 if window_left is None or window_left < 0 else int(window_left)
         if head_dim_vo not in (None, head_dim_qk):
             raise NotImplementedError(f"{name}: head_dim_vo {head_dim_vo} != head_dim_qk")
         if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:
@@ -258,6 +259,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self._plan = dict(qo_indptr=tables[0], indptr=tables[1], indices=tables[2],
                           last_page_len=tables[3], batch=batch, T=T, Hq=num_qo_heads,
                           Hkv=num_kv_heads, D=head_dim_qk, P=page_size, mode=mode, packed=packed, extent=extent,
+                          window_left=window_left,
                           plan=plan_d, items=items.value, woff_word=int(plan[4]),
                           sm_scale=(1.0 / math.sqrt(head_dim_qk)) if sm_scale is None else sm_scale)
 
@@ -297,7 +299,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
         _lib.call("pie_hip_attention_prefill", q.data_ptr(), q.stride(0), q.stride(1), kp, vp, ps,
                   ss, hs, npages, p["qo_indptr"].data_ptr(), p["indptr"].data_ptr(),
                   p["indices"].data_ptr(), p["last_page_len"].data_ptr(), Hq, Hkv, D, P,
-                  float(p["sm_scale"]), p["mode"], packed.data_ptr() if packed is not None else None,
+                  float(p["sm_scale"]), p["mode"], p["window_left"],
+                  packed.data_ptr() if packed is not None else None,
                   p["extent"].data_ptr() if p["extent"] is not None else None,
                   p["plan"].data_ptr(), p["items"], p["woff_word"], out.data_ptr(), out.stride(0),
                   out.stride(1), _stream(q))

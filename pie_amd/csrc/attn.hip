@@ -309,8 +309,8 @@ __device__ __forceinline__ void split_range(int kv_len, int splits, int j, int& 
 template <int D>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv, int G, int Hq,
-    float scale_log2, int splits, uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs,
-    float* __restrict__ part_o, float* __restrict__ part_lse) {
+    float scale_log2, int splits, int window_left, uint16_t* __restrict__ out, int64_t o_ts,
+    int64_t o_hs, float* __restrict__ part_o, float* __restrict__ part_lse) {
   using W = WaveAttn<D>;
   constexpr int kVtile = kTileTokens * D;  // elements of one wave's V tile
   constexpr int kSmem = (4 * kVtile * 2 > 4 * 16 * (D + 2) * 4) ? 4 * kVtile * 2 : 4 * 16 * (D + 2) * 4;
@@ -322,8 +322,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int kv_len = kv_length(kv, b);
+  // sliding window: the query (position kv_len - 1) sees positions >= kv_len - 1 - window_left
+  const int ws = window_left >= 0 ? max(0, kv_len - 1 - window_left) : 0;
   int kv0, kv1;
-  split_range(kv_len, splits, slot - b * splits, kv0, kv1);
+  split_range(kv_len - ws, splits, slot - b * splits, kv0, kv1);
+  kv0 += ws;
+  kv1 += ws;
   const int page0 = kv.indptr[b];
 
   W st;
@@ -479,20 +483,26 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(int B, int Hq, int split
 #ifndef PIE_PREFILL_NW
 #define PIE_PREFILL_NW 4
 #endif
+#ifndef PIE_PREFILL_RT
+#define PIE_PREFILL_RT (8 / PIE_PREFILL_NW)
+#endif
 template <int D>
 constexpr int prefill_waves() { return D == 128 ? PIE_PREFILL_NW : 4; }
 template <int D>
-constexpr int prefill_row_tiles() { return D == 256 ? 1 : D == 128 ? 8 / PIE_PREFILL_NW : 2; }
+constexpr int prefill_row_tiles() { return D == 256 ? 1 : D == 128 ? PIE_PREFILL_RT : 2; }
+template <int D>
+constexpr int prefill_min_waves() { return (D == 256 || prefill_row_tiles<D>() > 2) ? 1 : 2; }
 template <int D>
 constexpr int prefill_rows() { return 16 * prefill_waves<D>() * prefill_row_tiles<D>(); }
 constexpr int kPlanHeader = 16;  // plan words before the items: [0] items, [1] batch, [2] rows per item
 
 template <int D>
-__global__ __launch_bounds__(64 * prefill_waves<D>(), D == 256 ? 1 : 2) void attn_prefill_kernel(
+__global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv,
     const int32_t* __restrict__ qo_indptr, int G, float scale_log2, const int32_t* __restrict__ plan,
-    int mode, const uint32_t* __restrict__ packed, const int64_t* __restrict__ word_off,
-    const int32_t* __restrict__ extent, uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
+    int mode, int window_left, const uint32_t* __restrict__ packed,
+    const int64_t* __restrict__ word_off, const int32_t* __restrict__ extent,
+    uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
   using W = WaveAttn<D>;
   constexpr int NS = W::NS, NB = W::NB, CH = D / 8, RPI = 64 / CH;
   constexpr int RT = prefill_row_tiles<D>(), kPrefillRows = prefill_rows<D>();
@@ -516,7 +526,7 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), D == 256 ? 1 : 2) void att
 
   // this lane's query rows (row n of each of the wave's row tiles)
   W st[RT];
-  int lim[RT], tok[RT];
+  int lim[RT], tok[RT], lo[RT];  // visible positions of the row: lo..lim (and the mask)
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     st[rt].init();
@@ -525,6 +535,7 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), D == 256 ? 1 : 2) void att
     const int i = valid ? R / G : 0, hg = valid ? R - i * G : 0;
     tok[rt] = i;
     lim[rt] = !valid ? -1 : mode == 1 ? min(kv_len - qo_len + i, kv_len - 1) : kv_len - 1;
+    lo[rt] = window_left >= 0 ? kv_len - qo_len + i - window_left : 0;
     const uint16_t* qp = q + (int64_t)(q0 + i) * q_ts + (int64_t)(kvh * G + hg) * q_hs;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
@@ -544,6 +555,17 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), D == 256 ? 1 : 2) void att
     if ((int)threadIdx.x < kPrefillRows && r < rows) atomicMax(&wg_extent, extent[q0 + r / G]);
     __syncthreads();
     kv_end = min(kv_len, wg_extent);
+  }
+  // sliding window: no row of the work group sees positions before its first row's window
+  // (tiles start 32-aligned so mask words line up)
+  const int kv_begin = window_left >= 0 ? max(0, kv_len - qo_len + row0 / G - window_left) & ~31 : 0;
+  int wave_lo = 0;  // the largest window start of the wave's rows (uniform)
+  if (window_left >= 0) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) wave_lo = max(wave_lo, lim[rt] < 0 ? 0 : lo[rt]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) wave_lo = max(wave_lo, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, wave_lo));
+    wave_lo = uniform(wave_lo);
   }
   // mode 2: this lane's rows' mask words; modes 0/1: the last kv position every row of the wave
   // sees (tiles ending at or before it need no per-element visibility test)
@@ -568,7 +590,7 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), D == 256 ? 1 : 2) void att
   // will sit in LDS).
   struct Slot { u32x4_t k[NL], v[NL]; uint32_t mw[RT]; };
   const int win = max(kTileTokens, (kPageWin - 2) * kv.page_size / kTileTokens * kTileTokens);
-  for (int wt0 = 0; wt0 < kv_end; wt0 += win) {
+  for (int wt0 = kv_begin; wt0 < kv_end; wt0 += win) {
     const int wt1 = min(kv_end, wt0 + win);
     const int lp0 = (int)kv.pdiv.div((uint32_t)wt0);
     const int npg = (int)kv.pdiv.div((uint32_t)(wt1 - 1)) - lp0 + 1;
@@ -620,7 +642,7 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), D == 256 ? 1 : 2) void att
         if (lane < kTileTokens && t0 + lane < wt1) kv_offset_lds(kv, ptab, lp0, t0 + lane, kvh, pok);
         tv = __builtin_amdgcn_ballot_w64(pok);
       }
-      const bool full = mode != 2 && all_pages_ok && t0 + kTileTokens - 1 <= wave_lim;
+      const bool full = mode != 2 && all_pages_ok && t0 + kTileTokens - 1 <= wave_lim && t0 >= wave_lo;
       u32x4_t ka[2][NS];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -651,10 +673,23 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), D == 256 ? 1 : 2) void att
               vm |= (uint32_t)(t0 + r <= lim[rt] && ((tv >> r) & 1ull)) << (4 * u + i);
             }
         }
+        if (t0 < wave_lo) {  // the tile crosses some row's window start
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (t0 + 16 * u + 4 * g + i < lo[rt]) vm &= ~(1u << (4 * u + i));
+        }
         if (__builtin_amdgcn_ballot_w64(vm != 0xFFu) == 0) vm = 0xFFu;  // keep the fast path visible
         float sc[2][4];
         st[rt].scores(ka, vm, scale_log2, sc);
+#ifdef PIE_DIAG_NO_SOFTMAX
+        pa[rt] = u32x4_t{pack_bf2(sc[0][0], sc[0][1]), pack_bf2(sc[0][2], sc[0][3]),
+                         pack_bf2(sc[1][0], sc[1][1]), pack_bf2(sc[1][2], sc[1][3])};
+        rs[rt] = false;
+#else
         pa[rt] = st[rt].softmax(sc, lane, a[rt], rs[rt]);
+#endif
       }
       // PV: the V operand of each 16-dim block comes straight from LDS (transpose reads)
       const int j = (lane >> 2) & 3, qq = lane & 3;
@@ -775,9 +810,10 @@ static int paged_kv_desc(PagedKV* kv, const uint16_t* k_cache, const uint16_t* v
 template <int D>
 static void launch_decode(hipStream_t st, const uint16_t* q, int64_t q_ts, int64_t q_hs,
                           const PagedKV& kv, int G, int Hq, int Hkv, float sl2, int B, int splits,
-                          uint16_t* out, int64_t o_ts, int64_t o_hs, float* po, float* pl) {
+                          int window_left, uint16_t* out, int64_t o_ts, int64_t o_hs, float* po,
+                          float* pl) {
   hipLaunchKernelGGL(attn_decode_kernel<D>, dim3(B * splits, Hkv), dim3(256), 0, st, q, q_ts, q_hs, kv,
-                     G, Hq, sl2, splits, out, o_ts, o_hs, po, pl);
+                     G, Hq, sl2, splits, window_left, out, o_ts, o_hs, po, pl);
   if (splits > 1)
     hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(B, (Hq + 64 / (D / 8) - 1) / (64 / (D / 8))), dim3(64), 0,
                        st, B, Hq, splits, po, pl, out, o_ts, o_hs);
@@ -788,9 +824,9 @@ extern "C" int pie_hip_attention_decode(
     const pie_bf16* v_cache, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
     int64_t num_pages, const int32_t* kv_indptr, const int32_t* kv_indices,
     const int32_t* kv_last_page_len, int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
-    int64_t head_dim, int64_t page_size, float sm_scale, int64_t splits, void* workspace,
-    int64_t workspace_bytes, pie_bf16* out, int64_t o_tok_stride, int64_t o_head_stride,
-    void* stream) {
+    int64_t head_dim, int64_t page_size, float sm_scale, int64_t window_left, int64_t splits,
+    void* workspace, int64_t workspace_bytes, pie_bf16* out, int64_t o_tok_stride,
+    int64_t o_head_stride, void* stream) {
   PagedKV kv;
   int rc = paged_kv_desc(&kv, k_cache, v_cache, page_stride, slot_stride, head_stride, num_pages,
                          kv_indptr, kv_indices, kv_last_page_len, page_size, head_dim,
@@ -820,12 +856,13 @@ extern "C" int pie_hip_attention_decode(
   const float sl2 = sm_scale * 1.4426950408889634f;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int B = (int)batch, S = (int)splits, Hq = (int)num_qo_heads, Hkv = (int)num_kv_heads;
+  const int W = window_left < 0 ? -1 : (int)std::min<int64_t>(window_left, 1 << 30);
   switch (head_dim) {
-    case 64: launch_decode<64>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, out,
+    case 64: launch_decode<64>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, W, out,
                                o_tok_stride, o_head_stride, po, pl); break;
-    case 128: launch_decode<128>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, out,
+    case 128: launch_decode<128>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, W, out,
                                  o_tok_stride, o_head_stride, po, pl); break;
-    default: launch_decode<256>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, out,
+    default: launch_decode<256>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, W, out,
                                 o_tok_stride, o_head_stride, po, pl); break;
   }
   return check_launch("attention_decode");
@@ -907,10 +944,11 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
 template <int D>
 static void launch_prefill(hipStream_t st, dim3 grid, const uint16_t* q, int64_t q_ts, int64_t q_hs,
                            const PagedKV& kv, const int32_t* qo_indptr, int G, float sl2,
-                           const int32_t* plan, int mode, const uint32_t* packed, const int64_t* woff,
-                           const int32_t* extent, uint16_t* out, int64_t o_ts, int64_t o_hs) {
+                           const int32_t* plan, int mode, int window_left, const uint32_t* packed,
+                           const int64_t* woff, const int32_t* extent, uint16_t* out, int64_t o_ts,
+                           int64_t o_hs) {
   hipLaunchKernelGGL(attn_prefill_kernel<D>, grid, dim3(64 * prefill_waves<D>()), 0, st, q, q_ts, q_hs, kv,
-                     qo_indptr, G, sl2, plan, mode, packed, woff, extent, out, o_ts, o_hs);
+                     qo_indptr, G, sl2, plan, mode, window_left, packed, woff, extent, out, o_ts, o_hs);
 }
 
 // Visible extent of every query token under the packed mask: 1 + the last kv position whose bit
@@ -970,8 +1008,9 @@ extern "C" int pie_hip_attention_prefill(
     const pie_bf16* v_cache, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
     int64_t num_pages, const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
     const int32_t* kv_last_page_len, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
-    int64_t page_size, float sm_scale, int32_t mode, const uint32_t* packed_mask,
-    const int32_t* mask_extent, const int32_t* plan, int64_t num_items, int64_t mask_offsets_word, pie_bf16* out,
+    int64_t page_size, float sm_scale, int32_t mode, int64_t window_left,
+    const uint32_t* packed_mask, const int32_t* mask_extent, const int32_t* plan, int64_t num_items,
+    int64_t mask_offsets_word, pie_bf16* out,
     int64_t o_tok_stride, int64_t o_head_stride, void* stream) {
   PagedKV kv;
   int rc = paged_kv_desc(&kv, k_cache, v_cache, page_stride, slot_stride, head_stride, num_pages,
@@ -997,15 +1036,16 @@ extern "C" int pie_hip_attention_prefill(
   const int G = (int)(num_qo_heads / num_kv_heads);
   const float sl2 = sm_scale * 1.4426950408889634f;
   const int64_t* woff = mode == 2 ? reinterpret_cast<const int64_t*>(plan + mask_offsets_word) : nullptr;
+  const int Wl = window_left < 0 ? -1 : (int)std::min<int64_t>(window_left, 1 << 30);
   const dim3 grid((unsigned)num_items, (unsigned)num_kv_heads);
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (head_dim) {
     case 64: launch_prefill<64>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
-                                mode, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride); break;
+                                mode, Wl, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride); break;
     case 128: launch_prefill<128>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
-                                  mode, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride); break;
+                                  mode, Wl, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride); break;
     default: launch_prefill<256>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
-                                 mode, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride); break;
+                                 mode, Wl, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride); break;
   }
   return check_launch("attention_prefill");
 }

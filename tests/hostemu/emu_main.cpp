@@ -42,7 +42,8 @@ void oracle_rope_cs(uint16_t*, int64_t, int64_t, uint16_t*, int64_t, int64_t, co
                     int64_t, int64_t, int64_t, int, const float*, int64_t, int64_t);
 void oracle_attention(const uint16_t*, int64_t, int64_t, const uint16_t*, const uint16_t*, int64_t,
                       int64_t, int64_t, const int32_t*, const int32_t*, const int32_t*, const int32_t*,
-                      const uint8_t*, const int64_t*, int, int64_t, int64_t, int64_t, int64_t, int64_t, double,
+                      const uint8_t*, const int64_t*, int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
+                      double,
                       uint16_t*, int64_t, int64_t, double*);
 void oracle_sample(const float*, int64_t, int64_t, int64_t, int, const int32_t*, const float*, const float*,
                    const double*, int32_t*, unsigned char*);
@@ -355,9 +356,9 @@ static void case_variants(int64_t T, int64_t H, int64_t Hq, int64_t Hkv, int64_t
 // Paged decode attention: contexts in [lo, hi], random page permutation of an exact-size pool,
 // NHD cache; `chunk` = splits per request (0 = the library's choice).
 static void case_attn_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int lo, int hi,
-                             int64_t chunk) {
-  printf("attn_decode B=%lld Hq=%lld Hkv=%lld D=%lld P=%lld ctx=[%d,%d] chunk=%lld\n", (long long)B,
-         (long long)Hq, (long long)Hkv, (long long)D, (long long)P, lo, hi, (long long)chunk);
+                             int64_t chunk, int64_t window = -1) {
+  printf("attn_decode B=%lld Hq=%lld Hkv=%lld D=%lld P=%lld ctx=[%d,%d] chunk=%lld window=%lld\n", (long long)B,
+         (long long)Hq, (long long)Hkv, (long long)D, (long long)P, lo, hi, (long long)chunk, (long long)window);
   std::vector<int32_t> len(B), indptr(B + 1, 0), last(B);
   std::uniform_int_distribution<int> dl(lo, hi);
   for (int64_t b = 0; b < B; ++b) {
@@ -383,12 +384,12 @@ static void case_attn_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int6
   Buf<float> ws(std::max<int64_t>(B * splits * Hq * (D + 1), 1));
   rc_ok(pie_hip_attention_decode(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D,
                                  pages, ip.p, idx.p, ll.p, B, Hq, Hkv, D, P, 1.f / sqrtf((float)D),
-                                 splits, ws.p, (int64_t)(ws.n * 4), out.p, Hq * D, D, nullptr),
+                                 window, splits, ws.p, (int64_t)(ws.n * 4), out.p, Hq * D, D, nullptr),
         "attention_decode");
   std::vector<int32_t> qo(B + 1);
   for (int64_t b = 0; b <= B; ++b) qo[b] = (int32_t)b;
   oracle_attention(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, qo.data(), ip.p,
-                   idx.p, ll.p, nullptr, nullptr, 1, B, Hq, Hkv, D, P, 1.0 / sqrt((double)D), want.p, Hq * D,
+                   idx.p, ll.p, nullptr, nullptr, 1, window, B, Hq, Hkv, D, P, 1.0 / sqrt((double)D), want.p, Hq * D,
                    D, nullptr);
   printf("  splits %lld\n", (long long)splits);
   check_close("decode attention", out.p, want.p, B * Hq * D);
@@ -406,9 +407,9 @@ static void case_attn_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int6
 // Paged prefill attention: requests with ctx in [0, cmax] cached tokens and qo in [0, qmax] new
 // query tokens; mode 0 full, 1 causal, 2 a random custom mask.
 static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int cmax, int qmax,
-                              int mode, bool causal_mask = false) {
-  printf("attn_prefill B=%lld Hq=%lld Hkv=%lld D=%lld P=%lld ctx<=%d qo<=%d mode=%d\n", (long long)B,
-         (long long)Hq, (long long)Hkv, (long long)D, (long long)P, cmax, qmax, mode);
+                              int mode, bool causal_mask = false, int64_t window = -1) {
+  printf("attn_prefill B=%lld Hq=%lld Hkv=%lld D=%lld P=%lld ctx<=%d qo<=%d mode=%d window=%lld\n", (long long)B,
+         (long long)Hq, (long long)Hkv, (long long)D, (long long)P, cmax, qmax, mode, (long long)window);
   std::vector<int32_t> qo(B + 1, 0), indptr(B + 1, 0), last(B), kvl(B);
   std::uniform_int_distribution<int> dc(0, cmax), dq(0, qmax);
   for (int64_t b = 0; b < B; ++b) {
@@ -459,13 +460,13 @@ static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
     rc_ok(pie_hip_attention_pack_mask(mask.p, plan.p, qi.p, ip.p, ll.p, B, P, mw, T, packed.p, extent.p, nullptr),
           "pack_mask");
   rc_ok(pie_hip_attention_prefill(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, pages,
-                                  qi.p, ip.p, idx.p, ll.p, Hq, Hkv, D, P, 1.f / sqrtf((float)D), mode,
+                                  qi.p, ip.p, idx.p, ll.p, Hq, Hkv, D, P, 1.f / sqrtf((float)D), mode, window,
                                   mode == 2 ? packed.p : nullptr, mode == 2 ? extent.p : nullptr, plan.p, items,
                                   plan[4], out.p, Hq * D, D,
                                   nullptr),
         "attention_prefill");
   oracle_attention(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, qi.p, ip.p, idx.p,
-                   ll.p, mode == 2 ? mask.p : nullptr, mode == 2 ? moff.data() : nullptr, mode == 1, B, Hq,
+                   ll.p, mode == 2 ? mask.p : nullptr, mode == 2 ? moff.data() : nullptr, mode == 1, window, B, Hq,
                    Hkv, D, P, 1.0 / sqrt((double)D), want.p, Hq * D, D, nullptr);
   printf("  T=%lld items=%lld\n", (long long)T, (long long)items);
   check_close("prefill attention", out.p, want.p, T * Hq * D);
@@ -620,6 +621,7 @@ int main(int argc, char** argv) {
     case_attn_decode(2, 6, 1, 256, 8, 30, 300, 0);    // G = 6, D = 256, library's split count
     case_attn_decode(2, 16, 1, 128, 5, 20, 700, 5);   // G = 16, page size 5
     case_attn_decode(2, 4, 2, 64, 1, 600, 1500, 1);   // page size 1: several page-table windows
+    case_attn_decode(3, 8, 2, 128, 16, 1, 700, 3, 100);  // sliding window of 100 (+ the query)
   }
   if (all || c == "sample") {
     for (int mode = 0; mode <= 4; ++mode) case_sample(5, 301, mode, mode == 4);
@@ -636,6 +638,8 @@ int main(int argc, char** argv) {
     case_attn_prefill(2, 8, 2, 128, 16, 50, 100, 1);  // up to 400 rows: several items per request
     case_attn_prefill(2, 8, 2, 128, 16, 50, 100, 2);
     case_attn_prefill(3, 8, 2, 128, 16, 20, 120, 2, true);  // masks within the causal window
+    case_attn_prefill(3, 8, 2, 128, 16, 200, 120, 1, false, 70);  // causal + sliding window
+    case_attn_prefill(2, 8, 2, 128, 8, 100, 90, 2, false, 40);    // custom mask + sliding window
   }
   if (all || c == "qkfused") {
     case_qk_fused(5, 4, 2, 128);  // fused kernel

@@ -23,12 +23,12 @@ def _workspace(dev):
     return torch.zeros(WS_BYTES, dtype=torch.uint8, device=dev)
 
 
-def _decode(dev, a, splits=None, out=None):
+def _decode(dev, a, splits=None, out=None, window_left=-1):
     pb, lay = a["batch"], a["layout"]
     w = attention.BatchDecodeWithPagedKVCacheWrapper(_workspace(dev), lay)
     w.plan(pb.kv_indptr.to(dev), pb.kv_indices.to(dev), pb.kv_last_page_len.to(dev),
            a["Hq"], a["Hkv"], a["D"], pb.page_size, pos_encoding_mode="NONE",
-           q_data_type=torch.bfloat16)
+           q_data_type=torch.bfloat16, window_left=window_left)
     if splits is not None:
         w._plan["splits"] = splits
     o = w.run(a["q"].to(dev), a["cache"].to(dev), out=out)
@@ -36,11 +36,11 @@ def _decode(dev, a, splits=None, out=None):
     return o
 
 
-def _want(a, custom=None):
+def _want(a, custom=None, window_left=-1, causal=True):
     pb = a["batch"]
     return oracle.attention(N(a["q"]), N(a["cache"]), N(pb.qo_indptr), N(pb.kv_indptr),
                             N(pb.kv_indices), N(pb.kv_last_page_len), custom_mask=custom,
-                            layout=a["layout"])
+                            layout=a["layout"], window_left=window_left, causal=causal)
 
 
 def _tight(got, want, what):
@@ -175,13 +175,13 @@ def test_decode_rejects_bad_input(dev):
 
 
 # ----------------------------------------------------------------------------- prefill
-def _prefill(dev, a, causal=True, custom=None, out=None):
+def _prefill(dev, a, causal=True, custom=None, out=None, window_left=-1):
     pb = a["batch"]
     w = attention.BatchPrefillWithPagedKVCacheWrapper(_workspace(dev), a["layout"])
     w.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev),
            pb.kv_last_page_len.to(dev), a["Hq"], a["Hkv"], a["D"], pb.page_size,
            custom_mask=None if custom is None else torch.as_tensor(custom).to(dev), causal=causal,
-           q_data_type=torch.bfloat16)
+           q_data_type=torch.bfloat16, window_left=window_left)
     o = w.run(a["q"].to(dev), a["cache"].to(dev), out=out)
     torch.cuda.synchronize()
     return o
@@ -284,4 +284,72 @@ def test_prefill_rejects_bad_input(dev):
                custom_mask=torch.ones(3, dtype=torch.bool, device=dev))  # mask too short
     with pytest.raises(NotImplementedError):
         w.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev),
-               pb.kv_last_page_len.to(dev), 8, 2, 128, 16, window_left=128)
+               pb.kv_last_page_len.to(dev), 8, 2, 128, 16, logits_soft_cap=30.0)
+
+
+# ----------------------------------------------------------------------------- sliding window
+@pytest.mark.parametrize("window_left", [0, 31, 200, 4096])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_decode_sliding_window(dev, window_left, splits):
+    """flashinfer's window_left (OLMo-3 plans it per layer, olmo3.py:973-1005): the query sees
+    positions >= kv_len - 1 - window_left."""
+    g = torch.Generator().manual_seed(window_left + splits)
+    ctx = torch.randint(0, 900, (7,), generator=g).to(torch.int32)
+    a = wl.attn_batch(ctx, torch.ones(7, dtype=torch.int32), Hq=16, Hkv=4, D=128, page_size=16,
+                      seed=110 + splits)
+    got = _decode(dev, a, splits, window_left=window_left)
+    want = _want(a, window_left=window_left)
+    assert_bf16_close(N(got), want, what=f"window {window_left}")
+    _tight(got, want, f"window {window_left}")
+
+
+@pytest.mark.parametrize("window_left", [0, 50, 300])
+@pytest.mark.parametrize("mode", ["causal", "full", "custom"])
+def test_prefill_sliding_window(dev, window_left, mode):
+    g = torch.Generator().manual_seed(window_left * 3 + len(mode))
+    ctx = torch.randint(0, 400, (4,), generator=g).to(torch.int32)
+    qo = torch.randint(1, 200, (4,), generator=g).to(torch.int32)
+    a = wl.attn_batch(ctx, qo, Hq=32, Hkv=8, D=128, page_size=16, seed=120)
+    custom = None
+    if mode == "custom":
+        pb = a["batch"]
+        n = int((pb.lens.to(torch.int64) * pb.seq_lens.to(torch.int64)).sum())
+        custom = torch.rand(n, generator=g) < 0.6
+    got = _prefill(dev, a, causal=mode == "causal", custom=custom, window_left=window_left)
+    want = _want(a, custom=None if custom is None else custom.numpy(), window_left=window_left,
+                 causal=mode == "causal")
+    assert_bf16_close(N(got), want, what=f"{mode} window {window_left}")
+    _tight(got, want, f"{mode} window {window_left}")
+
+
+def test_decode_graph_with_window_like_olmo(dev):
+    """OLMo-3 captures decode graphs with window_left in the plan (olmo3.py:381-391)."""
+    B, P, window = 8, 16, 100
+    pool = B * 40
+    cache = wl.normal((pool + 1, 2, P, 8, 128), 130).to(dev)
+    ib = torch.arange(B + 1, dtype=torch.int32, device=dev)
+    xb = torch.full((pool + 1,), pool, dtype=torch.int32, device=dev)
+    lb = torch.ones(B, dtype=torch.int32, device=dev)
+    w = attention.BatchDecodeWithPagedKVCacheWrapper(_workspace(dev), "NHD", use_cuda_graph=True,
+                                                     paged_kv_indptr_buffer=ib,
+                                                     paged_kv_indices_buffer=xb,
+                                                     paged_kv_last_page_len_buffer=lb)
+    w.plan(ib, xb, lb, 32, 8, 128, P, q_data_type=torch.bfloat16, window_left=window)
+    q = torch.zeros((B, 32, 128), dtype=torch.bfloat16, device=dev)
+    out = torch.empty_like(q)
+    w.run(q, cache, out=out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        w.run(q, cache, out=out)
+    ctx = torch.randint(1, 40 * P - 1, (B,), generator=torch.Generator().manual_seed(131)).to(torch.int32)
+    pb = wl.paged_batch(ctx, torch.ones(B, dtype=torch.int32), P, pool, 132)
+    ib.copy_(pb.kv_indptr)
+    xb[: pb.kv_indices.numel()].copy_(pb.kv_indices)
+    lb.copy_(pb.kv_last_page_len)
+    q.copy_(wl.normal((B, 32, 128), 133))
+    graph.replay()
+    torch.cuda.synchronize()
+    a = {"q": q.cpu(), "cache": cache.cpu(), "batch": pb, "layout": "NHD"}
+    want = _want(a, window_left=window)
+    _tight(out, want, "graph replay with window")

@@ -457,7 +457,7 @@ def _gather_kv(cache, pb, b, layout="NHD"):
     return torch.stack(rows_k), torch.stack(rows_v)
 
 
-def _sdpa_reference(a, custom=None):
+def _sdpa_reference(a, custom=None, window_left=-1):
     """torch-CPU scaled_dot_product_attention in float64, one request at a time, with the
     causal window written as an explicit boolean mask (or the custom mask)."""
     pb, q = a["batch"], a["q"].to(torch.float64)
@@ -475,6 +475,9 @@ def _sdpa_reference(a, custom=None):
         else:
             m = torch.as_tensor(custom[moff:moff + qo_len * kv_len]).view(qo_len, kv_len).bool()
             moff += qo_len * kv_len
+        if window_left >= 0:
+            m = m & torch.tensor([[t >= kv_len - qo_len + i - window_left for t in range(kv_len)]
+                                  for i in range(qo_len)])
         k = k.repeat_interleave(G, dim=1).transpose(0, 1)  # [Hq, kv, D]
         v = v.repeat_interleave(G, dim=1).transpose(0, 1)
         o = F.scaled_dot_product_attention(q[q0:q1].transpose(0, 1), k, v, attn_mask=m)
@@ -526,6 +529,23 @@ def test_attention_custom_mask_vs_sdpa_and_causal():
     np.testing.assert_allclose(got, want.numpy(), rtol=2 ** -8, atol=1e-6)
     # the causal window written as a custom mask is the default behaviour, bit for bit
     assert_bits_equal(_oracle_attn(a, torch.cat(causal).numpy()), _oracle_attn(a), "causal mask")
+
+
+@pytest.mark.parametrize("window_left", [0, 5, 40])
+def test_attention_sliding_window_vs_torch_sdpa(window_left):
+    a = wl.attn_batch([37, 0, 5, 60], [1, 19, 12, 3], Hq=8, Hkv=2, D=64, page_size=16, seed=13)
+    want = _sdpa_reference(a, window_left=window_left).to(torch.float32)
+    got = oracle.bf16_to_f32(_oracle_attn(a, window_left=window_left))
+    assert np.abs(got - want.numpy()).max() <= 2 ** -8 * np.abs(want.numpy()).max() + 1e-6
+    if window_left == 0:  # each query sees only its own position: output = its v row, exactly
+        pb = a["batch"]
+        for b in range(4):
+            _, v = _gather_kv(a["cache"], pb, b)
+            q0, q1 = int(pb.qo_indptr[b]), int(pb.qo_indptr[b + 1])
+            L = int(pb.seq_lens[b])
+            for i in range(q1 - q0):
+                row = v[L - (q1 - q0) + i].repeat_interleave(4, 0).float().numpy()
+                assert (got[q0 + i] == row).all(), f"request {b} token {i}"
 
 
 def test_attention_closed_forms():
