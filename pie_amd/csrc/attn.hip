@@ -483,6 +483,9 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(int B, int Hq, int split
 #ifndef PIE_PREFILL_NW
 #define PIE_PREFILL_NW 4
 #endif
+#ifndef PIE_PREFILL_MFMA32  // D = 128 prefill on the 32x32x16 kernel (attn_prefill32_kernel)
+#define PIE_PREFILL_MFMA32 1
+#endif
 #ifndef PIE_PREFILL_RT
 #define PIE_PREFILL_RT (8 / PIE_PREFILL_NW)
 #endif
@@ -762,6 +765,272 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) vo
   }
 }
 
+
+// ------------------------------------------------------------------------------ prefill, D = 128
+// The same work items, visibility rules, K/V tile pipeline and masks as attn_prefill_kernel, with
+// the products on v_mfma_f32_32x32x16_bf16 and the output computed transposed:
+//   S^T = K Q^T    A = 32 kv tokens x 16 dims (lane (t, kg): token t's dims 8(2s+kg)..+8 at
+//                  step s, from LDS), B = 32 query rows (lane (r, kg): row r, the same dims)
+//   O^T = V^T P^T  A = 32 dims x 16 tokens (two transpose reads of 4 V rows each),
+//                  B = P^T: lane (r, kg) holds row r's probabilities of tokens
+//                  16j + 8(e/4) + 4kg + e%4, exactly 8 consecutive registers of S^T's C layout
+// so every lane owns one query row r = lane % 32 in both products: its running max, sum and
+// rescale factor are its own (one exchange with lane ^ 32 for the max), and no factor has to be
+// broadcast to other lanes. Each wave owns 32 rows; a work group of 4 waves, 128 rows.
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16_t mfma_32x32x16(const u32x4_t& a, const u32x4_t& b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// V-row swizzle for this kernel's transpose reads: one read takes 4 consecutive rows x 4 chunks
+// per half-wave, so rows r..r+3 XOR chunk bits 2-3 with r mod 4.
+__device__ __forceinline__ int v32_swizzle(int r) { return (r & 3) << 2; }
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
+    const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv,
+    const int32_t* __restrict__ qo_indptr, int G, float scale_log2, const int32_t* __restrict__ plan,
+    int mode, int window_left, const uint32_t* __restrict__ packed,
+    const int64_t* __restrict__ word_off, const int32_t* __restrict__ extent,
+    uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
+  static_assert(D == 128, "32x32 prefill is built for head_dim 128");
+  constexpr int NS = D / 16;  // QK k-steps
+  constexpr int NB = D / 32;  // 32-dim output blocks
+  constexpr int CH = D / 8, RPI = 64 / CH;
+  constexpr int kRows = 128, NT = 256;
+  constexpr int TILE = kTileTokens * D;
+  __shared__ __attribute__((aligned(16))) char smem[2 * 2 * TILE * 2];
+  __shared__ int32_t ptab[kPageWin];
+  __shared__ int window_bad;
+  __shared__ uint32_t mwt[2][NT];
+
+  const int32_t* item = plan + kPlanHeader + 2 * blockIdx.x;
+  const int b = item[0], row0 = item[1];
+  const int kvh = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
+  const int r32 = lane & 31, kg = lane >> 5;
+  const int q0 = qo_indptr[b], qo_len = qo_indptr[b + 1] - q0;
+  const int kv_len = kv_length(kv, b);
+  const int rows = qo_len * G;
+  const int page0 = kv.indptr[b];
+
+  // this lane's query row
+  const int R = row0 + 32 * w + r32;
+  const bool valid = R < rows;
+  const int tok = valid ? R / G : 0, hg = valid ? R - tok * G : 0;
+  const int lim = !valid ? -1 : mode == 1 ? min(kv_len - qo_len + tok, kv_len - 1) : kv_len - 1;
+  const int lo = window_left >= 0 ? kv_len - qo_len + tok - window_left : 0;
+  u32x4_t qb[NS];
+  {
+    const uint16_t* qp = q + (int64_t)(q0 + tok) * q_ts + (int64_t)(kvh * G + hg) * q_hs;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const u32x4_t z = {0u, 0u, 0u, 0u};
+      qb[s] = valid ? ld16v(qp + 8 * (2 * s + kg)) : z;
+    }
+  }
+  f32x16_t o[NB];
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[bb][i] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int last_row = min(rows, row0 + kRows) - 1;
+  int kv_end = mode == 1 ? min(kv_len, kv_len - qo_len + last_row / G + 1) : kv_len;
+  if (mode == 2) {
+    __shared__ int wg_extent;
+    if (threadIdx.x == 0) wg_extent = 0;
+    __syncthreads();
+    const int rr = row0 + (int)threadIdx.x;
+    if ((int)threadIdx.x < kRows && rr < rows) atomicMax(&wg_extent, extent[q0 + rr / G]);
+    __syncthreads();
+    kv_end = min(kv_len, wg_extent);
+  }
+  const int kv_begin = window_left >= 0 ? max(0, kv_len - qo_len + row0 / G - window_left) & ~31 : 0;
+  const int nw = (kv_len + 31) / 32;
+  const uint32_t* mword = mode == 2 ? packed + word_off[b] + (int64_t)tok * nw : nullptr;
+  // uniform bounds of the wave's rows: tiles inside [wave_lo, wave_lim] need no per-element test
+  int wave_lim = valid ? lim : 0x7fffffff, wave_lo = valid ? lo : 0;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    wave_lim = min(wave_lim, __builtin_amdgcn_ds_bpermute((lane ^ off) << 2, wave_lim));
+    wave_lo = max(wave_lo, __builtin_amdgcn_ds_bpermute((lane ^ off) << 2, wave_lo));
+  }
+  wave_lim = uniform(wave_lim);
+  wave_lo = uniform(wave_lo);
+
+  uint16_t* kt = reinterpret_cast<uint16_t*>(smem);  // [2 buffers][K, V][32][D]
+  constexpr int WR = kTileTokens / 4;  // rows of each K / V tile one wave loads
+  constexpr int NL = WR / RPI;
+  struct Slot { u32x4_t k[NL], v[NL]; uint32_t mw; };
+  const int win = max(kTileTokens, (kPageWin - 2) * kv.page_size / kTileTokens * kTileTokens);
+  for (int wt0 = kv_begin; wt0 < kv_end; wt0 += win) {
+    const int wt1 = min(kv_end, wt0 + win);
+    const int lp0 = (int)kv.pdiv.div((uint32_t)wt0);
+    const int npg = (int)kv.pdiv.div((uint32_t)(wt1 - 1)) - lp0 + 1;
+    const int ntiles = (wt1 - wt0 + kTileTokens - 1) / kTileTokens;
+    if (threadIdx.x == 0) window_bad = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < npg; i += NT) {
+      const int pg = kv.indices[page0 + lp0 + i];
+      ptab[i] = pg;
+      if ((unsigned)pg >= (unsigned)kv.num_pages) window_bad = 1;
+    }
+    __syncthreads();
+    const bool all_pages_ok = window_bad == 0;
+    auto gload = [&](Slot& sl, int tile) {
+      const int t0 = wt0 + tile * kTileTokens;
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        const int r = WR * w + RPI * i + lane / CH;
+        bool ok;
+        const uint64_t off = kv_offset_lds(kv, ptab, lp0, min(t0 + r, wt1 - 1), kvh, ok);
+        sl.k[i] = ld16v(kv.k + off + 8 * ((lane % CH) ^ chunk_swizzle<D>(r)));
+        sl.v[i] = ld16v(kv.v + off + 8 * ((lane % CH) ^ v32_swizzle(r)));
+      }
+      if (mode == 2) sl.mw = mword[t0 >> 5];
+    };
+    auto lwrite = [&](const Slot& sl, int tile) {
+      uint16_t* kd = kt + (tile & 1) * 2 * TILE;
+      if (mode == 2) mwt[tile & 1][threadIdx.x] = sl.mw;
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        *reinterpret_cast<u32x4_t*>(kd + (WR * w + RPI * i) * D + 8 * lane) = sl.k[i];
+        *reinterpret_cast<u32x4_t*>(kd + TILE + (WR * w + RPI * i) * D + 8 * lane) = sl.v[i];
+      }
+    };
+    auto compute = [&](int tile) {
+      const int t0 = wt0 + tile * kTileTokens;
+      const uint16_t* kd = kt + (tile & 1) * 2 * TILE;
+      // S^T: token r32 of the tile against this lane group's 32 rows
+      f32x16_t sacc;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sacc[i] = 0.f;
+      {
+        const int z = chunk_swizzle<D>(r32);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          const u32x4_t ka = *reinterpret_cast<const u32x4_t*>(kd + r32 * D + 8 * ((2 * s + kg) ^ z));
+          sacc = mfma_32x32x16(ka, qb[s], sacc);
+        }
+      }
+      // visibility of token tt(i) = 8(i/4) + 4kg + i%4 for this lane's row: mask bits by shifts,
+      // then the per-element bounds only in tiles that cross a row's limit or window start
+      uint32_t vis = 0xffffu;
+      if (mode == 2) {
+        const uint32_t mw = mwt[tile & 1][threadIdx.x];
+        vis = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) vis |= ((mw >> (8 * c + 4 * kg)) & 15u) << (4 * c);
+      }
+      if (!all_pages_ok || t0 + kTileTokens - 1 > wave_lim || t0 < wave_lo) {
+        uint64_t tv = 0xffffffffull;
+        if (!all_pages_ok) {
+          bool pok = false;
+          if (lane < kTileTokens && t0 + lane < wt1) kv_offset_lds(kv, ptab, lp0, t0 + lane, kvh, pok);
+          tv = __builtin_amdgcn_ballot_w64(pok);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int tt = 8 * (i >> 2) + 4 * kg + (i & 3), t = t0 + tt;
+          if (!(t <= lim && t >= lo && ((tv >> tt) & 1ull))) vis &= ~(1u << i);
+        }
+      }
+      float sc[16];
+      float mx = -INFINITY;
+      if (__builtin_amdgcn_ballot_w64(vis != 0xffffu) == 0) {  // wave-uniform: all visible
+#pragma unroll
+        for (int i = 0; i < 16; ++i) { sc[i] = sacc[i] * scale_log2; mx = fmaxf(mx, sc[i]); }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          sc[i] = ((vis >> i) & 1u) ? sacc[i] * scale_log2 : -INFINITY;
+          mx = fmaxf(mx, sc[i]);
+        }
+      }
+      mx = fmaxf(mx, lane_read(mx, lane ^ 32));
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = fast_exp2(m_run - m_use);
+      m_run = m_new;
+      float psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) { sc[i] = fast_exp2(sc[i] - m_use); psum += sc[i]; }
+      l_run = l_run * alpha + psum;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[bb][i] *= alpha;
+      }
+      u32x4_t pb[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        pb[j] = u32x4_t{pack_bf2(sc[8 * j], sc[8 * j + 1]), pack_bf2(sc[8 * j + 2], sc[8 * j + 3]),
+                        pack_bf2(sc[8 * j + 4], sc[8 * j + 5]), pack_bf2(sc[8 * j + 6], sc[8 * j + 7])};
+      // O^T += V^T P^T. Transpose-read source lanes: group G16 = lane / 16 reads rows
+      // 16j + 8h + 4kg + (lane%16)/4 (h: first or second 4 tokens), dims 32bb + 16(G16%2) + 4(lane%4)
+      const int g16 = lane >> 4, jj = (lane >> 2) & 3, qq = lane & 3;
+      const uint16_t* vbase = kd + TILE;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+          uint2 hv[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int r = 16 * j + 8 * h + 4 * kg + jj;
+            const int dim = 32 * bb + 16 * (g16 & 1) + 4 * qq;
+            const int c = (dim >> 3) ^ v32_swizzle(r);
+            hv[h] = lds_read_tr16(vbase + r * D + 8 * c + (dim & 7));
+          }
+          const u32x4_t va = {hv[0].x, hv[0].y, hv[1].x, hv[1].y};
+          o[bb] = mfma_32x32x16(va, pb[j], o[bb]);
+        }
+    };
+    Slot sa, sb;
+    gload(sa, 0);
+    if (ntiles > 1) gload(sb, 1);
+    lwrite(sa, 0);
+    if (ntiles > 2) gload(sa, 2);
+    __syncthreads();
+    for (int k = 0;;) {
+      compute(k);
+      if (k + 1 < ntiles) {
+        lwrite(sb, k + 1);
+        if (k + 3 < ntiles) gload(sb, k + 3);
+      }
+      __syncthreads();
+      if (++k >= ntiles) break;
+      compute(k);
+      if (k + 1 < ntiles) {
+        lwrite(sa, k + 1);
+        if (k + 3 < ntiles) gload(sa, k + 3);
+      }
+      __syncthreads();
+      if (++k >= ntiles) break;
+    }
+  }
+  // normalise and write: o[bb][i] is dim 32bb + 8(i/4) + 4kg + i%4 of row R; lanes r and r^32
+  // together cover 8 consecutive dims
+  const float L = l_run + lane_read(l_run, lane ^ 32);
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  if (valid) {
+    uint16_t* op = out + (int64_t)(q0 + tok) * o_ts + (int64_t)(kvh * G + hg) * o_hs;
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint2 v = {pack_bf2(o[bb][4 * c] * inv, o[bb][4 * c + 1] * inv),
+                         pack_bf2(o[bb][4 * c + 2] * inv, o[bb][4 * c + 3] * inv)};
+        *reinterpret_cast<uint2*>(op + 32 * bb + 8 * c + 4 * kg) = v;
+      }
+  }
+}
+
 }  // namespace pie
 
 using namespace pie;
@@ -947,8 +1216,12 @@ static void launch_prefill(hipStream_t st, dim3 grid, const uint16_t* q, int64_t
                            const int32_t* plan, int mode, int window_left, const uint32_t* packed,
                            const int64_t* woff, const int32_t* extent, uint16_t* out, int64_t o_ts,
                            int64_t o_hs) {
-  hipLaunchKernelGGL(attn_prefill_kernel<D>, grid, dim3(64 * prefill_waves<D>()), 0, st, q, q_ts, q_hs, kv,
-                     qo_indptr, G, sl2, plan, mode, window_left, packed, woff, extent, out, o_ts, o_hs);
+  if constexpr (D == 128 && PIE_PREFILL_MFMA32)
+    hipLaunchKernelGGL(attn_prefill32_kernel<128>, grid, dim3(256), 0, st, q, q_ts, q_hs, kv, qo_indptr, G,
+                       sl2, plan, mode, window_left, packed, woff, extent, out, o_ts, o_hs);
+  else
+    hipLaunchKernelGGL(attn_prefill_kernel<D>, grid, dim3(64 * prefill_waves<D>()), 0, st, q, q_ts, q_hs, kv,
+                       qo_indptr, G, sl2, plan, mode, window_left, packed, woff, extent, out, o_ts, o_hs);
 }
 
 // Visible extent of every query token under the packed mask: 1 + the last kv position whose bit

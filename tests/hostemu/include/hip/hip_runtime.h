@@ -4,7 +4,7 @@
 //
 // Emulated: thread/block indices, __shared__ (function-local statics: blocks run one after
 // another), __syncthreads (block barrier), DPP row_ror / quad_perm, readlane, readfirstlane
-// (wave barriers), ballot, ds_bpermute, MFMA 16x16x32 bf16, ds_read_b64_tr_b16 (wave-wide
+// (wave barriers), ballot, ds_bpermute, MFMA 16x16x32 and 32x32x16 bf16, ds_read_b64_tr_b16 (wave-wide
 // gathers), global_load_lds (a per-lane copy), the fp builtins used, hipLaunchKernelGGL and the few runtime calls made.
 #pragma once
 
@@ -152,6 +152,33 @@ VC mfma_16x16x32_bf16(VA a, VB b, VC c, int, int, int) {
   return r;
 }
 
+// v_mfma_f32_32x32x16_bf16: lane l supplies A[l%32][8(l/32)+j] and B[8(l/32)+j][l%32] and
+// receives C[8(i/4) + 4(l/32) + i%4][l%32] for i = 0..15.
+template <typename VA, typename VB, typename VC>
+VC mfma_32x32x16_bf16(VA a, VB b, VC c, int, int, int) {
+  static_assert(sizeof(VA) == 16 && sizeof(VB) == 16 && sizeof(VC) == 64, "operand sizes");
+  Wave* w = ctx->wave;
+  const int lane = ctx->lane;
+  memcpy(w->ma[lane], &a, 16);
+  memcpy(w->mb[lane], &b, 16);
+  w->bar.arrive_and_wait();
+  float cf[16];
+  memcpy(cf, &c, 64);
+  const int col = lane % 32;
+  for (int i = 0; i < 16; ++i) {
+    const int row = 8 * (i / 4) + 4 * (lane / 32) + i % 4;
+    float acc = cf[i];
+    for (int k = 0; k < 16; ++k)
+      acc += bf16_bits_to_float(w->ma[row + 32 * (k / 8)][k % 8]) *
+             bf16_bits_to_float(w->mb[col + 32 * (k / 8)][k % 8]);
+    cf[i] = acc;
+  }
+  w->bar.arrive_and_wait();
+  VC r;
+  memcpy(&r, cf, 64);
+  return r;
+}
+
 // ds_read_b64_tr_b16: within each 16-lane group, output lane r element j is element r%4 of
 // the 8 bytes addressed by lane 4j + r/4 of the group.
 template <typename P>
@@ -222,6 +249,7 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 #define __builtin_amdgcn_ballot_w64 emu::ballot
 #define __builtin_amdgcn_ds_bpermute emu::bpermute
 #define __builtin_amdgcn_mfma_f32_16x16x32_bf16 emu::mfma_16x16x32_bf16
+#define __builtin_amdgcn_mfma_f32_32x32x16_bf16 emu::mfma_32x32x16_bf16
 #define __builtin_amdgcn_ds_read_tr16_b64_v4i16 emu::ds_read_tr16_b64
 #define __builtin_amdgcn_global_load_lds emu::global_load_lds
 #define __builtin_amdgcn_s_waitcnt(x) ((void)(x))
