@@ -477,24 +477,18 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(int B, int Hq, int split
 // Visibility: mode 0 every cached position, 1 causal (t <= kv_len - qo_len + i), 2 the custom
 // mask, bit-packed by attn_pack_mask_kernel: query token i of request b reads 32-bit word
 // w (kv positions 32w..32w+31) at packed + word_off[b] + i * ceil(kv_len / 32) + w.
-// Work-group shape: for D = 128, PIE_PREFILL_NW waves of 8 / PIE_PREFILL_NW 16-row MFMA row tiles
-// each; D = 64 uses 4 waves of two tiles (a wave's share of a K/V tile must fill one load
-// instruction), D = 256 4 waves of one tile (its accumulators would not fit twice).
-#ifndef PIE_PREFILL_NW
-#define PIE_PREFILL_NW 4
-#endif
-#ifndef PIE_PREFILL_MFMA32  // D = 128 prefill on the 32x32x16 kernel (attn_prefill32_kernel)
+// Work-group shape of attn_prefill_kernel: 4 waves of two 16-row MFMA row tiles (one for D = 256,
+// whose accumulators would not fit twice). Head dim 128 runs attn_prefill32_kernel (32 rows per
+// wave, same 128-row work items) unless PIE_PREFILL_MFMA32=0 selects this kernel for comparison.
+#ifndef PIE_PREFILL_MFMA32
 #define PIE_PREFILL_MFMA32 1
 #endif
-#ifndef PIE_PREFILL_RT
-#define PIE_PREFILL_RT (8 / PIE_PREFILL_NW)
-#endif
 template <int D>
-constexpr int prefill_waves() { return D == 128 ? PIE_PREFILL_NW : 4; }
+constexpr int prefill_waves() { return 4; }
 template <int D>
-constexpr int prefill_row_tiles() { return D == 256 ? 1 : D == 128 ? PIE_PREFILL_RT : 2; }
+constexpr int prefill_row_tiles() { return D == 256 ? 1 : 2; }
 template <int D>
-constexpr int prefill_min_waves() { return (D == 256 || prefill_row_tiles<D>() > 2) ? 1 : 2; }
+constexpr int prefill_min_waves() { return D == 256 ? 1 : 2; }
 template <int D>
 constexpr int prefill_rows() { return 16 * prefill_waves<D>() * prefill_row_tiles<D>(); }
 constexpr int kPlanHeader = 16;  // plan words before the items: [0] items, [1] batch, [2] rows per item
@@ -686,13 +680,7 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) vo
         if (__builtin_amdgcn_ballot_w64(vm != 0xFFu) == 0) vm = 0xFFu;  // keep the fast path visible
         float sc[2][4];
         st[rt].scores(ka, vm, scale_log2, sc);
-#ifdef PIE_DIAG_NO_SOFTMAX
-        pa[rt] = u32x4_t{pack_bf2(sc[0][0], sc[0][1]), pack_bf2(sc[0][2], sc[0][3]),
-                         pack_bf2(sc[1][0], sc[1][1]), pack_bf2(sc[1][2], sc[1][3])};
-        rs[rt] = false;
-#else
         pa[rt] = st[rt].softmax(sc, lane, a[rt], rs[rt]);
-#endif
       }
       // PV: the V operand of each 16-dim block comes straight from LDS (transpose reads)
       const int j = (lane >> 2) & 3, qq = lane & 3;
