@@ -4,7 +4,7 @@
 // pie/src/flashinfer_metal/sampling.py:19-79).
 //
 // One work group of 1024 threads per row; rows of 32k-256k vocabulary entries are streamed from
-// HBM/L2 with 16-byte loads in every pass.
+// HBM/L2 with 16-byte loads.
 //
 // Filters (flashinfer's semantics, exact): top_k keeps token i iff fewer than k tokens are
 // strictly more probable (tokens tied with the k-th largest all stay); top_p keeps i iff the mass
@@ -14,8 +14,13 @@
 // counts (top_k) or masses (top_p) per digit. Masses are fixed point (p * 2^40 rounded, summed in
 // 64-bit integers), so every sum is exact and independent of thread order: the same row always
 // gives the same kept set and the same sample.
+// Two row reads in the common case: pass A finds a floor under the threshold (from each thread's
+// two largest keys, or the row maximum for min_p), pass B copies the elements above it into LDS
+// in vocabulary order, and the radix selects and the draw run over that short list. Plain
+// sampling, and rows whose list would not fit, take the direct passes over the row.
 // Draw: inverse CDF in index order over the kept tokens, target u * kept mass, with u from
-// Philox4x32-10 (counter = (offset, row), key = seed) or caller-given uniforms.
+// Philox4x32-10 (counter = (offset, row), key = seed) or caller-given uniforms; the kept-mass
+// pass sums chunks of the row so that only the chunk holding the target is scanned.
 #include <math.h>
 
 #include "common.h"
@@ -126,15 +131,18 @@ __device__ __forceinline__ void for_row(const float* p, int V, bool vec, F&& f) 
 }
 
 // Radix search over keys >= lo (8 bits per pass, most significant first). by_mass = false: the
-// key of the need-th largest key (top-k threshold). by_mass = true: the smallest key v such that
-// the mass of keys strictly above v is below thr (top-p threshold; the maximal key when thr <= 0);
-// returns 0 if no key >= lo exists.
+// key of the need-th largest key (top-k threshold; 0 if fewer than need keys >= lo exist).
+// by_mass = true: the smallest key v such that the mass of keys strictly above v is below thr
+// (top-p threshold; the maximal key when thr <= 0); 0 if no key >= lo exists. Each pass counts
+// the digits of the keys under the current prefix; wave 0 then scans the 256 digits from the top
+// (4 per lane) to pick the next one.
 __device__ uint32_t radix_threshold(const float* p, int V, bool vec, uint32_t lo, bool by_mass,
                                     uint32_t need, double thr, SampleShared& sh) {
   uint32_t prefix = 0, pmask = 0;
   uint64_t above = 0;  // mass of keys above the current prefix bucket (by_mass)
   for (int shift = 24; shift >= 0; shift -= 8) {
     for (int i = threadIdx.x; i < 256; i += kSampThreads) { sh.cnt[i] = 0; sh.mass[i] = 0; }
+    if (threadIdx.x == 0) sh.u32a = 0xffffffffu;
     __syncthreads();
     for_row(p, V, vec, [&](int, float x) {
       const uint32_t k = prob_key(x);
@@ -144,38 +152,72 @@ __device__ uint32_t radix_threshold(const float* p, int V, bool vec, uint32_t lo
       if (by_mass) atomicAdd((unsigned long long*)&sh.mass[d], (unsigned long long)prob_mass(x));
     });
     __syncthreads();
-    if (threadIdx.x == 0) {
-      uint32_t dsel = 0;
-      bool found = false;
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      uint32_t c[4];
+      uint64_t m[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {  // this lane's digits, descending: 255 - 4 lane - e
+        c[e] = sh.cnt[255 - 4 * lane - e];
+        m[e] = by_mass ? sh.mass[255 - 4 * lane - e] : 0ull;
+      }
+      const uint32_t lc = c[0] + c[1] + c[2] + c[3];
+      const uint64_t lm = m[0] + m[1] + m[2] + m[3];
+      uint32_t ic = lc;
+      uint64_t im = lm;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t yc = (uint32_t)__builtin_amdgcn_ds_bpermute((lane >= o ? lane - o : lane) << 2, (int)ic);
+        const uint64_t ym = by_mass ? shfl_u64(im, lane >= o ? lane - o : lane) : 0ull;
+        if (lane >= o) { ic += yc; im += ym; }
+      }
+      uint32_t cc = ic - lc;          // keys in the digits above this lane's first
+      uint64_t ma = above + im - lm;  // their mass plus the mass above the prefix
       if (!by_mass) {
-        uint32_t c = 0;
-        for (int d = 255; d >= 0; --d) {
-          if (c + sh.cnt[d] >= need && sh.cnt[d] > 0) { dsel = (uint32_t)d; need -= c; found = true; break; }
-          c += sh.cnt[d];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (c[e] && cc < need && cc + c[e] >= need) {  // exactly one digit qualifies
+            sh.u32a = prefix | ((uint32_t)(255 - 4 * lane - e) << shift);
+            sh.u32b = need - cc;
+          }
+          cc += c[e];
         }
       } else {
-        uint64_t a = above, a_sel = above;
-        int hi = -1;
-        for (int d = 255; d >= 0; --d) {
-          if (sh.cnt[d] > 0) {
-            if (hi < 0) hi = d;
-            if ((double)a < thr) { dsel = (uint32_t)d; a_sel = a; found = true; }
-            else break;
+        // the lowest non-empty digit whose mass above is below thr (masses above only grow
+        // downwards, so the qualifying digits run from the top); the highest non-empty digit
+        // when none qualifies
+        int low = 256, high = -1;
+        uint64_t a = ma;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int d = 255 - 4 * lane - e;
+          if (c[e]) {
+            if ((double)a < thr) low = d;
+            high = max(high, d);
           }
-          a += sh.mass[d];
+          a += m[e];
         }
-        if (!found && hi >= 0) { dsel = (uint32_t)hi; a_sel = above; found = true; }  // thr <= 0: the maximum
-        above = a_sel;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+          low = min(low, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, low));
+          high = max(high, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, high));
+        }
+        const int dsel = low < 256 ? low : high;
+        if (dsel >= 0 && (255 - dsel) / 4 == lane) {  // the owner of dsel records the mass above it
+          const int ei = (255 - dsel) % 4;
+          uint64_t a2 = ma;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a2 += e < ei ? m[e] : 0ull;
+          sh.u32a = prefix | ((uint32_t)dsel << shift);
+          sh.u64a = low < 256 ? a2 : above;
+        }
       }
-      sh.u32a = found ? (prefix | (dsel << shift)) : 0xffffffffu;
-      sh.u32b = need;
-      sh.u64a = above;
     }
     __syncthreads();
     if (sh.u32a == 0xffffffffu) return 0u;
     prefix = sh.u32a;
-    need = sh.u32b;
-    above = sh.u64a;
+    if (!by_mass) need = sh.u32b;
+    if (by_mass) above = sh.u64a;
     pmask |= 255u << shift;
     __syncthreads();
   }
@@ -201,33 +243,40 @@ struct SampleArgs {
   int32_t vec;  // rows are 16-byte aligned: 16-byte loads
 };
 
-__global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
-  __shared__ SampleShared sh;
-  const int r = blockIdx.x;
-  const int src = a.rows ? a.rows[r] : r;
-  if (src < 0 || src >= a.nrows) {  // a row index outside probs: no draw
+// Draw for output row r from the values p[0, V): thresholds by radix select, then the inverse CDF
+// in order. idx (optional) maps a position in p to the vocabulary index (p is then the row's
+// candidate list, ascending in vocabulary index). npos: the row's count of p > 0 (-1: count it
+// here over p). row_tot: the row's total mass for top_p (0: sum it here over p). Candidate lists
+// hold every element at or above the threshold being searched, so the counts and masses that
+// decide it are the same as over the whole row.
+__device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, int V, bool vec, const SampleArgs& a, int r,
+                           int64_t npos, uint64_t row_tot, SampleShared& sh) {
+  if (V == 0) {  // nothing to draw from (an empty candidate list)
     if (threadIdx.x == 0) a.out[r] = -1;
     return;
   }
-  const float* p = a.probs + (int64_t)src * a.stride;
-  const int V = a.V;
-  const bool vec = a.vec != 0;
   // lower bound on kept keys (1 = every p > 0)
   uint32_t lo = 1u;
   if (a.mode == 2 || a.mode == 4) {
     const int32_t k = a.top_k ? a.top_k[r] : a.top_k_s;
     if (k > 0 && k < V) {
-      uint32_t npos = 0;
-      for_row(p, V, vec, [&](int, float x) { npos += prob_key(x) != 0; });
-      npos = (uint32_t)block_sum_u64(npos, sh);
-      if ((uint32_t)k < npos) lo = max(1u, radix_threshold(p, V, vec, 1u, false, (uint32_t)k, 0.0, sh));
+      if (npos < 0) {
+        uint32_t c = 0;
+        for_row(p, V, vec, [&](int, float x) { c += prob_key(x) != 0; });
+        npos = (int64_t)block_sum_u64(c, sh);
+      }
+      if ((int64_t)k < npos) lo = max(1u, radix_threshold(p, V, vec, 1u, false, (uint32_t)k, 0.0, sh));
     }
   }
   if (a.mode == 1 || a.mode == 4) {
     const float tp = a.top_p ? a.top_p[r] : a.top_p_s;
     uint64_t tot = 0;
-    for_row(p, V, vec, [&](int, float x) { if (prob_key(x) >= lo) tot += prob_mass(x); });
-    tot = block_sum_u64(tot, sh);
+    if (a.mode == 1 && row_tot) {
+      tot = row_tot;
+    } else {
+      for_row(p, V, vec, [&](int, float x) { if (prob_key(x) >= lo) tot += prob_mass(x); });
+      tot = block_sum_u64(tot, sh);
+    }
     const uint32_t t = radix_threshold(p, V, vec, lo, true, 0u, (double)tp * (double)tot, sh);
     if (t > lo) lo = t;
   }
@@ -244,65 +293,348 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
     if (a.mode == 3 && !((double)x >= mthr)) return 0ull;
     return prob_mass(x);
   };
-  uint64_t tot = 0;
-  int last = -1;
-  for_row(p, V, vec, [&](int i, float x) {
-    const uint64_t m = kept_mass(x);
-    tot += m;
-    if (m) last = max(last, i);
-  });
-  tot = block_sum_u64(tot, sh);
-  {
-    const int lane = threadIdx.x & 63;
+  // kept-mass pass: the sums of chunks of whole 4096-element tiles (at most 256 chunks), so that
+  // the inverse CDF scans only the chunk where the target falls
+  constexpr int kTile = 4 * kSampThreads;
+  const int ntiles = (V + kTile - 1) / kTile;
+  const int tpc = (ntiles + 255) / 256;  // tiles per chunk
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int i = threadIdx.x; i < 256; i += kSampThreads) sh.mass[i] = 0;
+  __syncthreads();
+  auto load4 = [&](int i0, float (&x)[4]) {
+    if (vec && i0 + 3 < V) {
+      const float4 v = *reinterpret_cast<const float4*>(p + i0);
+      x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+    } else {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) last = max(last, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, last));
-    __syncthreads();
-    if (lane == 0) sh.wsum[threadIdx.x >> 6] = (uint64_t)(int64_t)last;
-    __syncthreads();
-    for (int i = 0; i < kSampWaves; ++i) last = max(last, (int)(int64_t)sh.wsum[i]);
+      for (int e = 0; e < 4; ++e) x[e] = i0 + e < V ? p[i0 + e] : 0.f;
+    }
+  };
+  int last = -1;
+  uint64_t acc = 0;
+  for (int t0 = 0; t0 < ntiles; t0 += 4) {  // four 16-byte loads in flight
+    float x[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (t0 + u < ntiles) load4((t0 + u) * kTile + 4 * threadIdx.x, x[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = t0 + u;
+      if (t >= ntiles) break;
+      const int i0 = t * kTile + 4 * threadIdx.x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t m = kept_mass(x[u][e]);
+        acc += m;
+        if (m) last = max(last, i0 + e);
+      }
+      if ((t + 1) % tpc == 0 || t == ntiles - 1) {  // chunk t / tpc ends here
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) acc += shfl_u64(acc, lane ^ o);
+        if (lane == 0 && acc) atomicAdd((unsigned long long*)&sh.mass[t / tpc], (unsigned long long)acc);
+        acc = 0;
+      }
+    }
   }
-  const double u = a.uniforms ? a.uniforms[r] : philox_uniform(a.seed, a.offset, (uint32_t)r);
-  const double target = u * (double)tot;
-  // inverse CDF: tiles of 4 consecutive elements per thread, block-scanned in index order
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) last = max(last, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, last));
+  if (lane == 0) sh.wsum[w] = (uint64_t)(int64_t)last;
   if (threadIdx.x == 0) sh.pick = -1;
   __syncthreads();
-  uint64_t run = 0;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int base = 0; base < V; base += 4 * kSampThreads) {
-    const int i0 = base + 4 * threadIdx.x;
-    uint64_t m[4];
+  for (int i = 0; i < kSampWaves; ++i) last = max(last, (int)(int64_t)sh.wsum[i]);
+  // wave 0: the total, the target and the first chunk whose inclusive prefix exceeds it
+  if (threadIdx.x < 64) {
+    uint64_t c[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) m[e] = i0 + e < V ? kept_mass(p[i0 + e]) : 0ull;
-    const uint64_t mine = m[0] + m[1] + m[2] + m[3];
-    // inclusive scan of `mine` over the block
-    uint64_t incl = mine;
+    for (int e = 0; e < 4; ++e) c[e] = sh.mass[4 * lane + e];
+    const uint64_t lm = c[0] + c[1] + c[2] + c[3];
+    uint64_t incl = lm;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const uint64_t y = shfl_u64(incl, lane >= o ? lane - o : lane);
       if (lane >= o) incl += y;
     }
-    __syncthreads();
-    if (lane == 63) sh.wsum[w] = incl;
-    __syncthreads();
-    uint64_t before = run, tile = 0;
-    for (int i = 0; i < kSampWaves; ++i) {
-      if (i < w) before += sh.wsum[i];
-      tile += sh.wsum[i];
-    }
-    const uint64_t excl = before + incl - mine;
-    if (mine && (double)(excl + mine) > target && !((double)excl > target)) {
-      uint64_t c = excl;
+    const uint64_t tot = shfl_u64(incl, 63);
+    const double u = a.uniforms ? a.uniforms[r] : philox_uniform(a.seed, a.offset, (uint32_t)r);
+    const double target = u * (double)tot;
+    uint64_t run = incl - lm;
+    int first = 256;
+    uint64_t first_excl = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        c += m[e];
-        if (m[e] && (double)c > target) { sh.pick = i0 + e; break; }
+    for (int e = 0; e < 4; ++e) {
+      if (first == 256 && c[e] && (double)(run + c[e]) > target) { first = 4 * lane + e; first_excl = run; }
+      run += c[e];
+    }
+    int f = first;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) f = min(f, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, f));
+    if (first == f && f < 256) {
+      sh.u32a = (uint32_t)f;
+      sh.u64a = first_excl;
+    }
+    if (lane == 0) {
+      if (f == 256) sh.u32a = 0xffffffffu;
+      sh.u64b = __builtin_bit_cast(uint64_t, target);
+    }
+  }
+  __syncthreads();
+  // inverse CDF inside the chunk: tiles of 4 consecutive elements per thread, block-scanned in
+  // index order
+  if (sh.u32a != 0xffffffffu) {
+    const int chunk = (int)sh.u32a;
+    const double target = __builtin_bit_cast(double, sh.u64b);
+    uint64_t run = sh.u64a;
+    const int end = min(V, (chunk + 1) * tpc * kTile);
+    for (int base = chunk * tpc * kTile; base < end; base += kTile) {
+      const int i0 = base + 4 * threadIdx.x;
+      float x[4];
+      load4(i0, x);
+      uint64_t m[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) m[e] = kept_mass(x[e]);
+      const uint64_t mine = m[0] + m[1] + m[2] + m[3];
+      // inclusive scan of `mine` over the block
+      uint64_t incl = mine;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t y = shfl_u64(incl, lane >= o ? lane - o : lane);
+        if (lane >= o) incl += y;
+      }
+      __syncthreads();
+      if (lane == 63) sh.wsum[w] = incl;
+      __syncthreads();
+      uint64_t before = run, tile = 0;
+      for (int i = 0; i < kSampWaves; ++i) {
+        if (i < w) before += sh.wsum[i];
+        tile += sh.wsum[i];
+      }
+      const uint64_t excl = before + incl - mine;
+      if (mine && (double)(excl + mine) > target && !((double)excl > target)) {
+        uint64_t c = excl;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          c += m[e];
+          if (m[e] && (double)c > target) { sh.pick = i0 + e; break; }
+        }
+      }
+      __syncthreads();
+      if (sh.pick >= 0) break;
+      run += tile;
+    }
+  }
+  if (threadIdx.x == 0) {
+    const int j = sh.pick >= 0 ? sh.pick : last;
+    a.out[r] = (idx && j >= 0) ? (int32_t)idx[j] : j;
+  }
+}
+
+// Candidate lists. Pass A keeps each thread's two largest keys (2048 elements of the row, its
+// largest among them) with the row's count of p > 0 and, for top_p, its total mass. Any subset's
+// k-th largest key is at most the row's, and any subset whose mass reaches the top-p threshold
+// bounds the row's top-p threshold from below the same way (the subset's mass above a key is at
+// most the row's), so the subset's own thresholds are floors for the row's. Pass B copies every
+// element at or above the floor into LDS in vocabulary order (each wave owns a contiguous
+// segment of the row and appends with ballots), and the exact selection and the draw then run
+// over that list. No floor (k above the subset's count, a subset mass below the threshold), or
+// more than kWaveCands candidates in some wave's segment, sends the row to the direct passes.
+constexpr int kWaveCands = 512;
+constexpr int kCands = kWaveCands * kSampWaves;
+
+struct alignas(16) CandShared {
+  float val[kCands];  // the per-thread tops (pass A), then the candidates
+  uint32_t idx[kCands];
+  int32_t wn[kSampWaves];
+};
+
+// Pass A of the candidate lists: each thread's two largest keys, stored as floats at
+// tops[2 thread], tops[2 thread + 1]; count = the thread's count of p > 0, mass = its mass (when
+// with_mass). Returns the mass of the two stored keys.
+constexpr int kTops = 2 * kSampThreads;
+__device__ __forceinline__ uint64_t thread_tops(const float* p, int V, bool vec, bool with_mass, float* tops,
+                                                uint32_t& count, uint64_t& mass) {
+  uint32_t t1 = 0u, t2 = 0u, c = 0;
+  uint64_t m = 0;
+  for_row(p, V, vec, [&](int, float x) {
+    const uint32_t key = prob_key(x);
+    c += key != 0;
+    if (with_mass) m += prob_mass(x);
+    t2 = max(t2, min(t1, key));
+    t1 = max(t1, key);
+  });
+  count = c;
+  mass = m;
+  tops[2 * threadIdx.x] = __builtin_bit_cast(float, t1);
+  tops[2 * threadIdx.x + 1] = __builtin_bit_cast(float, t2);
+  return prob_mass(__builtin_bit_cast(float, t1)) + prob_mass(__builtin_bit_cast(float, t2));
+}
+
+// Appends this wave's candidates (pred(i, x)) to val/idx[w * kWaveCands ...] in index order and
+// returns their count (which may exceed kWaveCands; only the first kWaveCands are stored).
+template <typename P>
+__device__ int compact_segment(const float* p, int V, bool vec, P&& pred, CandShared& cs) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  float* val = cs.val + w * kWaveCands;
+  uint32_t* idx = cs.idx + w * kWaveCands;
+  int n = 0;
+  auto emit = [&](uint32_t bits, int i0, const float* x, int stride) {
+    const uint32_t c = __builtin_popcount(bits);
+    if (__builtin_amdgcn_ballot_w64(c != 0) == 0) return;
+    const uint64_t b0 = __builtin_amdgcn_ballot_w64(c & 1u), b1 = __builtin_amdgcn_ballot_w64(c & 2u),
+                   b2 = __builtin_amdgcn_ballot_w64(c & 4u);
+    int pos = n + __builtin_popcountll(b0 & lt) + 2 * __builtin_popcountll(b1 & lt) +
+              4 * __builtin_popcountll(b2 & lt);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (bits >> e & 1u) {
+        if (pos < kWaveCands) { val[pos] = x[e]; idx[pos] = (uint32_t)(i0 + e * stride); }
+        ++pos;
+      }
+    n += __builtin_popcountll(b0) + 2 * __builtin_popcountll(b1) + 4 * __builtin_popcountll(b2);
+  };
+  if (vec) {
+    const int nv = V >> 2;
+    const int seg = (nv + kSampWaves - 1) / kSampWaves;
+    const int v0 = w * seg, v1 = min(nv, v0 + seg);
+    int vb = v0;  // wave-uniform position: every lane runs the same trips (ballots need them all)
+    for (; vb + 4 * 64 <= v1; vb += 4 * 64) {
+      float4 x[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) x[k] = *reinterpret_cast<const float4*>(p + 4 * (vb + lane + 64 * k));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float xe[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+        const int i0 = 4 * (vb + lane + 64 * k);
+        uint32_t bits = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bits |= (uint32_t)pred(i0 + e, xe[e]) << e;
+        emit(bits, i0, xe, 1);
+      }
+    }
+    for (; vb < v1; vb += 64) {
+      const int v = vb + lane;
+      float xe[4] = {0.f, 0.f, 0.f, 0.f};
+      uint32_t bits = 0;
+      if (v < v1) {
+        const float4 x = *reinterpret_cast<const float4*>(p + 4 * v);
+        xe[0] = x.x; xe[1] = x.y; xe[2] = x.z; xe[3] = x.w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bits |= (uint32_t)pred(4 * v + e, xe[e]) << e;
+      }
+      emit(bits, 4 * v, xe, 1);
+    }
+    if (w == kSampWaves - 1) {  // the last < 4 elements belong to the last segment
+      const int i = 4 * nv + lane;
+      float xe[4] = {i < V ? p[i] : 0.f, 0.f, 0.f, 0.f};
+      emit(i < V ? (uint32_t)pred(i, xe[0]) : 0u, i, xe, 0);
+    }
+  } else {
+    const int seg = (V + kSampWaves - 1) / kSampWaves;
+    const int i1 = min(V, w * seg + seg);
+    for (int i = w * seg + lane; i - lane < i1; i += 64) {
+      float xe[4] = {i < i1 ? p[i] : 0.f, 0.f, 0.f, 0.f};
+      emit(i < i1 ? (uint32_t)pred(i, xe[0]) : 0u, i, xe, 0);
+    }
+  }
+  return n;
+}
+
+__global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
+  __shared__ SampleShared sh;
+  __shared__ CandShared cs;
+  const int r = blockIdx.x;
+  const int src = a.rows ? a.rows[r] : r;
+  if (src < 0 || src >= a.nrows) {  // a row index outside probs: no draw
+    if (threadIdx.x == 0) a.out[r] = -1;
+    return;
+  }
+  const float* p = a.probs + (int64_t)src * a.stride;
+  const int V = a.V;
+  const bool vec = a.vec != 0;
+  const int mode = a.mode;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int32_t k = (mode == 2 || mode == 4) ? (a.top_k ? a.top_k[r] : a.top_k_s) : 0;
+  // what the selection runs over: the row (direct passes) or its candidate list
+  const float* sp = p;
+  const uint32_t* sidx = nullptr;
+  int sV = V;
+  bool svec = vec;
+  int64_t npos = -1;
+  uint64_t row_tot = 0;
+  // plain sampling, and top_k with k outside (0, V), keep every p > 0: no candidate list
+  if (!(mode == 0 || ((mode == 2 || mode == 4) && !(k > 0 && k < V)))) {
+    // pass A
+    bool lists = true;
+    uint32_t cand_lo = 1u;  // candidates: key >= cand_lo (top_k, top_p) or x >= mthr (min_p)
+    double mthr = 0.0;
+    if (mode == 3) {
+      uint32_t mk = 0;
+      for_row(p, V, vec, [&](int, float x) { mk = max(mk, prob_key(x)); });
+      mk = block_max_u32(mk, sh);
+      mthr = (double)(a.min_p ? a.min_p[r] : a.min_p_s) * (double)__builtin_bit_cast(float, mk);
+    } else {
+      const bool by_mass = mode == 1;
+      uint32_t c = 0;
+      uint64_t m = 0;
+      uint64_t tm = thread_tops(p, V, vec, by_mass, cs.val, c, m);
+      npos = (int64_t)block_sum_u64(c, sh);
+      if (by_mass) {
+        row_tot = block_sum_u64(m, sh);
+        tm = block_sum_u64(tm, sh);
+        const double thr = (double)(a.top_p ? a.top_p[r] : a.top_p_s) * (double)row_tot;
+        // a floor needs the subset's mass to reach the threshold
+        cand_lo = (double)tm < thr ? 0u : radix_threshold(cs.val, kTops, true, 1u, true, 0u, thr, sh);
+      } else if ((int64_t)k < npos) {
+        cand_lo = radix_threshold(cs.val, kTops, true, 1u, false, (uint32_t)k, 0.0, sh);
+      } else {
+        cand_lo = 1u;  // k >= the count of p > 0: top_k keeps everything
+      }
+      lists = cand_lo > 1u;
+      __syncthreads();  // the tops are dead from here: their memory holds the candidates
+    }
+    if (lists) {
+      // pass B
+      const int n = compact_segment(p, V, vec, [&](int, float x) {
+        return mode == 3 ? (prob_key(x) != 0 && (double)x >= mthr) : prob_key(x) >= cand_lo;
+      }, cs);
+      if (lane == 0) cs.wn[w] = n;
+      __syncthreads();
+      int total = 0;
+      bool over = false;
+      for (int i = 0; i < kSampWaves; ++i) {
+        over |= cs.wn[i] > kWaveCands;
+        total += cs.wn[i];
+      }
+      // with too many candidates in some segment, the direct passes run over the row
+      if (!over) {
+        // close the gaps between the segments' lists (moves go to lower slots: read, then write)
+        constexpr int J = kCands / kSampThreads;
+        float mv[J];
+        uint32_t mi[J];
+        int md[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          const int s = threadIdx.x + j * kSampThreads;
+          const int sw = s / kWaveCands, so = s % kWaveCands;
+          int base = 0;
+          for (int i = 0; i < sw; ++i) base += cs.wn[i];
+          md[j] = so < cs.wn[sw] ? base + so : -1;
+          mv[j] = cs.val[s];
+          mi[j] = cs.idx[s];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+          if (md[j] >= 0) { cs.val[md[j]] = mv[j]; cs.idx[md[j]] = mi[j]; }
+        sp = cs.val;
+        sidx = cs.idx;
+        sV = total;
+        svec = true;
       }
     }
     __syncthreads();
-    if (sh.pick >= 0) break;
-    run += tile;
   }
-  if (threadIdx.x == 0) a.out[r] = sh.pick >= 0 ? sh.pick : last;
+  sample_row(sp, sidx, sV, svec, a, r, npos, row_tot, sh);
 }
 
 // safe_scaled_softmax: probs = softmax(logits / T) per row, or the one-hot of the first maximum

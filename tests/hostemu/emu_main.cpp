@@ -482,13 +482,20 @@ static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
 // ---------------------------------------------------------------------------- sampling
 // Probabilities are multiples of 2^-30 (exact in the kernel's 2^-40 fixed point and in float64),
 // so kept sets and draws must match the oracle exactly; ties are forced in some rows.
-static void case_sample(int64_t B, int64_t V, int mode, bool row_map) {
-  printf("sample B=%lld V=%lld mode=%d rows=%d\n", (long long)B, (long long)V, mode, (int)row_map);
+// peaked: p = softmax of N(0, 3) logits (a few dominant tokens, as after an LM head) with k up to
+// 64, so the candidate lists are short; otherwise near-uniform rows whose lists can overflow.
+static void case_sample(int64_t B, int64_t V, int mode, bool row_map, bool peaked = false) {
+  printf("sample B=%lld V=%lld mode=%d rows=%d peaked=%d\n", (long long)B, (long long)V, mode, (int)row_map,
+         (int)peaked);
   Buf<float> probs(B * V);
   std::uniform_int_distribution<int> dq(0, 1 << 12);
+  std::normal_distribution<double> dn(0.0, 3.0);
   for (int64_t r = 0; r < B; ++r) {
     double tot = 0;
-    for (int64_t i = 0; i < V; ++i) { probs[r * V + i] = (float)dq(rng); tot += probs[r * V + i]; }
+    for (int64_t i = 0; i < V; ++i) {
+      probs[r * V + i] = peaked ? (float)(exp(dn(rng)) * 1024.0) : (float)dq(rng);
+      tot += probs[r * V + i];
+    }
     if (r % 3 == 1) for (int64_t i = 0; i < V; i += 7) probs[r * V + i] = probs[r * V];  // ties
     if (r % 4 == 2) probs[r * V + 3] = 0.f;
     for (int64_t i = 0; i < V; ++i) probs[r * V + i] = (float)(ldexp(floor(probs[r * V + i] / tot * 1073741824.0), -30));
@@ -497,7 +504,7 @@ static void case_sample(int64_t B, int64_t V, int mode, bool row_map) {
   Buf<float> topp(B), minp(B);
   Buf<double> u(B);
   std::uniform_real_distribution<double> du(0.0, 1.0);
-  std::uniform_int_distribution<int> dk(1, (int)V + 2);
+  std::uniform_int_distribution<int> dk(1, peaked ? 64 : (int)V + 2);
   for (int64_t r = 0; r < B; ++r) {
     rows[r] = row_map ? (int32_t)((r * 5 + 1) % B) : (int32_t)r;
     topk[r] = r == 0 ? 0 : dk(rng);
@@ -626,6 +633,11 @@ int main(int argc, char** argv) {
   if (all || c == "sample") {
     for (int mode = 0; mode <= 4; ++mode) case_sample(5, 301, mode, mode == 4);
     case_sample(3, 4099, 4, false);  // several 4096-element scan tiles
+    for (int mode = 1; mode <= 4; ++mode) case_sample(4, 20000, mode, false, true);  // candidate lists
+    case_sample(3, 20003, 4, false, true);  // candidate lists, scalar loads
+    case_sample(3, 40000, 1, false);        // top_p lists that overflow: direct passes
+    case_sample(1, 1100003, 0, false);      // more than 256 tiles: chunks of several tiles
+    case_sample(1, 1100000, 3, false);
     case_softmax(3, 1000, false);
     case_softmax(3, 777, true);
   }

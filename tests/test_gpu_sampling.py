@@ -67,6 +67,22 @@ def test_sample_exact_vs_oracle(dev, mode, V):
     assert kept[np.arange(B), got].all()
 
 
+@pytest.mark.parametrize("mode", list(SAMPLERS))
+def test_sample_long_rows(dev, mode):
+    """Rows of more than 256 tiles of 4096 (the draw's chunks then span several tiles), one with
+    a length that is not a multiple of 4 (scalar loads)."""
+    for V in (1_100_000, 1_048_583):
+        print(f"sample mode={mode} V={V}", flush=True)
+        B = 4
+        probs = _grid_probs(B, V, V + 1)
+        prm = _params(B, V, V + 2)
+        dp = {k: v.to(dev) for k, v in prm.items()}
+        got = _call(mode, probs.to(dev), dp, uniforms=dp["u"]).cpu().numpy()
+        want, _ = oracle.sample(probs.numpy(), mode, prm["u"].numpy(), top_k=prm["top_k"].numpy(),
+                                top_p=prm["top_p"].numpy(), min_p=prm["min_p"].numpy())
+        assert (got == want).all(), f"V={V}: {got} vs {want}"
+
+
 def test_sample_scalar_params_and_row_indices(dev):
     B, V = 16, 1000
     probs = _grid_probs(B, V, 5)
