@@ -638,9 +638,10 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
 }
 
 // safe_scaled_softmax: probs = softmax(logits / T) per row, or the one-hot of the first maximum
-// when T < greedy_threshold. Two passes over the row: (max, first argmax, sum of exp2 relative to
-// a running max) with 16-byte loads, then the normalised write; fp32 math in the exp2 domain,
-// output in the logits' dtype.
+// when T < greedy_threshold; fp32 math in the exp2 domain, output in the logits' dtype. This
+// streaming kernel serves rows too long (or not aligned) for the register-resident one below:
+// two passes over the row, (max, first argmax, sum of exp2 relative to a running max) with
+// 16-byte loads, then the normalised write.
 template <bool BF16>
 struct RowIO {
   static constexpr int E = BF16 ? 8 : 4;  // elements per 16-byte vector
@@ -752,6 +753,138 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_kernel(const void
     IO::put(orow, i, greedy_row ? (i == A ? 1.f : 0.f) : __builtin_amdgcn_exp2f(fmaf(IO::get(row, i), c, -mc)) * inv);
 }
 
+// safe_scaled_softmax with the row held in registers (NV 16-byte vectors per thread, the row's
+// last V % E elements one per thread): one read and one write of the row. The maximum first (and,
+// for greedy rows, its first index), then the sum of exp2(x*c - max*c), then the write from
+// registers.
+__device__ __forceinline__ float block_max_f(float v, float* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1)
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, __builtin_bit_cast(int, v))));
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int i = 1; i < kSampWaves; ++i) t = fmaxf(t, red[i]);
+  return t;
+}
+__device__ __forceinline__ float block_sum_f(float v, float* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, __builtin_bit_cast(int, v)));
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < kSampWaves; ++i) t += red[i];
+  return t;
+}
+__device__ __forceinline__ int block_min_i(int v, float* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = min(v, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, v));
+  __syncthreads();
+  if (lane == 0) red[w] = __builtin_bit_cast(float, v);
+  __syncthreads();
+  int t = __builtin_bit_cast(int, red[0]);
+#pragma unroll
+  for (int i = 1; i < kSampWaves; ++i) t = min(t, __builtin_bit_cast(int, red[i]));
+  return t;
+}
+
+template <bool BF16, int NV>
+__global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
+    const void* __restrict__ logits, int64_t stride, int V, const float* __restrict__ temps, float greedy,
+    void* __restrict__ out, int64_t out_stride) {
+  using IO = RowIO<BF16>;
+  constexpr int E = IO::E;
+  __shared__ float red[kSampWaves];
+  const int r = blockIdx.x;
+  const char* row = reinterpret_cast<const char*>(logits) + (int64_t)r * stride * (BF16 ? 2 : 4);
+  char* orow = reinterpret_cast<char*>(out) + (int64_t)r * out_stride * (BF16 ? 2 : 4);
+  const int nv = V / E;
+  uint4 d[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int v = threadIdx.x + j * kSampThreads;
+    d[j] = v < nv ? ld16(row + (int64_t)v * 16) : make_uint4(0u, 0u, 0u, 0u);
+  }
+  const int it = nv * E + threadIdx.x;  // this thread's tail element, if any
+  const float xt = it < V ? IO::get(row, it) : -INFINITY;
+  const float T = temps[r];
+  const bool greedy_row = T < greedy;
+  const float c = greedy_row ? 1.f : 1.4426950408889634f / T;
+  auto unpack = [&](const uint4& q, float (&x)[E]) {
+    if (BF16) {
+      unpack8(q, x);
+    } else {
+      x[0] = __uint_as_float(q.x); x[1] = __uint_as_float(q.y); x[2] = __uint_as_float(q.z); x[3] = __uint_as_float(q.w);
+    }
+  };
+  float mx = xt;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    if (threadIdx.x + j * kSampThreads >= nv) break;
+    float x[E];
+    unpack(d[j], x);
+#pragma unroll
+    for (int e = 0; e < E; ++e) mx = fmaxf(mx, x[e]);
+  }
+  const float M = block_max_f(mx, red);
+  if (greedy_row) {
+    int am = 0x7fffffff;  // first index holding the maximum
+#pragma unroll
+    for (int j = NV - 1; j >= 0; --j) {
+      const int v = threadIdx.x + j * kSampThreads;
+      if (v >= nv) continue;
+      float x[E];
+      unpack(d[j], x);
+#pragma unroll
+      for (int e = E - 1; e >= 0; --e)
+        if (x[e] == M) am = v * E + e;
+    }
+    if (it < V && xt == M) am = min(am, it);
+    const int A = block_min_i(am, red);
+    float one[E];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int v = threadIdx.x + j * kSampThreads;
+      if (v >= nv) break;
+#pragma unroll
+      for (int e = 0; e < E; ++e) one[e] = v * E + e == A ? 1.f : 0.f;
+      IO::store(orow, (int64_t)v * E, one);
+    }
+    if (it < V) IO::put(orow, it, it == A ? 1.f : 0.f);
+    return;
+  }
+  const float mc = M * c;
+  float s = it < V ? __builtin_amdgcn_exp2f(fmaf(xt, c, -mc)) : 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    if (threadIdx.x + j * kSampThreads >= nv) break;
+    float x[E];
+    unpack(d[j], x);
+#pragma unroll
+    for (int e = 0; e < E; ++e) s += __builtin_amdgcn_exp2f(fmaf(x[e], c, -mc));
+  }
+  const float inv = 1.f / block_sum_f(s, red);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int v = threadIdx.x + j * kSampThreads;
+    if (v >= nv) break;
+    float x[E];
+    unpack(d[j], x);
+#pragma unroll
+    for (int e = 0; e < E; ++e) x[e] = __builtin_amdgcn_exp2f(fmaf(x[e], c, -mc)) * inv;
+    IO::store(orow, (int64_t)v * E, x);
+  }
+  if (it < V) IO::put(orow, it, __builtin_amdgcn_exp2f(fmaf(xt, c, -mc)) * inv);
+}
+
 }  // namespace pie
 
 using namespace pie;
@@ -788,11 +921,29 @@ extern "C" int pie_hip_scaled_softmax(const void* logits, int32_t is_bf16, int64
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t e = is_bf16 ? 8 : 4;  // elements per 16-byte vector
   const int vec = aligned16(logits) && aligned16(out) && stride % e == 0 && out_stride % e == 0;
-  if (is_bf16)
-    hipLaunchKernelGGL(scaled_softmax_kernel<true>, dim3((unsigned)batch), dim3(kSampThreads), 0, st, logits,
-                       stride, (int)vocab, temperatures, greedy_threshold, out, out_stride, vec);
-  else
-    hipLaunchKernelGGL(scaled_softmax_kernel<false>, dim3((unsigned)batch), dim3(kSampThreads), 0, st, logits,
-                       stride, (int)vocab, temperatures, greedy_threshold, out, out_stride, vec);
+  // rows of up to 20 vectors per thread stay in registers (bf16: 163,840 entries; fp32: 81,920)
+  const int64_t per_thread = (vocab / e + kSampThreads - 1) / kSampThreads;
+  const dim3 grid((unsigned)batch), block(kSampThreads);
+#define PIE_SOFTMAX_RESIDENT(BF, NV)                                                                      \
+  hipLaunchKernelGGL((scaled_softmax_resident_kernel<BF, NV>), grid, block, 0, st, logits, stride, (int)vocab, \
+                     temperatures, greedy_threshold, out, out_stride)
+  if (vec && per_thread <= 20) {
+    if (is_bf16) {
+      if (per_thread <= 8) PIE_SOFTMAX_RESIDENT(true, 8);
+      else if (per_thread <= 16) PIE_SOFTMAX_RESIDENT(true, 16);
+      else PIE_SOFTMAX_RESIDENT(true, 20);
+    } else {
+      if (per_thread <= 8) PIE_SOFTMAX_RESIDENT(false, 8);
+      else if (per_thread <= 16) PIE_SOFTMAX_RESIDENT(false, 16);
+      else PIE_SOFTMAX_RESIDENT(false, 20);
+    }
+  } else if (is_bf16) {
+    hipLaunchKernelGGL(scaled_softmax_kernel<true>, grid, block, 0, st, logits, stride, (int)vocab, temperatures,
+                       greedy_threshold, out, out_stride, vec);
+  } else {
+    hipLaunchKernelGGL(scaled_softmax_kernel<false>, grid, block, 0, st, logits, stride, (int)vocab, temperatures,
+                       greedy_threshold, out, out_stride, vec);
+  }
+#undef PIE_SOFTMAX_RESIDENT
   return check_launch("scaled_softmax");
 }

@@ -640,6 +640,7 @@ int main(int argc, char** argv) {
     case_sample(1, 1100000, 3, false);
     case_softmax(3, 1000, false);
     case_softmax(3, 777, true);
+    case_softmax(2, 70003, false);   // rows not 16-byte aligned: the streaming kernel
   }
   if (all || c == "prefill") {
     case_attn_prefill(3, 8, 2, 128, 16, 40, 45, 1);   // causal, chunked prefill over cached context

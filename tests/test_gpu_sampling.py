@@ -148,14 +148,23 @@ def test_sample_full_vocab_kept_sets(dev, V):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_safe_scaled_softmax(dev, dtype):
-    B, V = 8, 128256
+@pytest.mark.parametrize("V,pad", [(128256, 0), (151936, 0), (50257, 7), (70001, 3), (200003, 0)])
+def test_safe_scaled_softmax(dev, dtype, V, pad):
+    """Row lengths that run the register-resident kernel at each of its sizes (with and without
+    tail elements, padded row strides) and the streaming one (200003: too long for registers;
+    unpadded odd lengths: rows not 16-byte aligned)."""
+    print(f"safe_scaled_softmax V={V} pad={pad} {dtype}", flush=True)
+    B = 8
     g = torch.Generator().manual_seed(21)
-    logits = (torch.randn(B, V, generator=g) * 4).to(dtype)
+    full = (torch.randn(B, V + pad, generator=g) * 4)
+    full[0, 5] = full[0, V - 1] = full[0].max() + 1  # tied maxima: the first one wins
+    full = full.to(dtype)
+    logits = full[:, :V]
     temps = torch.tensor([0.0, 1e-6, 0.3, 0.7, 1.0, 1.0, 1.7, 5.0])
-    got = sampling.safe_scaled_softmax(logits.to(dev), temps.to(dev))
+    got = sampling.safe_scaled_softmax(full.to(dev)[:, :V], temps.to(dev))
     want = oracle.scaled_softmax(logits.float().numpy(), temps.numpy())
     gotf = got.float().cpu().numpy().astype(np.float64)
+    assert gotf[0, 5] == 1.0, "first of tied maxima"
     assert (gotf[:2] == want[:2]).all(), "greedy rows are exact one-hots"
     rel = 2 ** -7 if dtype == torch.bfloat16 else 1e-5
     bad = np.abs(gotf - want) > rel * np.abs(want) + 1e-30
