@@ -67,7 +67,7 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 // measured fastest on MI355X in steady state (back-to-back launches over buffers larger than
 // the last-level cache, so a kernel pays for draining its own writes): non-temporal stores for
 // every large streamed output (e.g. SiLU-and-mul 6.47 vs 6.13 TB/s, embedding 6.27 vs
-// 5.23 TB/s), cached loads and stores for the RMSNorm rows.
+// 5.23 TB/s), non-temporal loads and stores for large RMSNorm row lists (row_ld / row_st below).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_nt(const void* p) {
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
@@ -79,6 +79,34 @@ __device__ __forceinline__ void st_nt(void* p, const uint4& v) {
 }
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ void st16(void* p, const uint4& v) { *reinterpret_cast<uint4*>(p) = v; }
+// 16-byte vector i of a row whose base address is the same in every lane of the wave, through a
+// buffer resource: with NT the access carries the non-temporal cache policy as an operand of the
+// instruction, where compiler passes cannot drop it (LLVM's loop-invariant code motion drops the
+// !nontemporal metadata of plain stores in some loop shapes).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* row_base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(row_base);  // the same in every lane: say so
+  const uint64_t u = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(a >> 32)) << 32) |
+                     (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(u), 0, 0x7fffffff, 0x00020000);
+}
+template <bool NT>
+__device__ __forceinline__ uint4 row_ld(const void* row_base, int i) {
+  if constexpr (NT) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(row_rsrc(row_base), i * 16, 0, 2);
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return ld16(reinterpret_cast<const char*>(row_base) + (int64_t)i * 16);
+  }
+}
+template <bool NT>
+__device__ __forceinline__ void row_st(void* row_base, int i, const uint4& v) {
+  if constexpr (NT) {
+    const u32x4_t w = {v.x, v.y, v.z, v.w};
+    __builtin_amdgcn_raw_buffer_store_b128(w, row_rsrc(row_base), i * 16, 0, 2);
+  } else {
+    st16(reinterpret_cast<char*>(row_base) + (int64_t)i * 16, v);
+  }
+}
 
 // ---------------------------------------------------------------- reductions (device)
 // Sum over each 16-lane DPP row, result broadcast to all 16 lanes (row_ror 8,4,2,1).

@@ -143,7 +143,7 @@ constexpr int kRowsPerGroup = 1;
 // of wave g in the group owns vectors j*64*W + g*64 + l. W = 1 for long row lists (no barrier);
 // W > 1 spreads short lists (decode batches) over the chip, combining the W partial sums of
 // squares through LDS in a fixed order. The weight row stays in registers across rows.
-template <int VPL, int RPG, bool ADD, bool GEMMA>
+template <int VPL, int RPG, bool ADD, bool GEMMA, bool NT>
 __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
   __shared__ acc_t<GEMMA> part[RPG][8];
   const RowSet& s = a.set[0];
@@ -154,9 +154,7 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
   const int vstep = 64 * W;
   const int v0 = gsub * 64 + lane;
 
-  uint4 wv[VPL];
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) wv[j] = wprep8<GEMMA>(ld16(s.w + (int64_t)(v0 + j * vstep) * 8));
+  uint4 wv[VPL];  // loaded after each row's inputs are in flight (a hit in L2 after the first row)
 
   // A group handles RPG rows at once (rows base+grp, base+grp+G, ...): all their loads are in
   // flight before the first reduction. Block-uniform trip count: every thread reaches every
@@ -175,12 +173,17 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
       if (live[k]) row_offsets(s, r, oi, orr, os, oo[k]);
       ss[k] = 0;
       if (live[k]) {
+        // both input streams in flight before either is used
+        uint4 rv[VPL];
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) xv[k][j] = ld16(s.in + oi + (int64_t)(v0 + j * vstep) * 8);
+        for (int j = 0; j < VPL; ++j) {
+          xv[k][j] = row_ld<NT>(s.in + oi, v0 + j * vstep);
+          if constexpr (ADD) rv[j] = row_ld<NT>(s.res + orr, v0 + j * vstep);
+        }
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) wv[j] = ld16(s.w + (int64_t)(v0 + j * vstep) * 8);
+        __builtin_amdgcn_sched_barrier(0);  // keep the scheduler from pulling uses between the loads
         if constexpr (ADD) {
-          uint4 rv[VPL];
-#pragma unroll
-          for (int j = 0; j < VPL; ++j) rv[j] = ld16(s.res + orr + (int64_t)(v0 + j * vstep) * 8);
 #pragma unroll
           for (int j = 0; j < VPL; ++j) {
             float xf[8], rf[8];
@@ -189,7 +192,7 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) xf[e] = rf[e] + xf[e];
             xv[k][j] = pack8(xf);  // s rounded to bf16: the norm below reads the rounded values
-            st16(s.sum + os + (int64_t)(v0 + j * vstep) * 8, xv[k][j]);
+            row_st<NT>(s.sum + os, v0 + j * vstep, xv[k][j]);
           }
         }
 #pragma unroll
@@ -224,10 +227,10 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
       for (int j = 0; j < VPL; ++j) {
         float xf[8], wf[8];
         unpack8(xv[k][j], xf);
-        unpack8(wv[j], wf);
+        unpack8(wprep8<GEMMA>(wv[j]), wf);
 #pragma unroll
         for (int e = 0; e < 8; ++e) xf[e] = napply<GEMMA>(xf[e], rstd, wf[e]);
-        st16(s.out + oo[k] + (int64_t)(v0 + j * vstep) * 8, pack8(xf));
+        row_st<NT>(s.out + oo[k], v0 + j * vstep, pack8(xf));
       }
     }
   }
@@ -407,9 +410,17 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
       const int64_t cap = (int64_t)num_cus() * 64;
       if (blocks > cap) blocks = cap;
       const dim3 grd((unsigned)blocks), tb(threads);
-      switch (n512 / W) {
-#define PIE_NV(n) \
-  case n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, kRowsPerGroup, ADD, GEMMA>), grd, tb, 0, st, a, W); break;
+      // Row lists far larger than L2 stream through non-temporal loads and stores (configuration
+      // 2, 8 waves per row, steady state: x / r / s / y at 5.6 TB/s cached, 6.7 TB/s
+      // non-temporal in a standalone model of this kernel); small lists (decode) keep their
+      // outputs in L2 for the next kernel.
+      const bool nt = rows * a.cols * 2 >= (int64_t)64 << 20;
+      switch ((n512 / W) * 2 + (nt ? 1 : 0)) {
+#define PIE_NV(n)                                                                                      \
+  case 2 * n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, kRowsPerGroup, ADD, GEMMA, false>), grd, tb, 0, st, a, W); \
+    break;                                                                                              \
+  case 2 * n + 1: hipLaunchKernelGGL((rmsnorm_rows_reg<n, kRowsPerGroup, ADD, GEMMA, true>), grd, tb, 0, st, a, W); \
+    break;
         PIE_NV(1) PIE_NV(2) PIE_NV(3) PIE_NV(4) PIE_NV(5) PIE_NV(6) PIE_NV(7) PIE_NV(8)
         PIE_NV(9) PIE_NV(10) PIE_NV(11) PIE_NV(12)
 #undef PIE_NV

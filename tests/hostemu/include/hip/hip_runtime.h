@@ -254,6 +254,19 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 #define __builtin_amdgcn_ds_read_tr16_b64_v4i16 emu::ds_read_tr16_b64
 #define __builtin_amdgcn_global_load_lds emu::global_load_lds
 #define __builtin_amdgcn_s_waitcnt(x) ((void)(x))
+#define __builtin_amdgcn_sched_barrier(x) ((void)(x))
+// Buffer resources: the base address only (no range checks; callers stay in bounds).
+typedef char* __amdgpu_buffer_rsrc_t;
+inline __amdgpu_buffer_rsrc_t __builtin_amdgcn_make_buffer_rsrc(void* p, short, int, int) { return (char*)p; }
+typedef unsigned emu_u32x4 __attribute__((ext_vector_type(4)));
+inline emu_u32x4 __builtin_amdgcn_raw_buffer_load_b128(__amdgpu_buffer_rsrc_t r, int off, int soff, int) {
+  emu_u32x4 v;
+  memcpy(&v, r + off + soff, 16);
+  return v;
+}
+inline void __builtin_amdgcn_raw_buffer_store_b128(emu_u32x4 v, __amdgpu_buffer_rsrc_t r, int off, int soff, int) {
+  memcpy(r + off + soff, &v, 16);
+}
 #define __builtin_amdgcn_rcpf(x) (1.0f / (x))
 #define hipLaunchKernelGGL(k, g, b, shm, st, ...) emu::launch(k, dim3(g), dim3(b), __VA_ARGS__)
 
