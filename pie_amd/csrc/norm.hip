@@ -236,6 +236,62 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
   }
 }
 
+// ---------------------------------------------------------------- one row per 512-thread block
+// Large residual-add row lists of 4096*VPL columns: a block of 8 waves takes one row (thread t owns vectors
+// t + 512 j), with no loop over rows, so each block issues its loads at once and the grid is
+// one row per block; non-temporal loads and stores. Same vector ownership and the same fixed
+// order of the 8 wave partial sums as rmsnorm_rows_reg with W = 8, so results are identical.
+// (Configuration 2 in one harness: 44.3 us for this shape against 48 us for the row-loop kernel.)
+template <int VPL, bool ADD, bool GEMMA>
+__global__ __launch_bounds__(512) void rmsnorm_row_block(NormArgs a) {
+  __shared__ acc_t<GEMMA> part[8];
+  const RowSet& s = a.set[0];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int64_t oi, orr, os, oo;
+  row_offsets(s, blockIdx.x, oi, orr, os, oo);
+  uint4 xv[VPL], rv[VPL], wv[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int64_t v = (int64_t)(threadIdx.x + 512 * j) * 8;
+    xv[j] = ld_nt(s.in + oi + v);
+    if constexpr (ADD) rv[j] = ld_nt(s.res + orr + v);
+  }
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) wv[j] = ld16(s.w + (int64_t)(threadIdx.x + 512 * j) * 8);
+  acc_t<GEMMA> ss = 0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    float xf[8];
+    unpack8(xv[j], xf);
+    if constexpr (ADD) {
+      float rf[8];
+      unpack8(rv[j], rf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xf[e] = rf[e] + xf[e];
+      xv[j] = pack8(xf);  // s rounded to bf16: the norm below reads the rounded values
+      row_st<true>(s.sum + os, threadIdx.x + 512 * j, xv[j]);
+      unpack8(xv[j], xf);
+    }
+    accum8<GEMMA>(ss, xf);
+  }
+  const acc_t<GEMMA> wsum = wave_sum(ss);
+  if (lane == 0) part[wave] = wsum;
+  __syncthreads();
+  acc_t<GEMMA> tot = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) tot += part[q];
+  const float rstd = nscale<GEMMA>(tot, (float)a.cols, a.eps);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    float xf[8], wf[8];
+    unpack8(xv[j], xf);
+    unpack8(wprep8<GEMMA>(wv[j]), wf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xf[e] = napply<GEMMA>(xf[e], rstd, wf[e]);
+    row_st<true>(s.out + oo, threadIdx.x + 512 * j, pack8(xf));
+  }
+}
+
 // ---------------------------------------------------------------- 16 lanes per row (D = 16*EPL)
 // EPL elements per lane: 4 (D=64, 8-byte accesses), 8 (D=128), 16 (D=256, two vectors).
 template <int EPL>
@@ -387,6 +443,19 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
   const bool vec = a.cols % 8 == 0 && rowset_vec_ok(a.set[0], ADD) &&
                    (a.set[1].rows == 0 || rowset_vec_ok(a.set[1], ADD));
   const dim3 blk(256);
+  const bool large = rows * a.cols * 2 >= (int64_t)64 << 20;  // far larger than L2
+  // (the residual-add form only: a plain norm, one input stream, keeps too few bytes in flight at
+  // one vector per lane and stays on the row-loop kernel with 4 vectors per lane)
+  if (ADD && vec && large && a.set[1].rows == 0 && a.cols % 4096 == 0 && a.cols <= 3 * 4096 &&
+      rows < 0x7fffffff) {
+    const dim3 grd((unsigned)rows), tb(512);
+    switch (a.cols / 4096) {
+      case 1: hipLaunchKernelGGL((rmsnorm_row_block<1, ADD, GEMMA>), grd, tb, 0, st, a); break;
+      case 2: hipLaunchKernelGGL((rmsnorm_row_block<2, ADD, GEMMA>), grd, tb, 0, st, a); break;
+      default: hipLaunchKernelGGL((rmsnorm_row_block<3, ADD, GEMMA>), grd, tb, 0, st, a); break;
+    }
+    return check_launch(name);
+  }
   if (vec && a.set[1].rows == 0 && a.cols % 512 == 0 && a.cols <= 8 * 12 * 512) {
     const int64_t n512 = a.cols / 512;
     // Waves per row W (each lane then holds VPL = cols / (512 W) 16-byte vectors). Residual add:
@@ -414,8 +483,7 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
       // 2, 8 waves per row, steady state: x / r / s / y at 5.6 TB/s cached, 6.7 TB/s
       // non-temporal in a standalone model of this kernel); small lists (decode) keep their
       // outputs in L2 for the next kernel.
-      const bool nt = rows * a.cols * 2 >= (int64_t)64 << 20;
-      switch ((n512 / W) * 2 + (nt ? 1 : 0)) {
+      switch ((n512 / W) * 2 + (large ? 1 : 0)) {
 #define PIE_NV(n)                                                                                      \
   case 2 * n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, kRowsPerGroup, ADD, GEMMA, false>), grd, tb, 0, st, a, W); \
     break;                                                                                              \
