@@ -436,6 +436,12 @@ bool rowset_vec_ok(const RowSet& s, bool add) {
   return ok;
 }
 
+// Measurement switch: 0 keeps large row lists on the cached row-loop kernel (configuration 2,
+// same box: per op 47.8 us against 44.1 us; in the back-to-back add-norm + SiLU step, whose
+// SiLU then drains the norm's cached writes, 6.44 against 6.35 TB/s).
+#ifndef PIE_NORM_LARGE_NT
+#define PIE_NORM_LARGE_NT 1
+#endif
 template <bool ADD, bool GEMMA>
 int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
   const int64_t rows = a.set[0].rows + a.set[1].rows;
@@ -443,7 +449,7 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
   const bool vec = a.cols % 8 == 0 && rowset_vec_ok(a.set[0], ADD) &&
                    (a.set[1].rows == 0 || rowset_vec_ok(a.set[1], ADD));
   const dim3 blk(256);
-  const bool large = rows * a.cols * 2 >= (int64_t)64 << 20;  // far larger than L2
+  const bool large = PIE_NORM_LARGE_NT && rows * a.cols * 2 >= (int64_t)64 << 20;  // far larger than L2
   // (the residual-add form only: a plain norm, one input stream, keeps too few bytes in flight at
   // one vector per lane and stays on the row-loop kernel with 4 vectors per lane)
   if (ADD && vec && large && a.set[1].rows == 0 && a.cols % 4096 == 0 && a.cols <= 3 * 4096 &&
