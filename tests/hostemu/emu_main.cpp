@@ -484,9 +484,9 @@ static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
 // so kept sets and draws must match the oracle exactly; ties are forced in some rows.
 // peaked: p = softmax of N(0, 3) logits (a few dominant tokens, as after an LM head) with k up to
 // 64, so the candidate lists are short; otherwise near-uniform rows whose lists can overflow.
-static void case_sample(int64_t B, int64_t V, int mode, bool row_map, bool peaked = false) {
-  printf("sample B=%lld V=%lld mode=%d rows=%d peaked=%d\n", (long long)B, (long long)V, mode, (int)row_map,
-         (int)peaked);
+static void case_sample(int64_t B, int64_t V, int mode, bool row_map, bool peaked = false, int64_t pad = 0) {
+  printf("sample B=%lld V=%lld mode=%d rows=%d peaked=%d pad=%lld\n", (long long)B, (long long)V, mode,
+         (int)row_map, (int)peaked, (long long)pad);
   Buf<float> probs(B * V);
   std::uniform_int_distribution<int> dq(0, 1 << 12);
   std::normal_distribution<double> dn(0.0, 3.0);
@@ -512,7 +512,10 @@ static void case_sample(int64_t B, int64_t V, int mode, bool row_map, bool peake
     minp[r] = (float)du(rng) * 0.5f;
     u[r] = du(rng);
   }
-  rc_ok(pie_hip_sample(probs.p, V, B, V, B, row_map ? rows.p : nullptr, mode, topk.p, 0, topp.p, 0.f, minp.p, 0.f,
+  const int64_t S = V + pad;  // row stride of the copy the kernel reads (exact-size buffer)
+  Buf<float> padded(B * S - pad);
+  for (int64_t r = 0; r < B; ++r) memcpy(padded.p + r * S, probs.p + r * V, V * 4);
+  rc_ok(pie_hip_sample(padded.p, S, B, V, B, row_map ? rows.p : nullptr, mode, topk.p, 0, topp.p, 0.f, minp.p, 0.f,
                        u.p, 0, 0, out.p, nullptr), "sample");
   Buf<float> mapped(B * V);
   for (int64_t r = 0; r < B; ++r) memcpy(mapped.p + r * V, probs.p + (int64_t)rows[r] * V, V * 4);
@@ -635,6 +638,8 @@ int main(int argc, char** argv) {
     case_sample(2, 4099, 4, false);  // several 4096-element scan tiles
     for (int mode = 1; mode <= 4; ++mode) case_sample(1, 10000, mode, false, true);  // candidate lists
     case_sample(1, 10003, 4, false, true);  // candidate lists, scalar loads
+    case_sample(2, 10003, 4, false, true, 1);  // 16-byte rows whose length is not a multiple of 4
+    case_sample(2, 10001, 3, false, true, 3);
     case_sample(1, 40000, 1, false);        // top_p lists that overflow: direct passes
     // (rows of more than 256 tiles, whose draw chunks span several tiles, run in the GPU tests)
     case_softmax(3, 1000, false);

@@ -83,6 +83,26 @@ def test_sample_long_rows(dev, mode):
         assert (got == want).all(), f"V={V}: {got} vs {want}"
 
 
+@pytest.mark.parametrize("mode", list(SAMPLERS))
+def test_sample_padded_rows(dev, mode):
+    """16-byte aligned rows whose length is not a multiple of 4 (a padded row stride): the
+    vector passes and the candidate lists' last elements."""
+    B, V, pad = 16, 128253, 3
+    g = torch.Generator().manual_seed(77)
+    full = torch.softmax(torch.randn(B, V + pad, generator=g, dtype=torch.float64) * 3, -1).float()
+    full[:, V:] = 0.9  # never read: beyond each row's V entries
+    probs = full[:, :V]
+    prm = _params(B, V, 78)
+    prm["top_k"] = torch.randint(1, 300, (B,), generator=g).to(torch.int32)
+    dp = {k: v.to(dev) for k, v in prm.items()}
+    got = _call(mode, full.to(dev)[:, :V], dp, uniforms=dp["u"]).cpu().numpy()
+    want, kept = oracle.sample(probs.contiguous().numpy(), mode, prm["u"].numpy(),
+                               top_k=prm["top_k"].numpy(), top_p=prm["top_p"].numpy(),
+                               min_p=prm["min_p"].numpy())
+    assert kept[np.arange(B), got].all()
+    assert (got == want).all(), f"{got} vs {want}"
+
+
 def test_sample_scalar_params_and_row_indices(dev):
     B, V = 16, 1000
     probs = _grid_probs(B, V, 5)
