@@ -70,15 +70,27 @@ struct RopeAppendArgs {
 };
 
 // cos/sin of pair i at position p: from the table when one is given, else from inv_freq.
+// (cos, sin) of the angle p * f for position p and frequency f, by the hardware sine / cosine,
+// which take revolutions: the revolutions p * (f / 2pi) are formed exactly from the fp32 product
+// and its fma-recovered low part, so only the fractional part matters and no precision is lost
+// to the angle's magnitude (positions up to 2^24); the result carries the rounding of f / 2pi
+// (~p * f * 6e-8 rad, the order of the reference's own fp32 angle p * f). p = 0 gives (1, 0).
+__device__ __forceinline__ float2 rope_pos_cs(int p, float f) {
+  const float fr = f * 0.15915494309189535f;  // f / 2pi
+  const float pf = (float)p;
+  const float hi = pf * fr;
+  const float lo = fmaf(pf, fr, -hi);
+  const float rev = __builtin_amdgcn_fractf(__builtin_amdgcn_fractf(hi) + lo);
+  return make_float2(__builtin_amdgcn_cosf(rev), __builtin_amdgcn_sinf(rev));
+}
+
 __device__ __forceinline__ float2 rope_cs(const RopeAppendArgs& a, int p, int i, int half) {
   if (a.cs) {
     if (p < 0 || (int64_t)p >= a.cs_rows) return make_float2(1.f, 0.f);
     const float* row = a.cs + (int64_t)p * a.cs_ld;
     return make_float2(row[i], row[half + i]);
   }
-  float sn, cs;
-  sincosf((float)p * a.inv_freq[i], &sn, &cs);
-  return make_float2(cs, sn);
+  return rope_pos_cs(p, a.inv_freq[i]);
 }
 
 
@@ -293,7 +305,7 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_append_d128(QkNormArgs qa) 
   // Latency order: position and the first batch of rows are requested before the page
   // lookup chain and the cos/sin table, which then overlap the loads in flight.
   constexpr int UB = 4;  // head rows per 16-lane group per batch
-  const float p = (float)a.pos[tq];
+  const int p = a.pos[tq];
   struct Batch {
     uint4 X[UB], Wt[UB];
     int kind[UB], hd[UB];  // kind: 0 q, 1 k, 2 v, 3 none
@@ -325,11 +337,7 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_append_d128(QkNormArgs qa) 
   Batch b = load_batch(sg);
   const int64_t kc = live ? slot_offset(a.c, tq) : -1;
   if (live) {
-    for (int i = gt; i < 64; i += gsize) {
-      float sn, cs;
-      sincosf(p * a.inv_freq[i], &sn, &cs);
-      tab[slot][i] = make_float2(cs, sn);
-    }
+    for (int i = gt; i < 64; i += gsize) tab[slot][i] = rope_pos_cs(p, a.inv_freq[i]);
   }
   __syncthreads();
   if (!live) return;  // whole token groups (waves) leave together
