@@ -72,7 +72,8 @@ struct RopeAppendArgs {
 // cos/sin of pair i at position p: from the table when one is given, else from inv_freq.
 // (cos, sin) of the angle p * f for position p and frequency f, by the hardware sine / cosine,
 // which take revolutions: the revolutions p * (f / 2pi) are formed exactly from the fp32 product
-// and its fma-recovered low part, so only the fractional part matters and no precision is lost
+// and its fma-recovered low part (the error-free TwoProduct of Ogita, Rump and Oishi, "Accurate
+// sum and dot product", SIAM J. Sci. Comput. 2005), so only the fractional part matters and no precision is lost
 // to the angle's magnitude (positions up to 2^24); the result carries the rounding of f / 2pi
 // (~p * f * 6e-8 rad, the order of the reference's own fp32 angle p * f). p = 0 gives (1, 0).
 __device__ __forceinline__ float2 rope_pos_cs(int p, float f) {
