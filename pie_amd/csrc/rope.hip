@@ -69,13 +69,13 @@ struct RopeAppendArgs {
   int64_t cs_rows, cs_ld;
 };
 
-// cos/sin of pair i at position p: from the table when one is given, else from inv_freq.
 // (cos, sin) of the angle p * f for position p and frequency f, by the hardware sine / cosine,
 // which take revolutions: the revolutions p * (f / 2pi) are formed exactly from the fp32 product
 // and its fma-recovered low part (the error-free TwoProduct of Ogita, Rump and Oishi, "Accurate
-// sum and dot product", SIAM J. Sci. Comput. 2005), so only the fractional part matters and no precision is lost
-// to the angle's magnitude (positions up to 2^24); the result carries the rounding of f / 2pi
-// (~p * f * 6e-8 rad, the order of the reference's own fp32 angle p * f). p = 0 gives (1, 0).
+// sum and dot product", SIAM J. Sci. Comput. 2005), so only the fractional part matters and no
+// precision is lost to the angle's magnitude (positions up to 2^24); the result carries the
+// rounding of f / 2pi (~p * f * 6e-8 rad, the order of the reference's own fp32 angle p * f).
+// p = 0 gives (1, 0).
 __device__ __forceinline__ float2 rope_pos_cs(int p, float f) {
   const float fr = f * 0.15915494309189535f;  // f / 2pi
   const float pf = (float)p;
@@ -85,6 +85,7 @@ __device__ __forceinline__ float2 rope_pos_cs(int p, float f) {
   return make_float2(__builtin_amdgcn_cosf(rev), __builtin_amdgcn_sinf(rev));
 }
 
+// cos/sin of pair i at position p: from the table when one is given, else from inv_freq.
 __device__ __forceinline__ float2 rope_cs(const RopeAppendArgs& a, int p, int i, int half) {
   if (a.cs) {
     if (p < 0 || (int64_t)p >= a.cs_rows) return make_float2(1.f, 0.f);
