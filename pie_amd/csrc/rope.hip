@@ -196,14 +196,32 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
   // Latency order: the position, the first batch of data and the page lookup chain are all
   // requested before the cos/sin table is computed, so they overlap it.
   const int p = ROPE ? a.pos[tq] : 0;
+  // This lane's cos/sin inputs (pair gt: a frequency, or a table row's two entries) are requested
+  // before the data: vector loads complete in order, so inputs requested after the data would
+  // hold the table (and the barrier behind it) until every data load had landed.
+  const bool early = ROPE && live && half <= gsize && gt < half;
+  const bool in_tab = a.cs && p >= 0 && (int64_t)p < a.cs_rows;
+  float in0 = 0.f, in1 = 0.f;
+  if (early) {
+    if (a.cs) {
+      const float* row = a.cs + (int64_t)(in_tab ? p : 0) * a.cs_ld;
+      in0 = row[gt];
+      in1 = row[half + gt];
+    } else {
+      in0 = a.inv_freq[gt];
+    }
+  }
   load_units<ROPE, APPEND, INTERLEAVE, UB>(b, g, gt);
   int64_t kc = -1;
   if constexpr (APPEND) {
     if (live) kc = slot_offset(cd, tq);
   }
   if constexpr (ROPE) {
-    if (live)
+    if (early) {
+      tab[slot][gt] = a.cs ? (in_tab ? make_float2(in0, in1) : make_float2(1.f, 0.f)) : rope_pos_cs(p, in0);
+    } else if (live && half > gsize) {
       for (int i = gt; i < half; i += gsize) tab[slot][i] = rope_cs(a, p, i, half);
+    }
     __syncthreads();
   }
   if (!live) return;
