@@ -354,11 +354,12 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_append_d128(QkNormArgs qa) 
     }
     return b;
   };
+  // this lane's frequency is requested before the rows: vector loads complete in order, so a
+  // frequency requested after them would hold the table until every row had landed
+  const float f0 = (live && gt < 64) ? a.inv_freq[gt] : 0.f;
   Batch b = load_batch(sg);
   const int64_t kc = live ? slot_offset(a.c, tq) : -1;
-  if (live) {
-    for (int i = gt; i < 64; i += gsize) tab[slot][i] = rope_pos_cs(p, a.inv_freq[i]);
-  }
+  if (live && gt < 64) tab[slot][gt] = rope_pos_cs(p, f0);
   __syncthreads();
   if (!live) return;  // whole token groups (waves) leave together
   const float2* tb = tab[slot] + lo * 8;
