@@ -97,12 +97,17 @@ def load() -> C.CDLL:
     return lib
 
 
+_fns: dict = {}
+
+
 def call(name: str, *args) -> None:
     """Invoke an entry point and raise PieHipError with the library's message on failure."""
-    lib = load()
-    rc = getattr(lib, name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(load(), name)
+    rc = fn(*args)
     if rc != 0:
-        msg = lib.pie_hip_last_error().decode(errors="replace")
+        msg = load().pie_hip_last_error().decode(errors="replace")
         if rc == 1:
             raise ValueError(f"{name}: {msg}")
         raise PieHipError(f"{name} failed ({rc}): {msg}")

@@ -52,7 +52,15 @@ _BF16 = torch.bfloat16
 
 
 # ----------------------------------------------------------------------------- helpers
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    """The current torch stream of t's device as a raw handle (the raw accessor skips building a
+    Stream object: ~0.2 µs against ~2 µs per call)."""
+    if _raw_stream is not None:
+        idx = t.device.index
+        return _raw_stream(torch.cuda.current_device() if idx is None else idx)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
