@@ -12,8 +12,9 @@ radix select, an inverse-CDF draw in index order. Randomness: Philox4x32-10 keye
 counted by ``offset``; when neither is given, a per-process seed (from torch's default generator)
 and an offset that advances by one per call, so successive calls draw independent numbers and a
 fixed (seed, offset) reproduces a draw exactly. ``generator=`` (a torch.Generator) supplies the
-seed and keeps its own offset. ``uniforms=`` (float64 [batch], this package's extension) fixes the
-uniform of every row, which tests use for exact comparisons.
+numbers: a CPU generator draws each call's seed from its own stream, a GPU generator gives its
+seed and its Philox offset, which each call advances. ``uniforms=`` (float64 [batch], this
+package's extension) fixes the uniform of every row, which tests use for exact comparisons.
 """
 from __future__ import annotations
 
@@ -32,18 +33,20 @@ __all__ = ["sampling_from_probs", "top_p_sampling_from_probs", "top_k_sampling_f
 _MODES = {"plain": 0, "top_p": 1, "top_k": 2, "min_p": 3, "top_k_top_p": 4}
 _lock = threading.Lock()
 _state = {"seed": None, "offset": 0}
-_gen_offsets: dict = {}
 
 
 def _seed_offset(generator, seed, offset):
     if seed is not None:
         return int(seed) & (2**64 - 1), int(offset or 0) & (2**64 - 1)
+    if generator is not None:
+        if generator.device.type == "cpu":
+            # a fresh 62-bit seed from the generator's own stream (advances it; no device sync)
+            return int(torch.randint(0, 2**62, (1,), generator=generator)), 0
+        # a GPU (Philox) generator: its seed, and its offset, which each call advances
+        off = generator.get_offset()
+        generator.set_offset(off + 4)
+        return generator.initial_seed() & (2**64 - 1), off
     with _lock:
-        if generator is not None:
-            key = id(generator)
-            off = _gen_offsets.get(key, 0)
-            _gen_offsets[key] = off + 1
-            return generator.initial_seed() & (2**64 - 1), off
         if _state["seed"] is None:
             _state["seed"] = int(torch.randint(0, 2**62, (1,)).item())
         off = _state["offset"]

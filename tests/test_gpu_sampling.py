@@ -142,7 +142,14 @@ def test_sample_reproducible_by_seed_and_offset(dev):
     assert torch.equal(a, b) and not torch.equal(a, c)
     g = torch.Generator().manual_seed(77)
     d, e = sampling.sampling_from_probs(probs, generator=g), sampling.sampling_from_probs(probs, generator=g)
-    assert not torch.equal(d, e)  # the generator's offset advances
+    assert not torch.equal(d, e)  # the generator advances
+    g2 = torch.Generator().manual_seed(77)  # the same seed replays the same sequence of draws
+    assert torch.equal(sampling.sampling_from_probs(probs, generator=g2), d)
+    assert torch.equal(sampling.sampling_from_probs(probs, generator=g2), e)
+    gg = torch.Generator(device=probs.device).manual_seed(5)  # a GPU generator: its offset advances
+    off0 = gg.get_offset()
+    f1, f2 = sampling.sampling_from_probs(probs, generator=gg), sampling.sampling_from_probs(probs, generator=gg)
+    assert not torch.equal(f1, f2) and gg.get_offset() > off0
 
 
 @pytest.mark.parametrize("V", [128256, 151936])
