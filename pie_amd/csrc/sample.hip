@@ -249,8 +249,9 @@ struct SampleArgs {
 // here over p). row_tot: the row's total mass for top_p (0: sum it here over p). Candidate lists
 // hold every element at or above the threshold being searched, so the counts and masses that
 // decide it are the same as over the whole row.
-__device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, int V, bool vec, const SampleArgs& a, int r,
-                           int64_t npos, uint64_t row_tot, SampleShared& sh) {
+__device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, int V, bool vec,
+                                           const SampleArgs& a, int r, int64_t npos, uint64_t row_tot,
+                                           SampleShared& sh) {
   if (V == 0) {  // nothing to draw from (an empty candidate list)
     if (threadIdx.x == 0) a.out[r] = -1;
     return;
