@@ -9,7 +9,8 @@ timed with HIP events on the stream it runs on; cpu_baseline = torch-CPU running
 reference's own expressions (`residual + x`, F.rms_norm, F.silu(gate) * up) on a bounded
 sample of the same workload; "ops" = every configuration's per-op µs / GB/s (steady state over
 buffer sets larger than the 256 MB last-level cache, and one launch after a flush) and the
-decode-chain µs (HIP-graph replay).
+decode-chain µs (HIP-graph replay); "cpu_ops" = torch-CPU GB/s of each configuration's
+expressions on bounded samples beside them.
 """
 from __future__ import annotations
 
@@ -73,6 +74,75 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
             "kind": "reference",
             "sample": f"{n} x 256-row slices of config 2 (add+rms_norm [256,4096], silu*mul "
                       f"[256,2x14336]) in torch-CPU bf16, {dt:.1f} s"}
+
+
+def cpu_ops(budget_each: float = 2.0) -> list:
+    """torch-CPU timings beside the per-op GPU figures, on bounded samples with all host threads:
+    RMSNorm (configuration 1, full size), add + RMSNorm and SiLU-and-mul (256-row slices of
+    configuration 2) and the embedding (configuration 4, full size) run the reference's own
+    torch expressions (kind "reference": llama3.py:555, :586, :569-572, :471). flashinfer has no
+    CPU path, so Llama-3.1 RoPE and the paged append (configuration 3, 2048-token slices) run a
+    torch restatement of flashinfer's semantics (kind "port"; the frequencies from oracle/).
+    The GPU bench runs these on the GPU box's host cores after the timed GPU work."""
+    import torch
+    import torch.nn.functional as F
+    import oracle
+    from pie_amd import workloads as wl
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+
+    def rate(name, kind, nbytes, fn, sample):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_each:
+            fn()
+            n += 1
+        dt = time.perf_counter() - t0
+        return {"op": name, "kind": kind, "gbs": round(n * nbytes / dt / 1e9, 3),
+                "us": round(dt / n * 1e6, 1), "cores": threads, "sample": sample}
+
+    out = []
+    c1 = wl.cfg1()
+    out.append(rate("cfg1 rmsnorm [2048,2048]", "reference", 2 * 2048 * 2048 * 2 + 2048 * 2,
+                    lambda: F.rms_norm(c1["x"], [2048], c1["w"], c1["eps"]), "full size"))
+    c2 = wl.cfg2(T=256)
+    b_add, b_silu = wl.cfg2_bytes(T=256)
+    I = c2["gate_up"].shape[1] // 2
+    out.append(rate("cfg2a add+rmsnorm", "reference", b_add,
+                    lambda: F.rms_norm(c2["r"] + c2["x"], [4096], c2["w"], c2["eps"]), "256 rows"))
+    g, u = torch.split(c2["gate_up"], [I, I], -1)
+    out.append(rate("cfg2b silu_and_mul", "reference", b_silu, lambda: F.silu(g) * u, "256 rows"))
+    c3 = wl.cfg3(B=4)  # four of configuration 3's requests (same generator), a 2048-token slice
+    pb = c3["batch"]
+    T = min(2048, int(pb.lens.sum()))
+    q, k, v = wl.split_qkv(c3["qkv"][:T].clone(), 32, 8, 128)
+    f = torch.tensor(oracle.inv_freq_llama31(128, **{kk: float(vv) for kk, vv in c3["rope"].items()}),
+                     dtype=torch.float32)
+    pos = pb.positions[:T].to(torch.float32)
+
+    def rope():  # half-split pairs in fp32, written back in place (flashinfer_metal/ops.py:306-346)
+        ang = pos[:, None] * f[None, :]
+        cs, sn = ang.cos()[:, None, :], ang.sin()[:, None, :]
+        for t in (q, k):
+            x, y = t[..., :64].float(), t[..., 64:].float()
+            t[..., :64] = (x * cs - y * sn).to(t.dtype)
+            t[..., 64:] = (x * sn + y * cs).to(t.dtype)
+    bts = wl.cfg3_bytes(T)
+    out.append(rate("cfg3 llama31 rope", "port", bts["rope"], rope, f"{T} tokens"))
+    cache = wl.sentinel_cache(c3["cache_shape"])
+    bidx, bpos = pb.batch_indices[:T].long(), pb.positions[:T].long()
+    pages = pb.kv_indices.long()[pb.kv_indptr.long()[bidx] + bpos // 16]
+    slots = bpos % 16
+
+    def append():  # cache[page, 0 / 1, slot] = k / v (flashinfer_metal/ops.py:349-389)
+        cache[pages, 0, slots] = k
+        cache[pages, 1, slots] = v
+    out.append(rate("cfg3 paged append", "port", bts["append"], append, f"{T} tokens"))
+    c4 = wl.cfg4()
+    ids = c4["ids"].long()  # all 16384 ids: the 268 MB the op moves do not stay in host caches
+    out.append(rate("cfg4 embedding", "reference", wl.cfg4_bytes(),
+                    lambda: F.embedding(ids, c4["W"]), "full size"))
+    return out
 
 
 def _rotating(calls, iters=60, reps=3):
@@ -523,6 +593,8 @@ def main():
                      "algorithmic_bytes": b_silu},
         "cpu_baseline": None if args.no_cpu else cpu_baseline(),
     }
+    if not args.no_cpu:
+        line["cpu_ops"] = cpu_ops()
     if ops_res is not None:
         line["ops"] = ops_res
     print(json.dumps(line))
