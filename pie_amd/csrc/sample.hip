@@ -895,6 +895,7 @@ extern "C" int pie_hip_sample(const float* probs, int64_t prob_stride, int64_t p
                               int32_t top_k_scalar, const float* top_p, float top_p_scalar,
                               const float* min_p, float min_p_scalar, const double* uniforms,
                               uint64_t seed, uint64_t offset, int32_t* out, void* stream) {
+  if (batch == 0) return PIE_HIP_OK;  // an empty batch (whose tensors may have null data)
   PIE_REQUIRE(probs && out, "sample: null probs or out");
   PIE_REQUIRE(vocab > 0 && vocab < (1ll << 28) && batch >= 0 && batch < (1ll << 31) &&
                   prob_stride >= vocab && prob_rows >= 0 && prob_rows < (1ll << 31) &&
@@ -914,6 +915,7 @@ extern "C" int pie_hip_sample(const float* probs, int64_t prob_stride, int64_t p
 extern "C" int pie_hip_scaled_softmax(const void* logits, int32_t is_bf16, int64_t stride, int64_t batch,
                                       int64_t vocab, const float* temperatures, float greedy_threshold,
                                       void* out, int64_t out_stride, void* stream) {
+  if (batch == 0) return PIE_HIP_OK;  // an empty batch (whose tensors may have null data)
   PIE_REQUIRE(logits && out && temperatures, "scaled_softmax: null pointer");
   PIE_REQUIRE(vocab > 0 && vocab < (1ll << 31) && batch >= 0 && batch < (1ll << 31) && stride >= vocab &&
                   out_stride >= vocab,
