@@ -776,6 +776,9 @@ __device__ __forceinline__ f32x16_t mfma_32x32x16(const u32x4_t& a, const u32x4_
 // per half-wave, so rows r..r+3 XOR chunk bits 2-3 with r mod 4.
 __device__ __forceinline__ int v32_swizzle(int r) { return (r & 3) << 2; }
 
+// Headroom (log2 units) the running maximum may trail a row's scores by before it is moved.
+constexpr float kLazyMax = 8.f;
+
 template <int D>
 __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
     const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv,
@@ -927,33 +930,47 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
           if (!(t <= lim && t >= lo && ((tv >> tt) & 1ull))) vis &= ~(1u << i);
         }
       }
-      float sc[16];
-      float mx = -INFINITY;
-      if (__builtin_amdgcn_ballot_w64(vis != 0xffffu) == 0) {  // wave-uniform: all visible
+      // Scores stay raw (q.k) until the exponent, where one fma applies the scale: the row maximum
+      // is taken over raw scores, negated when the scale is negative (a uniform branch), with
+      // hidden entries set to the raw value that scales to -inf (the scale is never 0 here).
+      const bool neg = scale_log2 < 0.f;
+      const bool masked = __builtin_amdgcn_ballot_w64(vis != 0xffffu) != 0;
+      if (masked) {
+        const float hidden = neg ? INFINITY : -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) { sc[i] = sacc[i] * scale_log2; mx = fmaxf(mx, sc[i]); }
+        for (int i = 0; i < 16; ++i) sacc[i] = ((vis >> i) & 1u) ? sacc[i] : hidden;
+      }
+      float mx = -INFINITY;
+      if (!neg) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[i]);
       } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          sc[i] = ((vis >> i) & 1u) ? sacc[i] * scale_log2 : -INFINITY;
-          mx = fmaxf(mx, sc[i]);
-        }
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, -sacc[i]);
       }
-      mx = fmaxf(mx, lane_read(mx, lane ^ 32));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      m_run = m_new;
-      float psum = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) { sc[i] = fast_exp2(sc[i] - m_use); psum += sc[i]; }
-      l_run = l_run * alpha + psum;
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+      mx = fmaxf(mx, lane_read(mx, lane ^ 32)) * fabsf(scale_log2);
+      // Lazy maximum: the reference maximum m_run moves (and O, l are rescaled) only when a row's
+      // tile maximum exceeds it by more than kLazyMax, so exponents stay <= 2^kLazyMax. The result
+      // is the same softmax (numerator and denominator share the reference), and the 64-register
+      // rescale runs a few times per row instead of on almost every tile.
+      if (__builtin_amdgcn_ballot_w64(mx > m_run + kLazyMax) != 0) {
+        const bool grow = mx > m_run + kLazyMax;
+        const float alpha = grow ? fast_exp2(m_run - mx) : 1.f;
+        if (grow) m_run = mx;
+        l_run *= alpha;
 #pragma unroll
         for (int bb = 0; bb < NB; ++bb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) o[bb][i] *= alpha;
       }
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+      float sc[16];
+      float psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sc[i] = fast_exp2(fmaf(sacc[i], scale_log2, -m_use));
+#pragma unroll
+      for (int i = 0; i < 16; ++i) psum += sc[i];
+      l_run += psum;
       u32x4_t pb[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -1204,9 +1221,11 @@ static void launch_prefill(hipStream_t st, dim3 grid, const uint16_t* q, int64_t
                            const int32_t* plan, int mode, int window_left, const uint32_t* packed,
                            const int64_t* woff, const int32_t* extent, uint16_t* out, int64_t o_ts,
                            int64_t o_hs) {
+  // attn_prefill32_kernel scales raw scores inside the exponent, where a zero scale would turn a
+  // hidden (-inf) score into NaN; 1e-30 gives the same result (every exponent rounds to 2^0).
   if constexpr (D == 128 && PIE_PREFILL_MFMA32)
     hipLaunchKernelGGL(attn_prefill32_kernel<128>, grid, dim3(256), 0, st, q, q_ts, q_hs, kv, qo_indptr, G,
-                       sl2, plan, mode, window_left, packed, woff, extent, out, o_ts, o_hs);
+                       sl2 == 0.f ? 1e-30f : sl2, plan, mode, window_left, packed, woff, extent, out, o_ts, o_hs);
   else
     hipLaunchKernelGGL(attn_prefill_kernel<D>, grid, dim3(64 * prefill_waves<D>()), 0, st, q, q_ts, q_hs, kv,
                        qo_indptr, G, sl2, plan, mode, window_left, packed, woff, extent, out, o_ts, o_hs);
