@@ -58,6 +58,12 @@ __device__ __forceinline__ u32x4_t ld16v(const uint16_t* p) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Online softmax with a lazy maximum: a row's reference maximum (and with it the rescale of its
+// output accumulators and sum) moves only when a tile's scores exceed it by more than kLazyMax
+// (log2 units), so every exponent stays <= 2^kLazyMax. Numerator and denominator share the
+// reference, so the softmax is the same; the rescale runs a few times per row, not per tile.
+constexpr float kLazyMax = 8.f;
+
 // Kernel argument: the paged KV cache and its page table.
 struct PagedKV {
   const uint16_t* k;       // k of page 0, slot 0, head 0
@@ -181,9 +187,10 @@ struct WaveAttn {
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
     mx = fmaxf(mx, lane_read(mx, lane ^ 16));
     mx = fmaxf(mx, lane_read(mx, lane ^ 32));
-    const float m_new = fmaxf(m, mx);
+    const bool grow = mx > m + kLazyMax;  // lazy maximum
+    const float m_new = grow ? mx : m;
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = fast_exp2(m - m_use);
+    const float alpha = grow ? fast_exp2(m - mx) : 1.f;
     float p[2][4], psum = 0.f;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
@@ -776,8 +783,6 @@ __device__ __forceinline__ f32x16_t mfma_32x32x16(const u32x4_t& a, const u32x4_
 // per half-wave, so rows r..r+3 XOR chunk bits 2-3 with r mod 4.
 __device__ __forceinline__ int v32_swizzle(int r) { return (r & 3) << 2; }
 
-// Headroom (log2 units) the running maximum may trail a row's scores by before it is moved.
-constexpr float kLazyMax = 8.f;
 
 template <int D>
 __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
@@ -949,10 +954,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, -sacc[i]);
       }
       mx = fmaxf(mx, lane_read(mx, lane ^ 32)) * fabsf(scale_log2);
-      // Lazy maximum: the reference maximum m_run moves (and O, l are rescaled) only when a row's
-      // tile maximum exceeds it by more than kLazyMax, so exponents stay <= 2^kLazyMax. The result
-      // is the same softmax (numerator and denominator share the reference), and the 64-register
-      // rescale runs a few times per row instead of on almost every tile.
+      // lazy maximum (kLazyMax)
       if (__builtin_amdgcn_ballot_w64(mx > m_run + kLazyMax) != 0) {
         const bool grow = mx > m_run + kLazyMax;
         const float alpha = grow ? fast_exp2(m_run - mx) : 1.f;

@@ -353,3 +353,61 @@ def test_decode_graph_with_window_like_olmo(dev):
     a = {"q": q.cpu(), "cache": cache.cpu(), "batch": pb, "layout": "NHD"}
     want = _want(a, window_left=window)
     _tight(out, want, "graph replay with window")
+
+
+def _ramp_batch(slope, D, Hq=8, Hkv=2, page_size=16):
+    """One fresh prefill (qo 200 tokens, no cached context) and one request with 300 cached
+    tokens and 1 query token, where token t's key is a_t in every dimension and every query
+    entry is 1: row scores rise (slope > 0) or fall (slope < 0) by |slope| log2 units per
+    token. Rising scores move each row's maximum on every tile, by less or more than the
+    kernels' lazy-maximum headroom (2^8) depending on the slope."""
+    a = wl.attn_batch(torch.tensor([0, 300]), torch.tensor([200, 1]), Hq=Hq, Hkv=Hkv, D=D,
+                      page_size=page_size, seed=131)
+    pb = a["batch"]
+    unit = D / np.sqrt(D) * np.log2(np.e)  # log2 units per unit of a_t (q = 1, scale 1/sqrt(D))
+    cache = a["cache"].clone()
+    for b in range(2):
+        kv = int(pb.seq_lens[b])
+        pages = pb.kv_indices[int(pb.kv_indptr[b]):int(pb.kv_indptr[b + 1])].long()
+        for t in range(kv):
+            cache[pages[t // page_size], 0, t % page_size] = slope * t / unit
+    a["cache"] = cache
+    a["q"] = torch.ones_like(a["q"])
+    return a
+
+
+@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("slope", [0.1, 0.3, 1.5, -1.5])
+def test_prefill_and_decode_with_rising_scores(dev, D, slope):
+    """Scores that rise steadily along the row (the running maximum grows inside the lazy
+    headroom, past it, or on every tile) or fall (it never grows) match the oracle."""
+    print(f"ramp D={D} slope={slope}", flush=True)
+    a = _ramp_batch(slope, D)
+    want = _want(a)
+    got = _prefill(dev, a)
+    assert_bf16_close(N(got), want, what=f"prefill slope {slope}")
+    _tight(got, want, f"prefill slope {slope}")
+    d = wl.attn_batch(torch.tensor([300]), torch.tensor([1]), Hq=8, Hkv=2, D=D, seed=131)
+    d["cache"], d["q"] = a["cache"], a["q"][200:201]
+    pb = a["batch"]
+    d["batch"] = wl.paged_batch(torch.tensor([300]), torch.tensor([1]), 16, pb.kv_indices.numel(), 0)
+    d["batch"].kv_indices[:] = pb.kv_indices[int(pb.kv_indptr[1]):]
+    for splits in (1, 3):
+        got = _decode(dev, d, splits=splits)
+        _tight(got, _want(d), f"decode slope {slope} splits {splits}")
+
+
+@pytest.mark.parametrize("sm_scale", [-0.09, 0.0])
+def test_prefill_negative_and_zero_scale(dev, sm_scale):
+    """A negative scale (the row maximum is the smallest raw score) and a zero scale (uniform
+    weights over the visible tokens) match the oracle."""
+    a = wl.attn_batch(torch.tensor([0, 70]), torch.tensor([90, 33]), Hq=8, Hkv=2, D=128, seed=133)
+    pb = a["batch"]
+    w = attention.BatchPrefillWithPagedKVCacheWrapper(_workspace(dev), "NHD")
+    w.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev),
+           pb.kv_last_page_len.to(dev), 8, 2, 128, pb.page_size, causal=True, sm_scale=sm_scale)
+    got = w.run(a["q"].to(dev), a["cache"].to(dev))
+    want = oracle.attention(N(a["q"]), N(a["cache"]), N(pb.qo_indptr), N(pb.kv_indptr),
+                            N(pb.kv_indices), N(pb.kv_last_page_len), causal=True,
+                            sm_scale=sm_scale)
+    _tight(got, want, f"sm_scale {sm_scale}")
