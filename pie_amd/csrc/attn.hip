@@ -788,6 +788,7 @@ template <int D>
 __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
     const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv,
     const int32_t* __restrict__ qo_indptr, int G, float scale_log2, const int32_t* __restrict__ plan,
+    int n_items, int n_kv_heads,
     int mode, int window_left, const uint32_t* __restrict__ packed,
     const int64_t* __restrict__ word_off, const int32_t* __restrict__ extent,
     uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
@@ -802,9 +803,16 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
   __shared__ int window_bad;
   __shared__ uint32_t mwt[2][NT];
 
-  const int32_t* item = plan + kPlanHeader + 2 * blockIdx.x;
+  // XCD-aware order: work groups are dispatched round-robin over the 8 XCDs (id mod 8), each with
+  // its own L2, so XCD x takes the contiguous run [x * per, (x + 1) * per) of the (kv head, item)
+  // units. The plan lists each request's items together, so the work groups an XCD runs at one
+  // time mostly read the same request's K/V prefix through one L2.
+  const int units = n_items * n_kv_heads, per = (units + 7) / 8;
+  const int u = (int)(blockIdx.x & 7u) * per + (int)(blockIdx.x >> 3);
+  if (u >= units) return;
+  const int kvh = u / n_items;
+  const int32_t* item = plan + kPlanHeader + 2 * (u - kvh * n_items);
   const int b = item[0], row0 = item[1];
-  const int kvh = blockIdx.y;
   const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
   const int r32 = lane & 31, kg = lane >> 5;
   const int q0 = qo_indptr[b], qo_len = qo_indptr[b + 1] - q0;
@@ -1168,7 +1176,7 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
               "prefill_plan: head_dim %lld not in {64, 128, 256}", (long long)head_dim);
   const int64_t G = num_qo_heads / num_kv_heads;
   const int64_t kPrefillRows = head_dim == 256 ? prefill_rows<256>() : prefill_rows<128>();
-  struct Item { int32_t b, row0; int64_t work; };
+  struct Item { int32_t b, row0; int64_t work, req_work; };
   std::vector<Item> items;
   std::vector<int64_t> moff((size_t)batch + 1, 0), woff((size_t)batch + 1, 0);
   int64_t mtotal = 0, wtotal = 0;
@@ -1186,10 +1194,17 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
     for (int64_t r0 = 0; r0 < qo * G; r0 += kPrefillRows) {
       const int64_t last = std::min(qo * G, r0 + kPrefillRows) - 1;
       const int64_t seen = mode == 1 ? std::max<int64_t>(0, std::min(kv, kv - qo + last / G + 1)) : kv;
-      items.push_back(Item{(int32_t)b, (int32_t)r0, seen});
+      items.push_back(Item{(int32_t)b, (int32_t)r0, seen, kv * qo});
     }
   }
-  std::stable_sort(items.begin(), items.end(), [](const Item& x, const Item& y) { return x.work > y.work; });
+  // Each request's items stay together (they share its K/V prefix, which the kernels' XCD-aware
+  // order keeps in one L2): longest requests first, and in each request the items that see the
+  // most K/V first, so the shortest work comes last.
+  std::stable_sort(items.begin(), items.end(), [](const Item& x, const Item& y) {
+    if (x.req_work != y.req_work) return x.req_work > y.req_work;
+    if (x.b != y.b) return x.b < y.b;
+    return x.work > y.work;
+  });
   int64_t words = kPlanHeader + 2 * (int64_t)items.size();
   words = (words + 1) / 2 * 2;  // int64 mask offsets start 8-byte aligned
   moff[(size_t)batch] = mtotal;
@@ -1225,12 +1240,15 @@ static void launch_prefill(hipStream_t st, dim3 grid, const uint16_t* q, int64_t
                            int64_t o_hs) {
   // attn_prefill32_kernel scales raw scores inside the exponent, where a zero scale would turn a
   // hidden (-inf) score into NaN; 1e-30 gives the same result (every exponent rounds to 2^0).
-  if constexpr (D == 128 && PIE_PREFILL_MFMA32)
-    hipLaunchKernelGGL(attn_prefill32_kernel<128>, grid, dim3(256), 0, st, q, q_ts, q_hs, kv, qo_indptr, G,
-                       sl2 == 0.f ? 1e-30f : sl2, plan, mode, window_left, packed, woff, extent, out, o_ts, o_hs);
-  else
+  if constexpr (D == 128 && PIE_PREFILL_MFMA32) {
+    const unsigned per = (grid.x * grid.y + 7) / 8;  // (kv head, item) units per XCD
+    hipLaunchKernelGGL(attn_prefill32_kernel<128>, dim3(8 * per), dim3(256), 0, st, q, q_ts, q_hs, kv,
+                       qo_indptr, G, sl2 == 0.f ? 1e-30f : sl2, plan, (int)grid.x, (int)grid.y, mode,
+                       window_left, packed, woff, extent, out, o_ts, o_hs);
+  } else {
     hipLaunchKernelGGL(attn_prefill_kernel<D>, grid, dim3(64 * prefill_waves<D>()), 0, st, q, q_ts, q_hs, kv,
                        qo_indptr, G, sl2, plan, mode, window_left, packed, woff, extent, out, o_ts, o_hs);
+  }
 }
 
 // Visible extent of every query token under the packed mask: 1 + the last kv position whose bit
@@ -1308,7 +1326,7 @@ extern "C" int pie_hip_attention_prefill(
   PIE_REQUIRE(mode >= 0 && mode <= 2 && (mode != 2 || (packed_mask && mask_extent && mask_offsets_word > 0 &&
                                                        mask_offsets_word % 2 == 0)),
               "attention_prefill: mode %d needs the packed mask and its plan offsets", mode);
-  PIE_REQUIRE(num_items >= 0 && num_items < (1ll << 31), "attention_prefill: bad item count");
+  PIE_REQUIRE(num_items >= 0 && num_items * num_kv_heads < (1ll << 31), "attention_prefill: bad item count");
   PIE_REQUIRE(plan[2] == (head_dim == 256 ? prefill_rows<256>() : prefill_rows<128>()),
               "attention_prefill: the plan was made for another head_dim");
   PIE_REQUIRE(aligned16(q) && aligned16(out) && q_tok_stride % 8 == 0 && q_head_stride % 8 == 0 &&
