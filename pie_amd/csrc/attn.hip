@@ -500,10 +500,25 @@ template <int D>
 constexpr int prefill_rows() { return 16 * prefill_waves<D>() * prefill_row_tiles<D>(); }
 constexpr int kPlanHeader = 16;  // plan words before the items: [0] items, [1] batch, [2] rows per item
 
+// XCD-aware order of the prefill grid: work groups are dispatched round-robin over the 8 XCDs
+// (id mod 8), each with its own L2, so XCD x takes the contiguous run [x * per, (x + 1) * per) of
+// the (kv head, item) units. The plan lists each request's items together, so the work groups an
+// XCD runs at one time mostly read the same request's K/V prefix through one L2. Returns the
+// unit's plan item and sets kvh, or nullptr for the padding work groups past the last unit.
+__device__ __forceinline__ const int32_t* prefill_unit(const int32_t* plan, int n_items, int n_kv_heads,
+                                                       int& kvh) {
+  const int units = n_items * n_kv_heads, per = (units + 7) / 8;
+  const int u = (int)(blockIdx.x & 7u) * per + (int)(blockIdx.x >> 3);
+  if (u >= units) return nullptr;
+  kvh = u / n_items;
+  return plan + kPlanHeader + 2 * (u - kvh * n_items);
+}
+
 template <int D>
 __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv,
     const int32_t* __restrict__ qo_indptr, int G, float scale_log2, const int32_t* __restrict__ plan,
+    int n_items, int n_kv_heads,
     int mode, int window_left, const uint32_t* __restrict__ packed,
     const int64_t* __restrict__ word_off, const int32_t* __restrict__ extent,
     uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
@@ -518,9 +533,10 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) vo
   __shared__ __attribute__((aligned(16))) char smem[kSmem];
   __shared__ int32_t ptab[kPageWin];
 
-  const int32_t* item = plan + kPlanHeader + 2 * blockIdx.x;
+  int kvh;
+  const int32_t* item = prefill_unit(plan, n_items, n_kv_heads, kvh);
+  if (!item) return;
   const int b = item[0], row0 = item[1];
-  const int kvh = blockIdx.y;
   const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int q0 = qo_indptr[b], qo_len = qo_indptr[b + 1] - q0;
@@ -803,15 +819,9 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
   __shared__ int window_bad;
   __shared__ uint32_t mwt[2][NT];
 
-  // XCD-aware order: work groups are dispatched round-robin over the 8 XCDs (id mod 8), each with
-  // its own L2, so XCD x takes the contiguous run [x * per, (x + 1) * per) of the (kv head, item)
-  // units. The plan lists each request's items together, so the work groups an XCD runs at one
-  // time mostly read the same request's K/V prefix through one L2.
-  const int units = n_items * n_kv_heads, per = (units + 7) / 8;
-  const int u = (int)(blockIdx.x & 7u) * per + (int)(blockIdx.x >> 3);
-  if (u >= units) return;
-  const int kvh = u / n_items;
-  const int32_t* item = plan + kPlanHeader + 2 * (u - kvh * n_items);
+  int kvh;
+  const int32_t* item = prefill_unit(plan, n_items, n_kv_heads, kvh);
+  if (!item) return;
   const int b = item[0], row0 = item[1];
   const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
   const int r32 = lane & 31, kg = lane >> 5;
@@ -1240,15 +1250,15 @@ static void launch_prefill(hipStream_t st, dim3 grid, const uint16_t* q, int64_t
                            int64_t o_hs) {
   // attn_prefill32_kernel scales raw scores inside the exponent, where a zero scale would turn a
   // hidden (-inf) score into NaN; 1e-30 gives the same result (every exponent rounds to 2^0).
-  if constexpr (D == 128 && PIE_PREFILL_MFMA32) {
-    const unsigned per = (grid.x * grid.y + 7) / 8;  // (kv head, item) units per XCD
-    hipLaunchKernelGGL(attn_prefill32_kernel<128>, dim3(8 * per), dim3(256), 0, st, q, q_ts, q_hs, kv,
-                       qo_indptr, G, sl2 == 0.f ? 1e-30f : sl2, plan, (int)grid.x, (int)grid.y, mode,
-                       window_left, packed, woff, extent, out, o_ts, o_hs);
-  } else {
-    hipLaunchKernelGGL(attn_prefill_kernel<D>, grid, dim3(64 * prefill_waves<D>()), 0, st, q, q_ts, q_hs, kv,
-                       qo_indptr, G, sl2, plan, mode, window_left, packed, woff, extent, out, o_ts, o_hs);
-  }
+  const dim3 xgrid(8 * ((grid.x * grid.y + 7) / 8));  // (kv head, item) units, padded to 8 XCDs
+  if constexpr (D == 128 && PIE_PREFILL_MFMA32)
+    hipLaunchKernelGGL(attn_prefill32_kernel<128>, xgrid, dim3(256), 0, st, q, q_ts, q_hs, kv, qo_indptr, G,
+                       sl2 == 0.f ? 1e-30f : sl2, plan, (int)grid.x, (int)grid.y, mode, window_left, packed,
+                       woff, extent, out, o_ts, o_hs);
+  else
+    hipLaunchKernelGGL(attn_prefill_kernel<D>, xgrid, dim3(64 * prefill_waves<D>()), 0, st, q, q_ts, q_hs, kv,
+                       qo_indptr, G, sl2, plan, (int)grid.x, (int)grid.y, mode, window_left, packed, woff,
+                       extent, out, o_ts, o_hs);
 }
 
 // Visible extent of every query token under the packed mask: 1 + the last kv position whose bit
