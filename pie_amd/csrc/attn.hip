@@ -795,6 +795,9 @@ __device__ __forceinline__ f32x16_t mfma_32x32x16(const u32x4_t& a, const u32x4_
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
+// Scheduling group: the next `n` instructions of class `mask` (0x8 MFMA, 0x100 LDS read).
+#define sched_group(mask, n) __builtin_amdgcn_sched_group_barrier((mask), (n), 0)
+
 // V-row swizzle for this kernel's transpose reads: one read takes 4 consecutive rows x 4 chunks
 // per half-wave, so rows r..r+3 XOR chunk bits 2-3 with r mod 4.
 __device__ __forceinline__ int v32_swizzle(int r) { return (r & 3) << 2; }
@@ -925,11 +928,17 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
       for (int i = 0; i < 16; ++i) sacc[i] = 0.f;
       {
         const int z = chunk_swizzle<D>(r32);
+        // K operands read four k-steps ahead of the MFMA chain. The schedule is pinned: left to
+        // itself the compiler reads two ahead and exposes the LDS latency four times per tile.
+        u32x4_t kr[NS];
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          const u32x4_t ka = *reinterpret_cast<const u32x4_t*>(kd + r32 * D + 8 * ((2 * s + kg) ^ z));
-          sacc = mfma_32x32x16(ka, qb[s], sacc);
-        }
+        for (int s = 0; s < NS; ++s) kr[s] = *reinterpret_cast<const u32x4_t*>(kd + r32 * D + 8 * ((2 * s + kg) ^ z));
+#pragma unroll
+        for (int s = 0; s < NS; ++s) sacc = mfma_32x32x16(kr[s], qb[s], sacc);
+        sched_group(0x100, 4);
+#pragma unroll
+        for (int s = 0; s < NS - 4; ++s) { sched_group(0x008, 1); sched_group(0x100, 1); }
+        sched_group(0x008, 4);
       }
       // visibility of token tt(i) = 8(i/4) + 4kg + i%4 for this lane's row: mask bits by shifts,
       // then the per-element bounds only in tiles that cross a row's limit or window start

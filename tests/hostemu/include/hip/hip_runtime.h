@@ -255,6 +255,7 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 #define __builtin_amdgcn_global_load_lds emu::global_load_lds
 #define __builtin_amdgcn_s_waitcnt(x) ((void)(x))
 #define __builtin_amdgcn_sched_barrier(x) ((void)(x))
+#define __builtin_amdgcn_sched_group_barrier(m, n, id) ((void)(m), (void)(n), (void)(id))
 // Hardware sine / cosine of x revolutions, and the fractional part.
 inline float __builtin_amdgcn_sinf(float x) { return (float)sin(6.283185307179586 * (double)x); }
 inline float __builtin_amdgcn_cosf(float x) { return (float)cos(6.283185307179586 * (double)x); }
