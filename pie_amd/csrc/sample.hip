@@ -737,7 +737,6 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_kernel(const void
     if (sm[i] != -INFINITY) S += ss[i] * __builtin_amdgcn_exp2f((sm[i] - M) * c);
   // pass 2: write
   const float inv = 1.f / S;
-  const float mc = M * c;
   for (int v = threadIdx.x; v < nv; v += kSampThreads) {
     float x[E];
     if (greedy_row) {
@@ -746,17 +745,17 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_kernel(const void
     } else {
       IO::load(row, (int64_t)v * E, x);
 #pragma unroll
-      for (int e = 0; e < E; ++e) x[e] = __builtin_amdgcn_exp2f(fmaf(x[e], c, -mc)) * inv;
+      for (int e = 0; e < E; ++e) x[e] = __builtin_amdgcn_exp2f((x[e] - M) * c) * inv;
     }
     IO::store(orow, (int64_t)v * E, x);
   }
   for (int i = nv * E + threadIdx.x; i < V; i += kSampThreads)
-    IO::put(orow, i, greedy_row ? (i == A ? 1.f : 0.f) : __builtin_amdgcn_exp2f(fmaf(IO::get(row, i), c, -mc)) * inv);
+    IO::put(orow, i, greedy_row ? (i == A ? 1.f : 0.f) : __builtin_amdgcn_exp2f((IO::get(row, i) - M) * c) * inv);
 }
 
 // safe_scaled_softmax with the row held in registers (NV 16-byte vectors per thread, the row's
 // last V % E elements one per thread): one read and one write of the row. The maximum first (and,
-// for greedy rows, its first index), then the sum of exp2(x*c - max*c), then the write from
+// for greedy rows, its first index), then the sum of exp2((x - max)*c), then the write from
 // registers.
 __device__ __forceinline__ float block_max_f(float v, float* red) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -862,15 +861,14 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
     if (it < V) IO::put(orow, it, it == A ? 1.f : 0.f);
     return;
   }
-  const float mc = M * c;
-  float s = it < V ? __builtin_amdgcn_exp2f(fmaf(xt, c, -mc)) : 0.f;
+  float s = it < V ? __builtin_amdgcn_exp2f((xt - M) * c) : 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     if (threadIdx.x + j * kSampThreads >= nv) break;
     float x[E];
     unpack(d[j], x);
 #pragma unroll
-    for (int e = 0; e < E; ++e) s += __builtin_amdgcn_exp2f(fmaf(x[e], c, -mc));
+    for (int e = 0; e < E; ++e) s += __builtin_amdgcn_exp2f((x[e] - M) * c);
   }
   const float inv = 1.f / block_sum_f(s, red);
 #pragma unroll
@@ -880,10 +878,10 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
     float x[E];
     unpack(d[j], x);
 #pragma unroll
-    for (int e = 0; e < E; ++e) x[e] = __builtin_amdgcn_exp2f(fmaf(x[e], c, -mc)) * inv;
+    for (int e = 0; e < E; ++e) x[e] = __builtin_amdgcn_exp2f((x[e] - M) * c) * inv;
     IO::store(orow, (int64_t)v * E, x);
   }
-  if (it < V) IO::put(orow, it, __builtin_amdgcn_exp2f(fmaf(xt, c, -mc)) * inv);
+  if (it < V) IO::put(orow, it, __builtin_amdgcn_exp2f((xt - M) * c) * inv);
 }
 
 }  // namespace pie

@@ -61,8 +61,10 @@ def test_one_entry_vocabulary(dev):
                    (sampling.min_p_sampling_from_probs, {"min_p": 0.1}),
                    (sampling.top_k_top_p_sampling_from_probs, {"top_k": 1, "top_p": 0.9})):
         assert fn(probs, **kw).tolist() == [0, 0, 0]
-    out = sampling.safe_scaled_softmax(torch.randn(3, 1, device=dev), torch.tensor([0.0, 0.5, 1.0], device=dev))
-    assert out.tolist() == [[1.0], [1.0], [1.0]]
+    g = torch.Generator().manual_seed(5)
+    logits = (torch.randn(64, 1, generator=g) * 30).to(dev)
+    out = sampling.safe_scaled_softmax(logits, torch.linspace(0, 2, 64).to(dev))
+    assert out.flatten().tolist() == [1.0] * 64  # exp(x - max) = exp(0), as torch computes it
 
 
 def test_prefill_with_requests_appending_nothing(dev):
