@@ -119,18 +119,6 @@ inline uint64_t ballot(bool v) {
 
 inline int bpermute(int addr, int v) { return (int)exchange_read((uint32_t)v, (addr >> 2) & 63); }
 
-// v_permlane32_swap: lanes 32-63 of vdst trade places with lanes 0-31 of vsrc; returns
-// {new vdst, new vsrc}.
-typedef uint32_t emu_u32x2 __attribute__((ext_vector_type(2)));
-inline emu_u32x2 permlane32_swap(uint32_t vdst, uint32_t vsrc, bool, bool) {
-  const int lane = ctx->lane;
-  const uint32_t d_hi = exchange_read(vdst, (lane & 31) + 32);  // vdst of lane l + 32
-  const uint32_t s_lo = exchange_read(vsrc, lane & 31);         // vsrc of lane l - 32
-  emu_u32x2 r;
-  r[0] = lane < 32 ? vdst : s_lo;
-  r[1] = lane < 32 ? d_hi : vsrc;
-  return r;
-}
 
 inline float bf16_bits_to_float(uint16_t h) {
   uint32_t u = (uint32_t)h << 16;
@@ -262,7 +250,6 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 #define __builtin_amdgcn_exp2f exp2f
 #define __builtin_amdgcn_ballot_w64 emu::ballot
 #define __builtin_amdgcn_ds_bpermute emu::bpermute
-#define __builtin_amdgcn_permlane32_swap emu::permlane32_swap
 #define __builtin_amdgcn_mfma_f32_16x16x32_bf16 emu::mfma_16x16x32_bf16
 #define __builtin_amdgcn_mfma_f32_32x32x16_bf16 emu::mfma_32x32x16_bf16
 #define __builtin_amdgcn_ds_read_tr16_b64_v4i16 emu::ds_read_tr16_b64
