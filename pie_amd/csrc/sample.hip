@@ -440,6 +440,12 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
 // more than kWaveCands candidates in some wave's segment, sends the row to the direct passes.
 constexpr int kWaveCands = 512;
 constexpr int kCands = kWaveCands * kSampWaves;
+// The one-read top_k path: the floor comes from the row's first kHeadElems elements; it runs for
+// k <= kOnePassMaxK (about k * V / kHeadElems candidates, well inside kCands at V = 128256) and
+// rows of at least kOnePassMinV elements (shorter rows gain little from skipping a read).
+constexpr int kHeadElems = 8192;
+constexpr int kOnePassMaxK = 256;
+constexpr int kOnePassMinV = 65536;
 
 struct alignas(16) CandShared {
   float val[kCands];  // the per-thread tops (pass A), then the candidates
@@ -562,8 +568,71 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
   bool svec = vec;
   int64_t npos = -1;
   uint64_t row_tot = 0;
+  // Copies the elements that satisfy pred into the candidate list and closes the gaps between
+  // the wave segments; false (and the list unused) when some segment overflowed.
+  auto gather = [&](auto&& pred) -> bool {
+    const int n = compact_segment(p, V, vec, pred, cs);
+    if (lane == 0) cs.wn[w] = n;
+    __syncthreads();
+    int total = 0;
+    bool over = false;
+    for (int i = 0; i < kSampWaves; ++i) {
+      over |= cs.wn[i] > kWaveCands;
+      total += cs.wn[i];
+    }
+    if (over) return false;
+    // close the gaps between the segments' lists (moves go to lower slots: read, then write)
+    constexpr int J = kCands / kSampThreads;
+    float mv[J];
+    uint32_t mi[J];
+    int md[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int s = threadIdx.x + j * kSampThreads;
+      const int sw = s / kWaveCands, so = s % kWaveCands;
+      int base = 0;
+      for (int i = 0; i < sw; ++i) base += cs.wn[i];
+      md[j] = so < cs.wn[sw] ? base + so : -1;
+      mv[j] = cs.val[s];
+      mi[j] = cs.idx[s];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (md[j] >= 0) { cs.val[md[j]] = mv[j]; cs.idx[md[j]] = mi[j]; }
+    sp = cs.val;
+    sidx = cs.idx;
+    sV = total;
+    svec = true;
+    return true;
+  };
+  bool listed = false;
+  // One read for top_k (alone or before top_p) with a small k over a long row: the k-th largest
+  // of the row's first kHeadElems elements is a floor under the row's k-th largest, so one pass
+  // collects every element at or above it (about k * V / kHeadElems of them for exchangeable
+  // rows) and counts the row's p > 0 on the way. Overflow falls back to the two passes below.
+  if ((mode == 2 || mode == 4) && vec && k > 0 && k <= kOnePassMaxK && V >= kOnePassMinV) {
+#pragma unroll
+    for (int j = 0; j < kHeadElems / 4 / kSampThreads; ++j) {
+      const int v = threadIdx.x + j * kSampThreads;
+      *reinterpret_cast<float4*>(cs.val + 4 * v) = *reinterpret_cast<const float4*>(p + 4 * v);
+    }
+    __syncthreads();
+    const uint32_t floor0 = radix_threshold(cs.val, kHeadElems, true, 1u, false, (uint32_t)k, 0.0, sh);
+    __syncthreads();  // the head copy is dead from here: its memory holds the candidates
+    if (floor0 > 1u) {
+      uint32_t c = 0;
+      listed = gather([&](int, float x) {
+        const uint32_t key = prob_key(x);
+        c += key != 0u;
+        return key >= floor0;
+      });
+      npos = (int64_t)block_sum_u64(c, sh);
+      __syncthreads();
+    }
+  }
   // plain sampling, and top_k with k outside (0, V), keep every p > 0: no candidate list
-  if (!(mode == 0 || ((mode == 2 || mode == 4) && !(k > 0 && k < V)))) {
+  if (!listed && !(mode == 0 || ((mode == 2 || mode == 4) && !(k > 0 && k < V)))) {
     // pass A
     bool lists = true;
     uint32_t cand_lo = 1u;  // candidates: key >= cand_lo (top_k, top_p) or x >= mthr (min_p)
@@ -594,44 +663,10 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
       __syncthreads();  // the tops are dead from here: their memory holds the candidates
     }
     if (lists) {
-      // pass B
-      const int n = compact_segment(p, V, vec, [&](int, float x) {
+      // pass B (with too many candidates in some segment, the direct passes run over the row)
+      gather([&](int, float x) {
         return mode == 3 ? (prob_key(x) != 0 && (double)x >= mthr) : prob_key(x) >= cand_lo;
-      }, cs);
-      if (lane == 0) cs.wn[w] = n;
-      __syncthreads();
-      int total = 0;
-      bool over = false;
-      for (int i = 0; i < kSampWaves; ++i) {
-        over |= cs.wn[i] > kWaveCands;
-        total += cs.wn[i];
-      }
-      // with too many candidates in some segment, the direct passes run over the row
-      if (!over) {
-        // close the gaps between the segments' lists (moves go to lower slots: read, then write)
-        constexpr int J = kCands / kSampThreads;
-        float mv[J];
-        uint32_t mi[J];
-        int md[J];
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-          const int s = threadIdx.x + j * kSampThreads;
-          const int sw = s / kWaveCands, so = s % kWaveCands;
-          int base = 0;
-          for (int i = 0; i < sw; ++i) base += cs.wn[i];
-          md[j] = so < cs.wn[sw] ? base + so : -1;
-          mv[j] = cs.val[s];
-          mi[j] = cs.idx[s];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < J; ++j)
-          if (md[j] >= 0) { cs.val[md[j]] = mv[j]; cs.idx[md[j]] = mi[j]; }
-        sp = cs.val;
-        sidx = cs.idx;
-        sV = total;
-        svec = true;
-      }
+      });
     }
     __syncthreads();
   }
@@ -922,21 +957,21 @@ extern "C" int pie_hip_scaled_softmax(const void* logits, int32_t is_bf16, int64
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t e = is_bf16 ? 8 : 4;  // elements per 16-byte vector
   const int vec = aligned16(logits) && aligned16(out) && stride % e == 0 && out_stride % e == 0;
-  // rows of up to 20 vectors per thread stay in registers (bf16: 163,840 entries; fp32: 81,920)
+  // rows of up to 20 vectors per thread stay in registers for bf16 (163,840 entries), 16 for fp32
+  // (65,536 entries: at 20 the fp32 kernel's registers spill)
   const int64_t per_thread = (vocab / e + kSampThreads - 1) / kSampThreads;
   const dim3 grid((unsigned)batch), block(kSampThreads);
 #define PIE_SOFTMAX_RESIDENT(BF, NV)                                                                      \
   hipLaunchKernelGGL((scaled_softmax_resident_kernel<BF, NV>), grid, block, 0, st, logits, stride, (int)vocab, \
                      temperatures, greedy_threshold, out, out_stride)
-  if (vec && per_thread <= 20) {
+  if (vec && per_thread <= (is_bf16 ? 20 : 16)) {
     if (is_bf16) {
       if (per_thread <= 8) PIE_SOFTMAX_RESIDENT(true, 8);
       else if (per_thread <= 16) PIE_SOFTMAX_RESIDENT(true, 16);
       else PIE_SOFTMAX_RESIDENT(true, 20);
     } else {
       if (per_thread <= 8) PIE_SOFTMAX_RESIDENT(false, 8);
-      else if (per_thread <= 16) PIE_SOFTMAX_RESIDENT(false, 16);
-      else PIE_SOFTMAX_RESIDENT(false, 20);
+      else PIE_SOFTMAX_RESIDENT(false, 16);
     }
   } else if (is_bf16) {
     hipLaunchKernelGGL(scaled_softmax_kernel<true>, grid, block, 0, st, logits, stride, (int)vocab, temperatures,

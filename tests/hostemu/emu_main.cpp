@@ -484,16 +484,19 @@ static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
 // so kept sets and draws must match the oracle exactly; ties are forced in some rows.
 // peaked: p = softmax of N(0, 3) logits (a few dominant tokens, as after an LM head) with k up to
 // 64, so the candidate lists are short; otherwise near-uniform rows whose lists can overflow.
-static void case_sample(int64_t B, int64_t V, int mode, bool row_map, bool peaked = false, int64_t pad = 0) {
-  printf("sample B=%lld V=%lld mode=%d rows=%d peaked=%d pad=%lld\n", (long long)B, (long long)V, mode,
-         (int)row_map, (int)peaked, (long long)pad);
+static void case_sample(int64_t B, int64_t V, int mode, bool row_map, bool peaked = false, int64_t pad = 0,
+                        int64_t zero_head = 0) {
+  printf("sample B=%lld V=%lld mode=%d rows=%d peaked=%d pad=%lld zero_head=%lld\n", (long long)B, (long long)V,
+         mode, (int)row_map, (int)peaked, (long long)pad, (long long)zero_head);
   Buf<float> probs(B * V);
   std::uniform_int_distribution<int> dq(0, 1 << 12);
   std::normal_distribution<double> dn(0.0, 3.0);
   for (int64_t r = 0; r < B; ++r) {
     double tot = 0;
     for (int64_t i = 0; i < V; ++i) {
-      probs[r * V + i] = peaked ? (float)(exp(dn(rng)) * 1024.0) : (float)dq(rng);
+      // zero_head > 0: the first zero_head entries are 0; < 0: the first -zero_head are tiny
+      probs[r * V + i] = i < zero_head ? 0.f : i < -zero_head ? 50.f
+                         : peaked ? (float)(exp(dn(rng)) * 1024.0) : (float)dq(rng);
       tot += probs[r * V + i];
     }
     if (r % 3 == 1) for (int64_t i = 0; i < V; i += 7) probs[r * V + i] = probs[r * V];  // ties
@@ -641,6 +644,13 @@ int main(int argc, char** argv) {
     case_sample(2, 10003, 4, false, true, 1);  // 16-byte rows whose length is not a multiple of 4
     case_sample(2, 10001, 3, false, true, 3);
     case_sample(1, 40000, 1, false);        // top_p lists that overflow: direct passes
+    // top_k over long rows: one read with a floor from the first 8192 entries (a row of ties
+    // overflows the list and falls back; a head with fewer than k positives does too)
+    case_sample(4, 70000, 2, false, true);
+    case_sample(4, 70000, 4, false, true);
+    case_sample(3, 70000, 4, false, true, 0, 8192);
+    case_sample(3, 70000, 2, false, true, 0, 8190);
+    case_sample(3, 70000, 4, false, true, 0, -8192);  // a low floor: the list overflows
     // (rows of more than 256 tiles, whose draw chunks span several tiles, run in the GPU tests)
     case_softmax(3, 1000, false);
     case_softmax(3, 777, true);
