@@ -209,3 +209,32 @@ def test_sampling_chain_like_pie(dev):
     assert tok.dtype == torch.int32 and tok.shape == (B,)
     assert int(tok[0]) == int(logits[0].argmax())  # greedy row
     assert ((tok >= 0) & (tok < V)).all()
+
+
+@pytest.mark.parametrize("mode", ["top_k", "top_k_top_p"])
+@pytest.mark.parametrize("head", ["plain", "zero", "tiny", "large"])
+def test_sample_top_k_one_read_and_fallbacks(dev, mode, head):
+    """top_k with small k over a long row takes its floor from the row's first 8192 entries:
+    an ordinary head (one read), a head of zeros (fewer than k positives there: the two-pass
+    path), a head of tiny positives (the floor admits almost the whole row: the candidate list
+    overflows and the two-pass path runs) and a head holding the row's largest entries."""
+    print(f"sample {mode} head={head}", flush=True)
+    B, V = 12, 128256
+    g = torch.Generator().manual_seed(91)
+    w = torch.randint(1, 4097, (B, V), generator=g).double() ** 2
+    if head == "zero":
+        w[:, :8192] = 0
+    elif head == "tiny":
+        w[:, :8192] = 1e3
+    elif head == "large":
+        w[:, :8192] *= 64
+    p = (torch.floor(w / w.sum(-1, keepdim=True) * 2**30) / 2**30).float()
+    prm = _params(B, V, 92)
+    prm["top_k"] = torch.randint(1, 257, (B,), generator=g).to(torch.int32)
+    prm["top_k"][1] = 256
+    dp = {k: v.to(dev) for k, v in prm.items()}
+    got = _call(mode, p.to(dev), dp, uniforms=dp["u"]).cpu().numpy()
+    want, kept = oracle.sample(p.numpy(), mode, prm["u"].numpy(), top_k=prm["top_k"].numpy(),
+                               top_p=prm["top_p"].numpy(), min_p=prm["min_p"].numpy())
+    assert kept[np.arange(B), got].all()
+    assert (got == want).all(), f"{got} vs {want}"
