@@ -16,7 +16,9 @@
 // gives the same kept set and the same sample.
 // Two row reads in the common case: pass A finds a floor under the threshold (from each thread's
 // two largest keys, or the row maximum for min_p), pass B copies the elements above it into LDS
-// in vocabulary order, and the radix selects and the draw run over that short list. Plain
+// in vocabulary order, and the radix selects and the draw run over that short list. top_k with a
+// small k over a long row needs one read: the k-th largest of the row's first 8192 entries is
+// already a floor, so the list is built in the same pass that counts the row's p > 0. Plain
 // sampling, and rows whose list would not fit, take the direct passes over the row.
 // Draw: inverse CDF in index order over the kept tokens, target u * kept mass, with u from
 // Philox4x32-10 (counter = (offset, row), key = seed) or caller-given uniforms; the kept-mass
