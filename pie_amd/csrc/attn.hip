@@ -514,12 +514,35 @@ __device__ __forceinline__ const int32_t* prefill_unit(const int32_t* plan, int 
   return plan + kPlanHeader + 2 * (u - kvh * n_items);
 }
 
+// attn_mask_extent_kernel marks a query token whose mask row is exactly causal (positions
+// 0..kv_len - qo_len + i, nothing else) with this bit of its extent.
+constexpr int kExtentCausal = 1 << 30;
+
+// Custom-mask prologue: the furthest position any of the work group's nrows rows (from row0) can
+// see, and whether every one of those rows' masks is exactly causal (then the causal path serves
+// them without reading mask words). Every thread of the work group calls it.
+__device__ __forceinline__ void mask_rows_extent(const int32_t* __restrict__ extent, int q0, int row0, int rows,
+                                                 int G, int nrows, int& ext, bool& causal) {
+  __shared__ int s_ext, s_mixed;
+  if (threadIdx.x == 0) { s_ext = 0; s_mixed = 0; }
+  __syncthreads();
+  const int r = row0 + (int)threadIdx.x;
+  if ((int)threadIdx.x < nrows && r < rows) {
+    const int e = extent[q0 + r / G];
+    atomicMax(&s_ext, e & ~kExtentCausal);
+    if (!(e & kExtentCausal)) atomicOr(&s_mixed, 1);
+  }
+  __syncthreads();
+  ext = s_ext;
+  causal = s_mixed == 0;
+}
+
 template <int D>
 __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv,
     const int32_t* __restrict__ qo_indptr, int G, float scale_log2, const int32_t* __restrict__ plan,
     int n_items, int n_kv_heads,
-    int mode, int window_left, const uint32_t* __restrict__ packed,
+    int mode_in, int window_left, const uint32_t* __restrict__ packed,
     const int64_t* __restrict__ word_off, const int32_t* __restrict__ extent,
     uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
   using W = WaveAttn<D>;
@@ -543,6 +566,12 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) vo
   const int kv_len = kv_length(kv, b);
   const int rows = qo_len * G;
   const int page0 = kv.indptr[b];
+  int mode = mode_in, mext = 0;  // a custom mask that is causal for all the rows: the causal path
+  if (mode_in == 2) {
+    bool causal;
+    mask_rows_extent(extent, q0, row0, rows, G, kPrefillRows, mext, causal);
+    mode = uniform(causal ? 1 : 2);  // wave-uniform (a scalar register), like the argument
+  }
 
   // this lane's query rows (row n of each of the wave's row tiles)
   W st[RT];
@@ -567,15 +596,7 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) vo
   // rows' query tokens, from attn_mask_extent_kernel)
   const int last_row = min(rows, row0 + kPrefillRows) - 1;
   int kv_end = mode == 1 ? min(kv_len, kv_len - qo_len + last_row / G + 1) : kv_len;
-  if (mode == 2) {
-    __shared__ int wg_extent;
-    if (threadIdx.x == 0) wg_extent = 0;
-    __syncthreads();
-    const int r = row0 + (int)threadIdx.x;
-    if ((int)threadIdx.x < kPrefillRows && r < rows) atomicMax(&wg_extent, extent[q0 + r / G]);
-    __syncthreads();
-    kv_end = min(kv_len, wg_extent);
-  }
+  if (mode == 2) kv_end = min(kv_len, mext);
   // sliding window: no row of the work group sees positions before its first row's window
   // (tiles start 32-aligned so mask words line up)
   const int kv_begin = window_left >= 0 ? max(0, kv_len - qo_len + row0 / G - window_left) & ~31 : 0;
@@ -808,7 +829,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
     const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv,
     const int32_t* __restrict__ qo_indptr, int G, float scale_log2, const int32_t* __restrict__ plan,
     int n_items, int n_kv_heads,
-    int mode, int window_left, const uint32_t* __restrict__ packed,
+    int mode_in, int window_left, const uint32_t* __restrict__ packed,
     const int64_t* __restrict__ word_off, const int32_t* __restrict__ extent,
     uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
   static_assert(D == 128, "32x32 prefill is built for head_dim 128");
@@ -832,6 +853,12 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
   const int kv_len = kv_length(kv, b);
   const int rows = qo_len * G;
   const int page0 = kv.indptr[b];
+  int mode = mode_in, mext = 0;  // a custom mask that is causal for all the rows: the causal path
+  if (mode_in == 2) {
+    bool causal;
+    mask_rows_extent(extent, q0, row0, rows, G, kRows, mext, causal);
+    mode = uniform(causal ? 1 : 2);  // wave-uniform (a scalar register), like the argument
+  }
 
   // this lane's query row
   const int R = row0 + 32 * w + r32;
@@ -857,15 +884,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
 
   const int last_row = min(rows, row0 + kRows) - 1;
   int kv_end = mode == 1 ? min(kv_len, kv_len - qo_len + last_row / G + 1) : kv_len;
-  if (mode == 2) {
-    __shared__ int wg_extent;
-    if (threadIdx.x == 0) wg_extent = 0;
-    __syncthreads();
-    const int rr = row0 + (int)threadIdx.x;
-    if ((int)threadIdx.x < kRows && rr < rows) atomicMax(&wg_extent, extent[q0 + rr / G]);
-    __syncthreads();
-    kv_end = min(kv_len, wg_extent);
-  }
+  if (mode == 2) kv_end = min(kv_len, mext);
   const int kv_begin = window_left >= 0 ? max(0, kv_len - qo_len + row0 / G - window_left) & ~31 : 0;
   const int nw = (kv_len + 31) / 32;
   const uint32_t* mword = mode == 2 ? packed + word_off[b] + (int64_t)tok * nw : nullptr;
@@ -1204,7 +1223,7 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
     const int64_t np = (int64_t)kv_indptr[b + 1] - kv_indptr[b];
     PIE_REQUIRE(qo >= 0 && np >= 0, "prefill_plan: indptr decreases at request %lld", (long long)b);
     const int64_t kv = np > 0 ? (np - 1) * page_size + kv_last_page_len[b] : 0;
-    PIE_REQUIRE(kv >= 0 && kv < (1ll << 31) && qo * G < (1ll << 31),
+    PIE_REQUIRE(kv >= 0 && kv < (mode == 2 ? kExtentCausal : (1ll << 31)) && qo * G < (1ll << 31),
                 "prefill_plan: request %lld too long", (long long)b);
     moff[(size_t)b] = mtotal;
     woff[(size_t)b] = wtotal;
@@ -1271,7 +1290,8 @@ static void launch_prefill(hipStream_t st, dim3 grid, const uint16_t* q, int64_t
 }
 
 // Visible extent of every query token under the packed mask: 1 + the last kv position whose bit
-// is set (0 if none). One thread per query token, scanning its words from the end.
+// is set (0 if none), with kExtentCausal set when the row is exactly causal. One thread per query
+// token, scanning its words from the end (and, for the causal test, from the start).
 __global__ __launch_bounds__(256) void attn_mask_extent_kernel(const uint32_t* __restrict__ packed,
                                                                const int32_t* __restrict__ plan,
                                                                const int32_t* __restrict__ qo_indptr,
@@ -1286,12 +1306,19 @@ __global__ __launch_bounds__(256) void attn_mask_extent_kernel(const uint32_t* _
     if (qo_indptr[mid] <= j) lo = mid; else hi = mid - 1;
   }
   const int b = lo, i = j - qo_indptr[b];
-  const int nw = (kv_length(kv, b) + 31) / 32;
+  const int kv_len = kv_length(kv, b);
+  const int nw = (kv_len + 31) / 32;
   const uint32_t* row = packed + woff[b] + (int64_t)i * nw;
   int e = 0;
   for (int w = nw - 1; w >= 0; --w)
     if (row[w]) { e = 32 * w + 32 - __builtin_clz(row[w]); break; }
-  extent[j] = e;
+  // exactly causal: the extent is the causal one and every bit below it is set
+  bool causal = e == kv_len - (qo_indptr[b + 1] - qo_indptr[b]) + i + 1;
+  for (int w = 0; causal && 32 * w < e; ++w) {
+    const int n = min(32, e - 32 * w);
+    causal = row[w] == (n == 32 ? 0xffffffffu : (1u << n) - 1u);
+  }
+  extent[j] = e | (causal ? kExtentCausal : 0);
 }
 
 // Bit-packs the custom mask: one thread per 32-bit word (query token i of request b, kv

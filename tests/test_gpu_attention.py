@@ -238,6 +238,31 @@ def test_prefill_pie_causal_mask_equals_causal_mode(dev):
     assert torch.equal(by_mask.view(torch.int16), by_mode.view(torch.int16))
 
 
+@pytest.mark.parametrize("D", [128, 64])
+def test_prefill_nearly_causal_masks(dev, D):
+    """Causal masks with a few bits changed (a hidden past position, a visible future one, a row
+    cut short): work groups whose rows are all exactly causal take the causal path, the others
+    read the mask; every row matches the oracle under the mask as given."""
+    print(f"nearly causal D={D}", flush=True)
+    a = wl.attn_batch(torch.tensor([0, 40, 333, 7, 0]), torch.tensor([130, 5, 64, 1, 70]), Hq=16,
+                      Hkv=4, D=D, page_size=16, seed=101)
+    pb = a["batch"]
+    mask = _brle_causal_mask(pb).clone()
+    starts = torch.cat([torch.zeros(1, dtype=torch.int64),
+                        torch.cumsum(pb.lens.to(torch.int64) * pb.seq_lens.to(torch.int64), 0)])
+    kv = [int(x) for x in pb.seq_lens]
+    mask[int(starts[0]) + 97 * kv[0] + 3] = False            # request 0, row 97: a hidden past position
+    mask[int(starts[2]) + 0 * kv[2] + kv[2] - 1] = True      # request 2, row 0: a visible future one
+    r4 = int(starts[4]) + 40 * kv[4]
+    mask[r4 + 20: r4 + 41] = False                            # request 4, row 40: cut short
+    want = _want(a, custom=mask.numpy(), causal=False)
+    got = _prefill(dev, a, custom=mask)
+    assert_bf16_close(N(got), want, what="nearly causal")
+    _tight(got, want, "nearly causal")
+    exact = _prefill(dev, a, custom=_brle_causal_mask(pb))
+    _tight(exact, _want(a), "exactly causal")
+
+
 def test_prefill_decode_rows_match_decode_wrapper(dev):
     """One query token per request: prefill (causal) and decode agree within bf16 rounding."""
     a = wl.attn_batch(torch.randint(0, 900, (7,), generator=torch.Generator().manual_seed(3)),
