@@ -125,3 +125,23 @@ def test_integration_installs_flashinfer_namespace():
     finally:
         integration.uninstall()
     assert "flashinfer" not in sys.modules and "flashinfer.sampling" not in sys.modules
+
+
+def test_prefill_plan_position_limits_without_a_gpu():
+    """The prefill plan (host code) takes requests of up to 2^31 - 1 positions, and up to
+    2^30 - 1 under a custom mask (the extent kernel marks exactly causal rows in bit 30)."""
+    def plan(kv_len, mode):
+        pages = (kv_len + 15) // 16
+        qo = np.array([0, 1], dtype=np.int32)
+        kv = np.array([0, pages], dtype=np.int32)
+        last = np.array([kv_len - 16 * (pages - 1)], dtype=np.int32)
+        buf = np.zeros(64, dtype=np.int32)
+        out = [C.c_int64(0) for _ in range(4)]
+        return _rc("pie_hip_attention_prefill_plan", qo.ctypes.data, kv.ctypes.data, last.ctypes.data,
+                   1, 16, 8, 2, 128, mode, buf.ctypes.data, buf.size, *[C.byref(o) for o in out])
+    assert plan((1 << 30) - 1, 2)[0] == 0
+    rc, msg = plan(1 << 30, 2)
+    assert rc == 1 and "too long" in msg
+    assert plan(1 << 30, 1)[0] == 0
+    rc, msg = plan((1 << 31) - 1 + 16, 1)
+    assert rc == 1
