@@ -297,6 +297,24 @@ int pie_hip_attention_decode(const pie_bf16* q, int64_t q_tok_stride, int64_t q_
 
 
 /*
+ * pie_hip_attention_decode without a workspace argument and without any allocation: the split
+ * partials go to a static device array of 32 MiB held by each GPU the library runs on until the
+ * process ends (need = batch * splits * num_qo_heads * (head_dim + 1) * 4 bytes when splits > 1;
+ * larger requests return PIE_HIP_EINVAL). Results equal pie_hip_attention_decode's bit for bit.
+ * No counterpart in the reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops). Calls that overlap on one GPU share the array and race.
+ */
+int pie_hip_attention_decode_noalloc(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                     const pie_bf16* k_cache, const pie_bf16* v_cache,
+                                     int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                                     int64_t num_pages, const int32_t* kv_indptr,
+                                     const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                                     int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
+                                     int64_t head_dim, int64_t page_size, float sm_scale,
+                                     int64_t window_left, int64_t splits, pie_bf16* out,
+                                     int64_t o_tok_stride, int64_t o_head_stride, void* stream);
+
+/*
  * Paged attention, prefill form: ragged query tokens per request (qo_indptr [B+1]), each
  * request's query tokens being its last qo_len positions. Query token i of request b attends
  * kv position t < kv_len when: mode 0 always (flashinfer's default, causal=False), mode 1

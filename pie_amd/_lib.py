@@ -48,6 +48,8 @@ SIGNATURES: dict[str, list] = {
     "pie_hip_attention_decode_plan": [i64, i64, i64, i64, vp],
     "pie_hip_attention_decode": [vp, i64, i64, vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, i64,
                                  i64, i64, i64, f32, i64, i64, vp, i64, vp, i64, i64, vp],
+    "pie_hip_attention_decode_noalloc": [vp, i64, i64, vp, vp, i64, i64, i64, i64, vp, vp, vp, i64,
+                                         i64, i64, i64, i64, f32, i64, i64, vp, i64, i64, vp],
     "pie_hip_attention_prefill_plan": [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp, i64, vp, vp,
                                        vp, vp],
     "pie_hip_attention_pack_mask": [vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp],

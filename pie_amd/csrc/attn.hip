@@ -25,6 +25,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -1141,18 +1142,18 @@ static void launch_decode(hipStream_t st, const uint16_t* q, int64_t q_ts, int64
                        st, B, Hq, splits, po, pl, out, o_ts, o_hs);
 }
 
-extern "C" int pie_hip_attention_decode(
+static int attention_decode_impl(
     const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride, const pie_bf16* k_cache,
     const pie_bf16* v_cache, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
     int64_t num_pages, const int32_t* kv_indptr, const int32_t* kv_indices,
     const int32_t* kv_last_page_len, int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
     int64_t head_dim, int64_t page_size, float sm_scale, int64_t window_left, int64_t splits,
     void* workspace, int64_t workspace_bytes, pie_bf16* out, int64_t o_tok_stride,
-    int64_t o_head_stride, void* stream) {
+    int64_t o_head_stride, void* stream, const char* what) {
   PagedKV kv;
   int rc = paged_kv_desc(&kv, k_cache, v_cache, page_stride, slot_stride, head_stride, num_pages,
                          kv_indptr, kv_indices, kv_last_page_len, page_size, head_dim,
-                         "attention_decode");
+                         what);
   if (rc) return rc;
   PIE_REQUIRE(q && out, "attention_decode: null q or out");
   PIE_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
@@ -1169,7 +1170,7 @@ extern "C" int pie_hip_attention_decode(
   const int64_t slots = splits > 1 ? batch * splits : 0;
   const int64_t need = slots * num_qo_heads * (head_dim + 1) * 4;
   PIE_REQUIRE(slots == 0 || (workspace && workspace_bytes >= need && aligned16(workspace)),
-              "attention_decode: workspace of %lld bytes < %lld needed for %lld splits",
+              "%s: workspace of %lld bytes < %lld needed for %lld splits", what,
               (long long)workspace_bytes, (long long)need, (long long)splits);
   if (batch == 0) return PIE_HIP_OK;
   float* po = static_cast<float*>(workspace);
@@ -1187,7 +1188,80 @@ extern "C" int pie_hip_attention_decode(
     default: launch_decode<256>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, W, out,
                                 o_tok_stride, o_head_stride, po, pl); break;
   }
-  return check_launch("attention_decode");
+  return check_launch(what);
+}
+
+extern "C" int pie_hip_attention_decode(
+    const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride, const pie_bf16* k_cache,
+    const pie_bf16* v_cache, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+    int64_t num_pages, const int32_t* kv_indptr, const int32_t* kv_indices,
+    const int32_t* kv_last_page_len, int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
+    int64_t head_dim, int64_t page_size, float sm_scale, int64_t window_left, int64_t splits,
+    void* workspace, int64_t workspace_bytes, pie_bf16* out, int64_t o_tok_stride,
+    int64_t o_head_stride, void* stream) {
+  return attention_decode_impl(q, q_tok_stride, q_head_stride, k_cache, v_cache, page_stride,
+                               slot_stride, head_stride, num_pages, kv_indptr, kv_indices,
+                               kv_last_page_len, batch, num_qo_heads, num_kv_heads, head_dim,
+                               page_size, sm_scale, window_left, splits, workspace, workspace_bytes,
+                               out, o_tok_stride, o_head_stride, stream, "attention_decode");
+}
+
+// ---------------------------------------------------------------- decode without allocation
+// The split partials (fp32 outputs + log2-sum-exp per (slot, head)) live in a file-scope device
+// array instead of a caller workspace, for callers that cannot allocate. Each device holds its
+// own copy; host code uses only the address hipGetSymbolAddress returns for the current device
+// (the array's name is a host-side stand-in, never a device address). Every partial a run
+// reads is written earlier in the same run (empty splits write zeros and -inf), so the array
+// needs no clearing between calls; calls that overlap on one device race on it.
+constexpr int64_t kDecodeScratchBytes = 32ll << 20;
+static __device__ __align__(256) char scratch[kDecodeScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[64] = {nullptr};
+
+static int decode_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64)
+    return set_error(PIE_HIP_ELAUNCH, "attention_decode_noalloc: no current device (%s)", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(PIE_HIP_ELAUNCH, "attention_decode_noalloc: hipGetSymbolAddress failed on device %d: %s",
+                       dev, hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return PIE_HIP_OK;
+}
+
+extern "C" int pie_hip_attention_decode_noalloc(
+    const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride, const pie_bf16* k_cache,
+    const pie_bf16* v_cache, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+    int64_t num_pages, const int32_t* kv_indptr, const int32_t* kv_indices,
+    const int32_t* kv_last_page_len, int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
+    int64_t head_dim, int64_t page_size, float sm_scale, int64_t window_left, int64_t splits,
+    pie_bf16* out, int64_t o_tok_stride, int64_t o_head_stride, void* stream) {
+  const char* what = "attention_decode_noalloc";
+  PIE_REQUIRE(batch >= 0 && splits >= 1 && splits <= 64 && num_qo_heads > 0 && head_dim > 0,
+              "%s: bad batch %lld / splits %lld", what, (long long)batch, (long long)splits);
+  const int64_t need = splits > 1 ? batch * splits * num_qo_heads * (head_dim + 1) * 4 : 0;
+  PIE_REQUIRE(need <= kDecodeScratchBytes,
+              "%s: %lld bytes of split partials exceed the %lld-byte static scratch (use fewer splits "
+              "or pie_hip_attention_decode with a workspace)",
+              what, (long long)need, (long long)kDecodeScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = decode_scratch(&ws);
+    if (rc) return rc;
+  }
+  return attention_decode_impl(q, q_tok_stride, q_head_stride, k_cache, v_cache, page_stride,
+                               slot_stride, head_stride, num_pages, kv_indptr, kv_indices,
+                               kv_last_page_len, batch, num_qo_heads, num_kv_heads, head_dim,
+                               page_size, sm_scale, window_left, splits, ws, kDecodeScratchBytes,
+                               out, o_tok_stride, o_head_stride, stream, what);
 }
 
 // Host: the prefill work list. Reads host copies of qo_indptr, kv_indptr and kv_last_page_len
