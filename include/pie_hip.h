@@ -240,6 +240,27 @@ int pie_hip_qk_rmsnorm_rope_append(const pie_bf16* q, int64_t q_tok_stride, int6
                                    int64_t page_size, void* stream);
 
 /*
+ * Grouped launch of independent per-layer ops: after pie_hip_group_begin, calls on this thread
+ * of pie_hip_embedding, pie_hip_fused_add_rmsnorm, pie_hip_silu_and_mul,
+ * pie_hip_gelu_tanh_and_mul and pie_hip_qk_rmsnorm_rope_append validate their arguments and are
+ * recorded (at most 8) instead of launched; pie_hip_group_end(stream) launches them, all on
+ * `stream` (every recorded call must name that stream), as ONE kernel whose block ranges run
+ * one q/k prologue, one add + RMSNorm (cols = 512, 1024, 2048 or 4096) and one gated activation
+ * side by side; whatever does not fit is launched after it as its own kernel. Results equal the
+ * separate calls' bit for bit. The recorded ops must be independent, with one exception: an
+ * embedding whose output is the x of a recorded add + RMSNorm (same rows, cols and row stride)
+ * runs fused into it, as the sequence embedding -> add -> norm. Any other overlap between one
+ * op's outputs and another op's operands makes pie_hip_group_end fail without launching. Other
+ * entry points called inside a group launch immediately. The group closes at
+ * pie_hip_group_end even when it fails.
+ * No single reference function: it replaces consecutive launches of the ops above in a decode
+ * step (pie/src/pie_worker/model/qwen3.py:468-472, :571 -> :538, :651-684, :553-556), which the
+ * reference issues one kernel each.
+ */
+int pie_hip_group_begin(void);
+int pie_hip_group_end(void* stream);
+
+/*
  * seq_lens[b] = (kv_indptr[b+1]-kv_indptr[b]-1)*page_size + last_page_len[b], or 0 when the
  * request holds no page. Replaces flashinfer.get_seq_lens (llama3.py:745-749;
  * spec pie/src/flashinfer_metal/ops.py:392-407).

@@ -58,6 +58,8 @@ SIGNATURES: dict[str, list] = {
                                   vp],
     "pie_hip_sample": [vp, i64, i64, i64, i64, vp, i32, vp, i32, vp, f32, vp, f32, vp, u64, u64, vp, vp],
     "pie_hip_scaled_softmax": [vp, i32, i64, i64, i64, vp, f32, vp, i64, vp],
+    "pie_hip_group_begin": [],
+    "pie_hip_group_end": [vp],
     "pie_hip_get_seq_lens": [vp, vp, i64, i64, vp, vp],
     "pie_hip_get_batch_indices_positions": [vp, vp, i64, i64, vp, vp, vp],
 }

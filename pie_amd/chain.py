@@ -8,6 +8,9 @@ out (they are not part of this path):
   (4) RoPE at each sequence's position and (5) paged-KV append   qwen3.py:665-684
       (fused=True runs (3)-(5) as one kernel, fused=False as three launches)
   (6) SiLU-and-mul                qwen3.py:553-556
+grouped=True (implies the fused prologue) records the ops in ops.op_group(), so the whole chain
+is ONE kernel launch: the embedding gather runs fused into the residual add + RMSNorm, and the
+q/k prologue and SiLU-and-mul, which do not depend on them here, run in their own block ranges.
 All buffers are preallocated, so ``run()`` launches kernels only and can be captured into a
 HIP graph (``capture()``), as the reference captures its decode layers (llama3.py:315-414).
 """
@@ -20,14 +23,18 @@ from . import workloads as wl
 
 
 class DecodeChain:
-    def __init__(self, cfg: dict, device, fused: bool = True):
+    def __init__(self, cfg: dict, device, fused: bool = True, grouped: bool = False,
+                 share: "DecodeChain | None" = None):
+        """share: take the embedding table and the paged cache of another chain (several chains
+        over their own activations, as the layers of one decode step share a cache pool)."""
         d = device
         self.cfg = cfg
-        self.fused = fused
+        self.fused = fused or grouped
+        self.grouped = grouped
         self.Hq, self.Hkv, self.D = cfg["Hq"], cfg["Hkv"], cfg["D"]
         self.eps, self.theta = cfg["eps"], cfg["theta"]
         pb = cfg["batch"]
-        self.W = cfg["W"].to(d)
+        self.W = share.W if share is not None else cfg["W"].to(d)
         self.ids = cfg["ids"].to(d)
         self.residual0 = cfg["residual"].to(d)
         self.residual = self.residual0.clone()
@@ -38,7 +45,7 @@ class DecodeChain:
         self.gate_up = cfg["gate_up"].to(d)
         self.batch = {n: getattr(pb, n).to(d) for n in (
             "batch_indices", "positions", "kv_indices", "kv_indptr", "kv_last_page_len")}
-        self.cache = wl.sentinel_cache(cfg["cache_shape"]).to(d)
+        self.cache = share.cache if share is not None else wl.sentinel_cache(cfg["cache_shape"]).to(d)
         B = self.ids.numel()
         self.hidden = torch.empty((B, cfg["H"]), dtype=torch.bfloat16, device=d)
         self.normed = torch.empty_like(self.hidden)
@@ -53,6 +60,13 @@ class DecodeChain:
         self.cache.view(torch.int16).fill_(wl.SENTINEL_BITS)
 
     def run(self):
+        if self.grouped:
+            with ops.op_group(self.hidden.device):
+                self._ops()
+        else:
+            self._ops()
+
+    def _ops(self):
         b = self.batch
         ops.embedding(self.ids, self.W, out=self.hidden)
         ops.add_rms_norm(self.hidden, self.residual, self.w_norm, self.eps, out=self.normed,

@@ -17,6 +17,70 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 int num_cus();  // compute units of the current device (cached per device)
 
+// ---------------------------------------------------------------- grouped launch (host)
+// Between pie_hip_group_begin and pie_hip_group_end (group.hip) the groupable entry points
+// validate their arguments, then hand them to group_add_* instead of launching; the group's
+// end launches them together. The records hold the entry points' own arguments.
+struct EmbedRec {
+  const int32_t* ids;
+  int64_t T;
+  const uint16_t* W;
+  int64_t V, H, w_rs;
+  uint16_t* out;
+  int64_t out_rs;
+};
+struct AddNormRec {
+  const uint16_t* x;
+  int64_t x_rs;
+  const uint16_t* r;
+  int64_t r_rs;
+  uint16_t* s;
+  int64_t s_rs;
+  uint16_t* y;
+  int64_t y_rs;
+  const uint16_t* w;
+  int64_t rows, cols;
+  float eps;
+};
+struct ActRec {
+  const uint16_t* in;
+  int64_t in_rs;
+  uint16_t* out;
+  int64_t out_rs, rows, I;
+  int gelu;  // 0 SiLU, 1 GELU(tanh)
+};
+struct QkRec {
+  const uint16_t* q;
+  int64_t q_ts, q_hs;
+  const uint16_t* k;
+  int64_t k_ts, k_hs;
+  const uint16_t* v;
+  int64_t v_ts, v_hs;
+  uint16_t* q_out;
+  int64_t qo_ts, qo_hs;
+  uint16_t* k_out;
+  int64_t ko_ts, ko_hs;
+  const uint16_t* qw;
+  const uint16_t* kw;
+  float eps;
+  const int32_t* pos;
+  int64_t T, Hq, Hkv, D;
+  const float* inv_freq;  // host array of D/2 values (copied when recorded)
+  const int32_t* batch_indices;
+  const int32_t* positions;
+  const int32_t* kv_indices;
+  const int32_t* kv_indptr;
+  int64_t batch_size;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int64_t num_pages, page_stride, slot_stride, head_stride, page_size;
+};
+bool group_is_open();
+int group_add_embedding(const EmbedRec& r, void* stream);
+int group_add_add_norm(const AddNormRec& r, void* stream);
+int group_add_act(const ActRec& r, void* stream);
+int group_add_qk(const QkRec& r, void* stream);
+
 #define PIE_REQUIRE(cond, ...)                                 \
   do {                                                         \
     if (!(cond)) return ::pie::set_error(PIE_HIP_EINVAL, __VA_ARGS__); \

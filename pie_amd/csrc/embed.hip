@@ -87,6 +87,8 @@ int embedding_impl(const int32_t* ids, int64_t T, const pie_bf16* W, int64_t V, 
   if (T == 0 || H == 0) return PIE_HIP_OK;
   PIE_REQUIRE(ids && out && (W || V == 0), "embedding: null pointer");
   PIE_REQUIRE(w_row_stride >= H && out_row_stride >= H, "embedding: row stride smaller than H");
+  if (!SCALE && group_is_open())
+    return group_add_embedding(EmbedRec{ids, T, W, V, H, w_row_stride, out, out_row_stride}, stream);
   EmbedArgs a{ids, W, out, T, V, H, w_row_stride, out_row_stride, 0, FastDiv{}, scale};
   const dim3 blk(256);
   const hipStream_t st = (hipStream_t)stream;

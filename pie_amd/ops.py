@@ -19,6 +19,9 @@ replacements for the inline torch expressions:
 plus fused entries with no single reference counterpart:
     apply_{llama31_,}rope_pos_ids_and_append_paged_kv_cache   RoPE + append in one HBM pass
     qk_rms_norm_rope_append                      q/k norm + RoPE + append (qwen3.py:651-684)
+    op_group()                                   context: the independent ops of a decode step
+                                                 (embedding -> add_rms_norm, q/k prologue,
+                                                 silu_and_mul) in ONE kernel launch
 
 variant ops of the other model families (gemma2/3, gpt-oss, olmo3):
     gemma_rms_norm, gemma_add_rms_norm, gemma_qk_rms_norm, gelu_tanh_and_mul,
@@ -31,6 +34,7 @@ no fallback: a missing library, a non-GPU tensor or an unsupported dtype raises.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 from typing import Optional, Sequence, Tuple, Union
 
@@ -45,13 +49,51 @@ __all__ = [
     "apply_llama31_rope_pos_ids_and_append_paged_kv_cache", "get_seq_lens",
     "get_batch_indices_positions", "rope_inv_freq", "llama31_inv_freq",
     "qk_rms_norm_rope_append", "gemma_rms_norm", "gemma_add_rms_norm", "gemma_qk_rms_norm",
-    "gelu_tanh_and_mul", "apply_rope_with_cos_sin_cache_inplace",
+    "gelu_tanh_and_mul", "apply_rope_with_cos_sin_cache_inplace", "op_group",
 ]
 
 _BF16 = torch.bfloat16
 
 
 # ----------------------------------------------------------------------------- helpers
+# Tensors handed to recorded calls while an op_group() is open: held until the group's kernel
+# is enqueued, so a temporary (a contiguous copy, a fresh output) cannot be freed and reused
+# before the kernel that reads or writes it is on the stream.
+_group_keep: Optional[list] = None
+
+
+def _keep(*tensors) -> None:
+    if _group_keep is not None:
+        _group_keep.extend(tensors)
+
+
+@contextlib.contextmanager
+def op_group(device: Optional[torch.device] = None):
+    """Record the groupable ops called inside the block and launch them as ONE kernel at its end
+    (pie_hip_group_begin / pie_hip_group_end) on the current stream. Groupable: ``embedding``
+    (no scale), ``add_rms_norm`` / ``fused_add_rmsnorm``, ``silu_and_mul``,
+    ``gelu_tanh_and_mul``, ``qk_rms_norm_rope_append``. The ops must be independent, except
+    that an embedding may produce the ``input`` of an ``add_rms_norm`` in the same group (it then
+    runs fused into the norm). Results equal the separate calls bit for bit. Other ops called
+    inside launch at once. Outputs hold their values only after the block exits."""
+    global _group_keep
+    if _group_keep is not None:
+        raise RuntimeError("op_group: groups do not nest")
+    _lib.call("pie_hip_group_begin")
+    _group_keep = []
+    ok = False
+    try:
+        yield
+        ok = True
+    finally:
+        keep, _group_keep = _group_keep, None
+        idx = torch.cuda.current_device() if device is None else torch.device(device).index
+        st = _raw_stream(idx) if _raw_stream is not None else torch.cuda.current_stream(idx).cuda_stream
+        if ok:
+            _lib.call("pie_hip_group_end", st)
+        else:  # close the group; the block's own exception is the one to report
+            _lib.load().pie_hip_group_end(st)
+        del keep
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
@@ -230,6 +272,7 @@ def add_rms_norm(input: torch.Tensor, residual: torch.Tensor, weight: torch.Tens
     if y2.data_ptr() != out.data_ptr() or s2.data_ptr() != residual_out.data_ptr():
         raise ValueError("add_rms_norm: outputs must be viewable as [rows, H]")
     weight = weight.contiguous()
+    _keep(x2, r2, y2, s2, weight)
     _lib.call("pie_hip_gemma_fused_add_rmsnorm" if _gemma else "pie_hip_fused_add_rmsnorm",
               x2.data_ptr(), x2.stride(0), r2.data_ptr(), r2.stride(0),
               s2.data_ptr(), s2.stride(0), y2.data_ptr(), y2.stride(0), weight.data_ptr(),
@@ -274,6 +317,7 @@ def _act_and_mul(name, sym, input, out):
     y2 = _rows(name, out, I)
     if y2.data_ptr() != out.data_ptr():
         raise ValueError(f"{name}: out must be viewable as [rows, I]")
+    _keep(x2, y2)
     _lib.call(sym, x2.data_ptr(), x2.stride(0), y2.data_ptr(), y2.stride(0), x2.shape[0], I,
               _stream(input))
     return out
@@ -303,6 +347,7 @@ def embedding(input: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Ten
     y2 = _rows("embedding", out, H)
     if y2.data_ptr() != out.data_ptr() or y2.shape[0] != T:
         raise ValueError("embedding: out must be viewable as [T, H]")
+    _keep(ids, weight, y2)
     if scale is None:
         _lib.call("pie_hip_embedding", ids.data_ptr(), T, weight.data_ptr(), V, H,
                   weight.stride(0), y2.data_ptr(), y2.stride(0), _stream(weight))
@@ -544,6 +589,8 @@ def qk_rms_norm_rope_append(q, k, v, q_weight, k_weight, eps, pos_ids, batch_ind
         raise ValueError("qk_rms_norm_rope_append: outputs must match inputs with unit inner stride")
     kp, vp, npages, ps, ss, hs, P = _cache_desc(paged_kv_cache, kv_layout, Hkv, D)
     q_weight, k_weight = q_weight.contiguous(), k_weight.contiguous()
+    _keep(q, k, v, q_out, k_out, q_weight, k_weight, pos_ids, batch_indices, positions,
+          paged_kv_cache, kv_indices, kv_indptr)
     _lib.call("pie_hip_qk_rmsnorm_rope_append", q.data_ptr(), q.stride(0), q.stride(1),
               k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
               q_out.data_ptr(), q_out.stride(0), q_out.stride(1), k_out.data_ptr(),

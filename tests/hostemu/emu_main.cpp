@@ -3,7 +3,7 @@
 // the results with the CPU oracle (oracle/oracle.c). TEST INFRASTRUCTURE.
 //
 //   emu_main <case>    case = norm | qk | silu | embed | rope | fused | decode | index | qkfused |
-//                      variants | fastdiv | attn | prefill | sample | all | big
+//                      variants | fastdiv | attn | prefill | sample | group | all | big
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -404,6 +404,108 @@ static void case_attn_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int6
   failures += !(worst <= 1.f);
 }
 
+// The allocation-free decode entry point against the workspace one, bit for bit: two calls in
+// a row, the second smaller, so partials left in the shared static array must not leak.
+static void case_attn_decode_noalloc() {
+  printf("attn_decode_noalloc\n");
+  for (int pass = 0; pass < 2; ++pass) {
+    const int64_t B = pass ? 2 : 5, Hq = 8, Hkv = 2, D = 128, P = 16, S = 3;
+    std::vector<int32_t> len(B), indptr(B + 1, 0), last(B);
+    std::uniform_int_distribution<int> dl(pass ? 1 : 300, pass ? 200 : 700);
+    for (int64_t b = 0; b < B; ++b) {
+      len[b] = dl(rng);
+      const int np = (len[b] + P - 1) / P;
+      indptr[b + 1] = indptr[b] + np;
+      last[b] = len[b] - (np - 1) * (int)P;
+    }
+    const int64_t pages = indptr[B], page_elems = 2 * P * Hkv * D;
+    Buf<int32_t> ip(B + 1), idx(pages), ll(B);
+    for (int64_t i = 0; i < pages; ++i) idx[i] = (int32_t)(pages - 1 - i);
+    for (int64_t b = 0; b <= B; ++b) ip[b] = indptr[b];
+    for (int64_t b = 0; b < B; ++b) ll[b] = last[b];
+    Buf<uint16_t> cache(pages * page_elems), q(B * Hq * D), a(B * Hq * D), b2(B * Hq * D);
+    fill_normal(cache);
+    fill_normal(q);
+    Buf<float> ws(B * S * Hq * (D + 1));
+    rc_ok(pie_hip_attention_decode(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D,
+                                   pages, ip.p, idx.p, ll.p, B, Hq, Hkv, D, P, 0.09f, -1, S, ws.p,
+                                   (int64_t)(ws.n * 4), a.p, Hq * D, D, nullptr), "decode");
+    rc_ok(pie_hip_attention_decode_noalloc(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems,
+                                           Hkv * D, D, pages, ip.p, idx.p, ll.p, B, Hq, Hkv, D, P, 0.09f,
+                                           -1, S, b2.p, Hq * D, D, nullptr), "decode_noalloc");
+    check_equal("noalloc decode == workspace decode", b2.p, a.p, a.n);
+  }
+  const int rc = pie_hip_attention_decode_noalloc(nullptr, 0, 0, nullptr, nullptr, 0, 0, 0, 1, nullptr,
+                                                  nullptr, nullptr, 256, 32, 8, 128, 16, 1.f, -1, 64,
+                                                  nullptr, 0, 0, nullptr);
+  if (rc != PIE_HIP_EINVAL) { printf("  FAIL: oversize noalloc decode accepted\n"); ++failures; }
+}
+
+// The grouped launch (embedding -> add + RMSNorm, q/k prologue, SiLU-and-mul in one kernel)
+// against the separate entry points, bit for bit.
+static void case_group(int64_t B, int64_t H, int64_t I, int64_t V, bool gelu) {
+  const int64_t Hq = 8, Hkv = 2, D = 128;
+  Paged pg = make_paged(B, 16, 10, 300, 1, 1);
+  const int64_t T = pg.T, row = (Hq + 2 * Hkv) * D, P = pg.P, page_elems = 2 * P * Hkv * D;
+  printf("group T=%lld H=%lld I=%lld V=%lld gelu=%d\n", (long long)T, (long long)H, (long long)I,
+         (long long)V, (int)gelu);
+  Buf<uint16_t> W(V * H), res(T * H), wn(H), qkv(T * row), qw(D), kw(D), gu(T * 2 * I);
+  fill_normal(W);
+  fill_normal(res);
+  fill_normal(wn, 1.f, .1f);
+  fill_normal(qkv);
+  fill_normal(qw, 1.f, .1f);
+  fill_normal(kw, 1.f, .1f);
+  fill_normal(gu);
+  Buf<int32_t> ids(T), bidx(T), pos(T), kvi(pg.kv_indices.size()), kvp(B + 1);
+  std::uniform_int_distribution<int> di(-2, (int)V + 1);  // a few out-of-range ids: zero rows
+  for (int64_t t = 0; t < T; ++t) ids[t] = di(rng);
+  copy_in(bidx, pg.bidx);
+  copy_in(pos, pg.pos);
+  copy_in(kvi, pg.kv_indices);
+  copy_in(kvp, pg.kv_indptr);
+  float inv[256];
+  rc_ok(pie_hip_rope_inv_freq(inv, D, 1.f, 1e6f), "inv_freq");
+  const uint16_t *q = qkv.p, *k = qkv.p + Hq * D, *v = qkv.p + (Hq + Hkv) * D;
+  struct Out {
+    Buf<uint16_t> hid, s, y, qo, ko, cache, act;
+    Out(int64_t T, int64_t H, int64_t Hq, int64_t Hkv, int64_t D, int64_t pool, int64_t pe, int64_t I)
+        : hid(T * H), s(T * H), y(T * H), qo(T * Hq * D), ko(T * Hkv * D), cache(pool * pe), act(T * I) {
+      for (size_t i = 0; i < cache.n; ++i) cache[i] = 0x7fa5;
+    }
+  };
+  Out a(T, H, Hq, Hkv, D, pg.pool, page_elems, I), b(T, H, Hq, Hkv, D, pg.pool, page_elems, I);
+  auto run = [&](Out& o) {
+    rc_ok(pie_hip_embedding(ids.p, T, W.p, V, H, H, o.hid.p, H, nullptr), "embedding");
+    rc_ok(pie_hip_fused_add_rmsnorm(o.hid.p, H, res.p, H, o.s.p, H, o.y.p, H, wn.p, T, H, 1e-6f, nullptr),
+          "add_rmsnorm");
+    rc_ok(pie_hip_qk_rmsnorm_rope_append(q, row, D, k, row, D, v, row, D, o.qo.p, Hq * D, D, o.ko.p,
+                                         Hkv * D, D, qw.p, kw.p, 1e-6f, pos.p, T, Hq, Hkv, D, inv, bidx.p,
+                                         pos.p, kvi.p, kvp.p, B, o.cache.p, o.cache.p + P * Hkv * D,
+                                         pg.pool, page_elems, Hkv * D, D, P, nullptr), "qk");
+    rc_ok((gelu ? pie_hip_gelu_tanh_and_mul : pie_hip_silu_and_mul)(gu.p, 2 * I, o.act.p, I, T, I, nullptr),
+          "act");
+  };
+  run(a);
+  rc_ok(pie_hip_group_begin(), "group_begin");
+  run(b);
+  rc_ok(pie_hip_group_end(nullptr), "group_end");
+  check_equal("group hidden", b.hid.p, a.hid.p, a.hid.n);
+  check_equal("group residual", b.s.p, a.s.p, a.s.n);
+  check_equal("group normed", b.y.p, a.y.p, a.y.n);
+  check_equal("group q", b.qo.p, a.qo.p, a.qo.n);
+  check_equal("group k", b.ko.p, a.ko.p, a.ko.n);
+  check_equal("group cache", b.cache.p, a.cache.p, a.cache.n);
+  check_equal("group act", b.act.p, a.act.p, a.act.n);
+  // a hazard (the activation writes the norm's residual input) is rejected without launching
+  rc_ok(pie_hip_group_begin(), "group_begin");
+  rc_ok(pie_hip_fused_add_rmsnorm(b.hid.p, H, res.p, H, b.s.p, H, b.y.p, H, wn.p, T, H, 1e-6f, nullptr), "n");
+  rc_ok(pie_hip_silu_and_mul(gu.p, 2 * I, res.p, I, T, std::min<int64_t>(I, H), nullptr), "a");
+  if (pie_hip_group_end(nullptr) != PIE_HIP_EINVAL) { printf("  FAIL: hazard accepted\n"); ++failures; }
+  check_equal("rejected group launched nothing", b.s.p, a.s.p, a.s.n);
+  if (pie_hip_group_end(nullptr) != PIE_HIP_EINVAL) { printf("  FAIL: end without begin\n"); ++failures; }
+}
+
 // Paged prefill attention: requests with ctx in [0, cmax] cached tokens and qo in [0, qmax] new
 // query tokens; mode 0 full, 1 causal, 2 a random custom mask.
 static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int cmax, int qmax,
@@ -667,6 +769,12 @@ int main(int argc, char** argv) {
     case_attn_prefill(3, 8, 2, 128, 16, 20, 120, 2, true);  // masks within the causal window
     case_attn_prefill(3, 8, 2, 128, 16, 200, 120, 1, false, 70);  // causal + sliding window
     case_attn_prefill(2, 8, 2, 128, 8, 100, 90, 2, false, 40);    // custom mask + sliding window
+  }
+  if (all || c == "group") {
+    case_group(5, 4096, 1536, 40, false);  // 8 norm vectors per lane pair (NJ = 2)
+    case_group(3, 1024, 256, 9, true);      // GELU, 2 waves per row
+    case_group(2, 896, 512, 7, false);      // norm width outside the group kernel: separate launches
+    case_attn_decode_noalloc();
   }
   if (all || c == "qkfused") {
     case_qk_fused(5, 4, 2, 128);  // fused kernel

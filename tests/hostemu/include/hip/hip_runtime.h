@@ -36,6 +36,8 @@ enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount = 1 };
 inline hipError_t hipGetLastError() { return hipSuccess; }
 inline const char* hipGetErrorString(hipError_t) { return "emulated"; }
 inline hipError_t hipGetDevice(int* d) { *d = 0; return hipSuccess; }
+inline hipError_t hipGetSymbolAddress(void** p, const void* sym) { *p = const_cast<void*>(sym); return hipSuccess; }
+#define HIP_SYMBOL(x) (&(x))
 inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
   const char* e = getenv("EMU_CUS");
   *v = e ? atoi(e) : 1;  // few "CUs" so grid caps engage and grid-stride loops iterate
@@ -47,7 +49,7 @@ inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
 #define __host__
 #define __forceinline__ inline
 #define __launch_bounds__(...)
-#define __align__(n) alignas(n)
+#define __align__(n) __attribute__((aligned(n)))
 #define __shared__ static
 
 namespace emu {

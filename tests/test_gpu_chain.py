@@ -1,6 +1,7 @@
-"""GPU: the Qwen3-8B decode-step op chain (configuration 5) eagerly vs the oracle, fused vs
-unfused, and HIP-graph replays vs the eager result (every replay checked, with eager work
-and synchronisation between replays)."""
+"""GPU: the Qwen3-8B decode-step op chain (configuration 5) eagerly vs the oracle, fused and
+grouped (one launch) vs unfused bit for bit, and HIP-graph replays vs the eager result (every
+replay checked, with eager work and synchronisation between replays). The configured
+151936-row table runs once, grouped, against the oracle."""
 from __future__ import annotations
 
 import pytest
@@ -25,10 +26,7 @@ def _snap(ch):
     return {k: N(v) for k, v in ch.outputs().items()}
 
 
-def test_chain_vs_oracle(dev, cfg):
-    ch = DecodeChain(cfg, dev, fused=True)
-    ch.run()
-    got = _snap(ch)
+def _check_vs_oracle(got, cfg):
     hid, _ = oracle.embedding(N(cfg["ids"]), N(cfg["W"]))
     assert_bits_equal(got["hidden"], hid, "embedding")
     y, s = oracle.add_rmsnorm(hid, N(cfg["residual"]), N(cfg["w_norm"]), cfg["eps"])
@@ -50,8 +48,28 @@ def test_chain_vs_oracle(dev, cfg):
     assert_bf16_close(got["act"], oracle.silu_and_mul(N(cfg["gate_up"])), what="silu")
 
 
-def test_chain_fused_equals_unfused(dev, cfg):
-    a, b = DecodeChain(cfg, dev, fused=True), DecodeChain(cfg, dev, fused=False)
+@pytest.mark.parametrize("grouped", [False, True])
+def test_chain_vs_oracle(dev, cfg, grouped):
+    print(f"chain vs oracle grouped={grouped}", flush=True)
+    ch = DecodeChain(cfg, dev, fused=True, grouped=grouped)
+    ch.run()
+    _check_vs_oracle(_snap(ch), cfg)
+
+
+def test_chain_full_vocabulary_grouped(dev):
+    """Configuration 5 exactly as configured: the [151936, 4096] embedding table."""
+    print("chain V=151936 grouped", flush=True)
+    full = wl.cfg5()
+    ch = DecodeChain(full, dev, grouped=True)
+    ch.run()
+    _check_vs_oracle(_snap(ch), full)
+
+
+@pytest.mark.parametrize("mode", ["fused", "grouped"])
+def test_chain_fused_equals_unfused(dev, cfg, mode):
+    print(f"chain {mode} vs unfused", flush=True)
+    a = DecodeChain(cfg, dev, fused=True, grouped=mode == "grouped")
+    b = DecodeChain(cfg, dev, fused=False)
     a.run()
     b.run()
     ga, gb = _snap(a), _snap(b)
@@ -59,8 +77,10 @@ def test_chain_fused_equals_unfused(dev, cfg):
         assert_bits_equal(ga[key], gb[key], key)
 
 
-def test_chain_graph_replays(dev, cfg):
-    ch = DecodeChain(cfg, dev, fused=True)
+@pytest.mark.parametrize("grouped", [False, True])
+def test_chain_graph_replays(dev, cfg, grouped):
+    print(f"chain graph replays grouped={grouped}", flush=True)
+    ch = DecodeChain(cfg, dev, fused=True, grouped=grouped)
     ch.reset()
     ch.run()
     eager = _snap(ch)

@@ -127,6 +127,23 @@ def test_integration_installs_flashinfer_namespace():
     assert "flashinfer" not in sys.modules and "flashinfer.sampling" not in sys.modules
 
 
+def test_integration_does_not_forward_unserved_names_by_default(monkeypatch):
+    import sys
+    import types
+    from pie_amd import integration
+    real = types.ModuleType("flashinfer")
+    real.mm_fp8 = lambda *a: "real"
+    monkeypatch.setitem(sys.modules, "flashinfer", real)
+    mod = integration.install()
+    try:
+        with pytest.raises(AttributeError, match="not provided by pie_amd"):
+            mod.mm_fp8
+        assert integration.install(forward_unserved=True).mm_fp8() == "real"
+    finally:
+        integration.uninstall()
+    assert sys.modules["flashinfer"] is real
+
+
 def test_prefill_plan_position_limits_without_a_gpu():
     """The prefill plan (host code) takes requests of up to 2^31 - 1 positions, and up to
     2^30 - 1 under a custom mask (the extent kernel marks exactly causal rows in bit 30)."""
