@@ -265,7 +265,54 @@ def measure_ops(dev, cold_iters=20, only=None):
         res.extend(_ops_sampling(dev, run))
     if want("cfg5"):
         res.extend(measure_chain(dev, flush, cold_iters))
+    if want("ceiling"):
+        res.extend(_ops_ceiling(dev, run))
     del scratch
+    return res
+
+
+def _ops_ceiling(dev, run):
+    """Measured ceilings for two access patterns (pie_amd/probe/probe.hip, no arithmetic and no
+    index logic): configuration 1's bytes as a plain copy (8 MiB read, 8 MiB written) and
+    configuration 3's paged append as a scatter of the same 2 KiB k / v rows from the same qkv
+    rows to the same cache slots, the slot offsets computed beforehand (plus their 16 B per row)."""
+    import ctypes as C
+
+    import torch
+    from pie_amd import build as B
+    from pie_amd import workloads as wl
+    lib = C.CDLL(str(B.PROBE_LIB))
+    lib.pie_probe_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_void_p]
+    lib.pie_probe_scatter.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
+                                      C.c_int64, C.c_void_p]
+    st = lambda: torch.cuda.current_stream().cuda_stream
+    n1 = 2048 * 2048 * 2
+
+    def make_copy(nt):
+        a = torch.empty(n1, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        return lambda: lib.pie_probe_copy(a.data_ptr(), b.data_ptr(), n1, nt, st())
+    res = [run("ceiling copy 8 MiB -> 8 MiB (cfg1 bytes), cached", 2 * n1, lambda: make_copy(0)),
+           run("ceiling copy 8 MiB -> 8 MiB (cfg1 bytes), non-temporal", 2 * n1, lambda: make_copy(1))]
+    c = wl.cfg3()
+    pb, T = c["batch"], c["qkv"].shape[0]
+    Hq, Hkv, D, P = 32, 8, 128, pb.page_size
+    row_b, kv_b = (Hq + 2 * Hkv) * D * 2, Hkv * D * 2
+    page = pb.kv_indices.long()[pb.kv_indptr.long()[pb.batch_indices.long()] + pb.positions.long() // P]
+    slot = pb.positions.long() % P
+    t = torch.arange(T, dtype=torch.int64)
+    dst_k = page * (2 * P * kv_b) + slot * kv_b
+    src = torch.stack([t * row_b + Hq * D * 2, t * row_b + (Hq + Hkv) * D * 2], 1).reshape(-1).to(dev)
+    dst = torch.stack([dst_k, dst_k + P * kv_b], 1).reshape(-1).to(dev)
+    qkv0 = c["qkv"].to(dev)
+
+    def make_scatter():
+        qkv = qkv0.clone()
+        cache = wl.sentinel_cache(c["cache_shape"]).to(dev)
+        return lambda: lib.pie_probe_scatter(qkv.data_ptr(), src.data_ptr(), cache.data_ptr(),
+                                             dst.data_ptr(), 2 * T, kv_b, st())
+    res.append(run(f"ceiling scatter of the cfg3 append pattern T={T}", 2 * T * 2 * kv_b + 2 * T * 16,
+                   make_scatter))
     return res
 
 
@@ -576,7 +623,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", choices=["all", "main", "ops", "copy", "chain"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--op", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "variants", "attn", "sample"], default=None,
+    ap.add_argument("--op", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "variants", "attn", "sample", "ceiling"], default=None,
                     help="with --only ops: measure one configuration")
     args = ap.parse_args()
     if args.gpus != 1:

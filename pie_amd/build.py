@@ -18,6 +18,9 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libpie_hip.so"
+# measurement probes (plain kernels with a hot-path kernel's access pattern; bench.py --op ceiling)
+PROBE_SRC = PKG / "probe" / "probe.hip"
+PROBE_LIB = PKG / "libpie_probe.so"
 ARCH = "gfx950"
 
 # Packed fp32 VALU ops are disabled: hipcc would otherwise form v_pk_{add,mul,fma}_f32 from
@@ -69,7 +72,22 @@ def build(verbose: bool = False, out: Path | None = None, defines: tuple[str, ..
     os.replace(tmp, lib)
     if verbose:
         print(f"built {lib}")
+    if not defines and out is None:
+        build_probe(verbose)
     return lib
+
+
+def build_probe(verbose: bool = False) -> Path:
+    """The measurement-probe library (not part of the C ABI)."""
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    cmd = [_hipcc(), *HIP_FLAGS, "-shared", "-o", str(tmp), str(PROBE_SRC)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {PROBE_SRC.name}:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    if verbose:
+        print(f"built {PROBE_LIB}")
+    return PROBE_LIB
 
 
 if __name__ == "__main__":

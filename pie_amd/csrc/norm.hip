@@ -56,7 +56,10 @@ __device__ __forceinline__ void row_offsets(const RowSet& s, int64_t r, int64_t&
 
 // Rows per wave group in flight at once. 1 measured best on configuration 2 (steady state:
 // 2 rows equal, 4 rows 6% slower: the extra registers cost more occupancy than they gain).
-constexpr int kRowsPerGroup = 1;
+#ifndef PIE_NORM_RPG
+#define PIE_NORM_RPG 1
+#endif
+constexpr int kRowsPerGroup = PIE_NORM_RPG;
 
 // ---------------------------------------------------------------- W waves per row, VPL*512*W cols
 // A row is held in registers by a group of W wavefronts (VPL 16-byte vectors per lane); lane l
@@ -369,7 +372,8 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
   const bool vec = a.cols % 8 == 0 && rowset_vec_ok(a.set[0], ADD) &&
                    (a.set[1].rows == 0 || rowset_vec_ok(a.set[1], ADD));
   const dim3 blk(256);
-  const bool large = PIE_NORM_LARGE_NT && rows * a.cols * 2 >= (int64_t)64 << 20;  // far larger than L2
+  const int64_t in_bytes = rows * a.cols * 2;
+  const bool large = PIE_NORM_LARGE_NT && in_bytes >= (int64_t)64 << 20;  // far larger than L2
   // (the residual-add form only: a plain norm, one input stream, keeps too few bytes in flight at
   // one vector per lane and stays on the row-loop kernel with 4 vectors per lane)
   if (ADD && vec && large && a.set[1].rows == 0 && a.cols % 4096 == 0 && a.cols <= 3 * 4096 &&
@@ -409,7 +413,16 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
       // 2, 8 waves per row, steady state: x / r / s / y at 5.6 TB/s cached, 6.7 TB/s
       // non-temporal in a standalone model of this kernel); small lists (decode) keep their
       // outputs in L2 for the next kernel.
-      switch ((n512 / W) * 2 + (large ? 1 : 0)) {
+      static const int forced_nt = [] {  // tuning override: PIE_HIP_NORM_NT=0|1
+        const char* e = getenv("PIE_HIP_NORM_NT");
+        return e ? atoi(e) : -1;
+      }();
+      // Non-temporal from 8 MB of input on (configuration 1, [2048, 2048] = 8 MiB, steady state:
+      // 4.72 us against 6.05 us cached; a plain copy of the same bytes takes 3.79 us
+      // non-temporal, 4.42 cached). Decode-sized lists keep their outputs in L2 for the next kernel.
+      const bool nt = forced_nt == 0 || forced_nt == 1 ? forced_nt == 1
+                                                       : PIE_NORM_LARGE_NT && in_bytes >= (int64_t)8 << 20;
+      switch ((n512 / W) * 2 + (nt ? 1 : 0)) {
 #define PIE_NV(n)                                                                                      \
   case 2 * n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, kRowsPerGroup, ADD, GEMMA, false>), grd, tb, 0, st, a, W); \
     break;                                                                                              \

@@ -22,6 +22,8 @@
 //   k tail units (dims >= rd) and v units: 16-byte copies into the cache page.
 // A token's Hkv*D row in a page is contiguous for NHD, so the 64 lanes of a wave write whole
 // 1 KiB runs of a page: the scatter is coalesced per (page, slot).
+#include <stdlib.h>
+
 #include "rope_dev.h"
 
 namespace pie {
@@ -207,20 +209,35 @@ struct AppendFlatArgs {
   uint32_t kunits;  // Hkv * (D/8): k chunks come first in a token
 };
 
+// U chunks per thread (units base + 256 i), every data load and page lookup issued before the
+// first store. WU: a token's units fill whole waves (units per token a multiple of 64), so the
+// token index is made wave-uniform and its three index loads become scalar loads.
+template <int U, bool WU>
 __global__ __launch_bounds__(256) void append_flat(AppendFlatArgs a) {
-  const uint32_t n = blockIdx.x * 256u + threadIdx.x;
-  if (n >= a.nunits) return;
-  const uint32_t t = a.upt.div(n);
-  uint32_t r = n - t * a.upt.d;
-  const bool isv = r >= a.kunits;
-  if (isv) r -= a.kunits;
-  const uint32_t head = a.cph.div(r), c = r - head * a.cph.d;
-  const uint16_t* src = isv ? a.h.v + (int64_t)t * a.h.v_ts + (int64_t)head * a.h.v_hs
-                            : a.h.k + (int64_t)t * a.h.k_ts + (int64_t)head * a.h.k_hs;
-  const uint4 x = ld_nt(src + c * 8);
-  const int64_t kc = slot_offset(a.c, t);
-  if (kc >= 0)
-    st_nt((isv ? a.c.v_cache : a.c.k_cache) + kc + (int64_t)head * a.c.head_stride + c * 8, x);
+  const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
+  uint4 x[U];
+  int64_t dst[U];
+  const uint16_t* cache[U];
+#pragma unroll
+  for (int i = 0; i < U; ++i) {
+    const uint32_t n = base + 256u * i;
+    const bool valid = n < a.nunits;
+    uint32_t t = a.upt.div(valid ? n : 0);
+    if constexpr (WU) t = (uint32_t)uniform((int)t);
+    uint32_t r = (valid ? n : 0) - t * a.upt.d;
+    const bool isv = r >= a.kunits;
+    if (isv) r -= a.kunits;
+    const uint32_t head = a.cph.div(r), c = r - head * a.cph.d;
+    const uint16_t* src = isv ? a.h.v + (int64_t)t * a.h.v_ts + (int64_t)head * a.h.v_hs
+                              : a.h.k + (int64_t)t * a.h.k_ts + (int64_t)head * a.h.k_hs;
+    x[i] = ld_nt(src + c * 8);
+    const int64_t kc = valid ? slot_offset(a.c, t) : -1;
+    dst[i] = kc < 0 ? -1 : kc + (int64_t)head * a.c.head_stride + c * 8;
+    cache[i] = isv ? a.c.v_cache : a.c.k_cache;
+  }
+#pragma unroll
+  for (int i = 0; i < U; ++i)
+    if (dst[i] >= 0) st_nt(const_cast<uint16_t*>(cache[i]) + dst[i], x[i]);
 }
 
 // ---------------------------------------------------------------- scalar fallbacks
@@ -280,7 +297,18 @@ int launch(RopeAppendArgs& a, bool rope, bool append, int interleave, hipStream_
     if (nunits < (1ll << 31)) {
       AppendFlatArgs f{h, a.c, (uint32_t)nunits, FastDiv::make((uint32_t)(2 * kunits)),
                        FastDiv::make((uint32_t)(h.D / 8)), (uint32_t)kunits};
-      hipLaunchKernelGGL(append_flat, dim3((unsigned)((nunits + 255) / 256)), dim3(256), 0, st, f);
+      static const int forced_u = [] {  // tuning override: PIE_HIP_APPEND_U=1|2|4
+        const char* e = getenv("PIE_HIP_APPEND_U");
+        return e ? atoi(e) : 0;
+      }();
+      const int U = forced_u == 1 || forced_u == 2 || forced_u == 4 ? forced_u : 1;
+      const bool wu = (2 * kunits) % 64 == 0;
+      const dim3 grd((unsigned)((nunits + 256 * U - 1) / (256 * U))), blk(256);
+#define PIE_AF(u)                                                                  \
+  if (wu) hipLaunchKernelGGL((append_flat<u, true>), grd, blk, 0, st, f);           \
+  else hipLaunchKernelGGL((append_flat<u, false>), grd, blk, 0, st, f);
+      if (U == 4) { PIE_AF(4) } else if (U == 2) { PIE_AF(2) } else { PIE_AF(1) }
+#undef PIE_AF
       return check_launch(name);
     }
   }
