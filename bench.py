@@ -401,12 +401,17 @@ def _ops_variants(dev, run):
         x, y = x0.clone(), torch.empty_like(x0)
         return lambda: ops.gemma_rms_norm(x, w, 1e-6, out=y)
 
+    def make_plain():
+        x, y = x0.clone(), torch.empty_like(x0)
+        return lambda: ops.rmsnorm(x, w, 1e-6, out=y)
+
     def make_gelu():
         gu = gu0.clone()
         act = torch.empty((gu.shape[0], gu.shape[1] // 2), dtype=gu.dtype, device=dev)
         return lambda: ops.gelu_tanh_and_mul(gu, out=act)
     res = [run("variant gemma add+rmsnorm [8192,4096]", b_add, make_gemma_add),
            run("variant gemma rmsnorm [8192,4096]", b_norm, make_gemma),
+           run("rmsnorm [8192,4096] (the plain norm at the Gemma shape)", b_norm, make_plain),
            run("variant gelu_tanh_and_mul [8192,2x14336]", b_act, make_gelu)]
     del x0, r0, gu0
     c4 = wl.cfg4()

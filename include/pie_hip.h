@@ -33,7 +33,8 @@ enum {
 /* Message describing the last nonzero return on this thread ("" if none). */
 const char* pie_hip_last_error(void);
 
-/* ABI version; bumped whenever a signature below changes (2: paged attention and sampling). */
+/* ABI version; bumped whenever a signature below changes (2: paged attention and sampling;
+ * 3: attention sinks). */
 int pie_hip_abi_version(void);
 
 /*
@@ -302,6 +303,10 @@ int pie_hip_get_batch_indices_positions(const int32_t* append_indptr, const int3
  * [0, num_pages) are treated as masked positions. window_left >= 0 is flashinfer's sliding
  * window (as olmo3.py:381-391, :973-1005 plans it): the query at position p = kv_len - 1 sees only
  * positions >= p - window_left; -1 = no window.
+ * sinks: NULL, or fp32 [num_qo_heads] attention-sink logits in the units of the scaled scores
+ * (gpt-oss, pie/src/pie_worker/model/gpt_oss.py:693-697, flashinfer's
+ * BatchAttentionWithAttentionSinkWrapper): head h's softmax denominator gains exp(sinks[h] - max)
+ * and no value, i.e. out = sum_t e^{s_t} v_t / (sum_t e^{s_t} + e^{sinks[h]}).
  */
 int pie_hip_attention_decode_plan(int64_t batch, int64_t num_kv_heads, int64_t max_kv_len,
                                   int64_t num_cus, int64_t* splits);
@@ -311,7 +316,8 @@ int pie_hip_attention_decode(const pie_bf16* q, int64_t q_tok_stride, int64_t q_
                              const int32_t* kv_indptr, const int32_t* kv_indices,
                              const int32_t* kv_last_page_len, int64_t batch, int64_t num_qo_heads,
                              int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
-                             float sm_scale, int64_t window_left, int64_t splits, void* workspace,
+                             float sm_scale, int64_t window_left, const float* sinks,
+                             int64_t splits, void* workspace,
                              int64_t workspace_bytes,
                              pie_bf16* out, int64_t o_tok_stride, int64_t o_head_stride,
                              void* stream);
@@ -332,7 +338,8 @@ int pie_hip_attention_decode_noalloc(const pie_bf16* q, int64_t q_tok_stride, in
                                      const int32_t* kv_indices, const int32_t* kv_last_page_len,
                                      int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
                                      int64_t head_dim, int64_t page_size, float sm_scale,
-                                     int64_t window_left, int64_t splits, pie_bf16* out,
+                                     int64_t window_left, const float* sinks, int64_t splits,
+                                     pie_bf16* out,
                                      int64_t o_tok_stride, int64_t o_head_stride, void* stream);
 
 /*
@@ -344,7 +351,7 @@ int pie_hip_attention_decode_noalloc(const pie_bf16* q, int64_t q_tok_stride, in
  * pie/src/pie_worker/batching.py:335-386 builds it). Cache addressing, heads and scale as in
  * the decode form. window_left >= 0 additionally hides positions t < p - window_left, with
  * p = kv_len - qo_len + i the query's own position (flashinfer's sliding window; -1 = none).
- * Rows that see nothing are 0.
+ * Rows that see nothing are 0. sinks: as in the decode form (NULL = none).
  * Replaces flashinfer.BatchPrefillWithPagedKVCacheWrapper.plan/.run as Pie calls them:
  *   pie/src/pie_worker/model/llama3.py:307-309 (construction), :779-790 (plan with the custom
  *   mask), :689 (run); API restated in pie/src/flashinfer_metal/ops.py:163-223.
@@ -379,6 +386,7 @@ int pie_hip_attention_prefill(const pie_bf16* q, int64_t q_tok_stride, int64_t q
                               const int32_t* kv_last_page_len, int64_t num_qo_heads,
                               int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                               float sm_scale, int32_t mode, int64_t window_left,
+                              const float* sinks,
                               const uint32_t* packed_mask, const int32_t* mask_extent,
                               const int32_t* plan, int64_t num_items,
                               int64_t mask_offsets_word,

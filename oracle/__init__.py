@@ -82,7 +82,8 @@ def _load():
                                   C.c_int, _f32p, i64, i64]),
         "oracle_attention": (None, [_u16p, i64, i64, C.c_void_p, C.c_void_p, i64, i64, i64,
                                     _i32p, _i32p, _i32p, _i32p, C.c_void_p, C.c_void_p, C.c_int, i64, i64, i64,
-                                    i64, i64, i64, C.c_double, _u16p, i64, i64, C.c_void_p]),
+                                    i64, i64, i64, C.c_double, _u16p, i64, i64, C.c_void_p,
+                                    C.c_void_p]),
         "oracle_scaled_softmax": (None, [_f32p, i64, i64, _f32p, C.c_double, _f64p]),
         "oracle_sample": (None, [_f32p, i64, i64, i64, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
                                  _f64p, _i32p, C.c_void_p]),
@@ -294,13 +295,14 @@ def batch_indices_positions(append_indptr, seq_lens_, nnz: int, fill: int = -1):
 
 def attention(q: np.ndarray, cache: np.ndarray, qo_indptr, kv_indptr, kv_indices, last_page_len,
               custom_mask=None, sm_scale: float | None = None, layout: str = "NHD",
-              return_lse: bool = False, causal: bool = True, window_left: int = -1):
+              return_lse: bool = False, causal: bool = True, window_left: int = -1, sinks=None):
     """Paged attention over cache [pages, 2, P, Hkv, D] (NHD) or [pages, 2, Hkv, P, D] (HND).
     q [T, Hq, D] bf16 bits -> out [T, Hq, D] bf16 bits (and lse [T, Hq] float64, natural log).
     custom_mask: flat bool/uint8, per request a row-major [qo_len, kv_len] block, concatenated
     in request order; None means the causal window t <= kv_len - qo_len + i (causal=True) or
     every cached position (causal=False); window_left >= 0 also hides positions before
-    kv_len - qo_len + i - window_left (flashinfer's sliding window)."""
+    kv_len - qo_len + i - window_left (flashinfer's sliding window). sinks: optional float32 [Hq]
+    attention-sink logits (gpt-oss): each head's denominator gains exp(sinks[h])."""
     q = np.ascontiguousarray(q, dtype=np.uint16)
     assert cache.flags.c_contiguous and cache.dtype == np.uint16
     T, Hq, D = q.shape
@@ -327,6 +329,8 @@ def attention(q: np.ndarray, cache: np.ndarray, qo_indptr, kv_indptr, kv_indices
         off = np.zeros(B, dtype=np.int64)
         off[1:] = np.cumsum(qol * kvl)[:-1]
         assert mask_arr.size >= int((qol * kvl).sum()), "custom_mask too short"
+    sk = None if sinks is None else np.ascontiguousarray(sinks, dtype=np.float32)
+    assert sk is None or sk.shape == (Hq,), "sinks must be [Hq]"
     base = cache.ctypes.data
     _load().oracle_attention(
         q, Hq * D, D, base, base + P * Hkv * D * 2, ps, ss, hs, qo_indptr, kv_indptr,
@@ -334,7 +338,7 @@ def attention(q: np.ndarray, cache: np.ndarray, qo_indptr, kv_indptr, kv_indices
         None if mask_arr is None else mask_arr.ctypes.data,
         None if off is None else off.ctypes.data, 1 if causal else 0, window_left, B, Hq, Hkv, D, P,
         scale, out, Hq * D, D,
-        lse.ctypes.data)
+        lse.ctypes.data, None if sinks is None else sk.ctypes.data)
     return (out, lse) if return_lse else out
 
 

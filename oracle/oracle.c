@@ -324,14 +324,18 @@ void oracle_batch_indices_positions(const int32_t* indptr, const int32_t* seq_le
  * output rounded once to bf16. A row with no allowed position gives 0 and lse = -inf.
  * Token t of request b lives in page kv_indices[kv_indptr[b] + t/P], slot t%P; k and v are
  * addressed as k_cache/v_cache + page*page_stride + slot*slot_stride + head*head_stride.
- * lse (optional, [T, Hq]) is the natural-log sum of exp(scaled scores).                  */
+ * lse (optional, [T, Hq]) is the natural-log sum of exp(scaled scores).
+ * sinks (optional, fp32 [Hq]): gpt-oss attention sinks (pie/src/pie_worker/model/gpt_oss.py:693-697,
+ * flashinfer's BatchAttentionWithAttentionSinkWrapper; the published gpt-oss attention appends
+ * the head's sink logit as one more score column, takes the softmax and drops that column):
+ * the denominator gains exp(sinks[h]), the numerator nothing; lse includes it.            */
 void oracle_attention(const uint16_t* q, int64_t q_ts, int64_t q_hs, const uint16_t* kc,
                       const uint16_t* vc, int64_t page_stride, int64_t slot_stride,
                       int64_t head_stride, const int32_t* qo_indptr, const int32_t* kv_indptr,
                       const int32_t* kv_indices, const int32_t* last_len, const uint8_t* mask,
                       const int64_t* mask_off, int causal, int64_t window_left, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
                       int64_t P, double sm_scale, uint16_t* out, int64_t o_ts, int64_t o_hs,
-                      double* lse) {
+                      double* lse, const float* sinks) {
   const int64_t G = Hq / Hkv;
   for (int64_t b = 0; b < B; ++b) {
     const int64_t np = kv_indptr[b + 1] - kv_indptr[b];
@@ -357,7 +361,10 @@ void oracle_attention(const uint16_t* q, int64_t q_ts, int64_t q_hs, const uint1
         }
         for (int64_t e = 0; e < D; ++e) acc[e] = 0;
         double den = 0;
+        const double sk = sinks ? (double)sinks[h] : -INFINITY;
+        if (sk > mx) mx = sk;
         if (mx > -INFINITY) {
+          if (sinks) den = exp(sk - mx);
           for (int64_t t = 0; t < kv_len; ++t) {
             if (s[t] == -INFINITY) continue;
             const double p = exp(s[t] - mx);

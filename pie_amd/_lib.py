@@ -47,15 +47,15 @@ SIGNATURES: dict[str, list] = {
                                        vp, vp, i64, vp, vp, i64, i64, i64, i64, i64, vp],
     "pie_hip_attention_decode_plan": [i64, i64, i64, i64, vp],
     "pie_hip_attention_decode": [vp, i64, i64, vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, i64,
-                                 i64, i64, i64, f32, i64, i64, vp, i64, vp, i64, i64, vp],
+                                 i64, i64, i64, f32, i64, vp, i64, vp, i64, vp, i64, i64, vp],
     "pie_hip_attention_decode_noalloc": [vp, i64, i64, vp, vp, i64, i64, i64, i64, vp, vp, vp, i64,
-                                         i64, i64, i64, i64, f32, i64, i64, vp, i64, i64, vp],
+                                         i64, i64, i64, i64, f32, i64, vp, i64, vp, i64, i64, vp],
     "pie_hip_attention_prefill_plan": [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp, i64, vp, vp,
                                        vp, vp],
     "pie_hip_attention_pack_mask": [vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp],
     "pie_hip_attention_prefill": [vp, i64, i64, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, i64,
-                                  i64, i64, i64, f32, i32, i64, vp, vp, vp, i64, i64, vp, i64, i64,
-                                  vp],
+                                  i64, i64, i64, f32, i32, i64, vp, vp, vp, vp, i64, i64, vp, i64,
+                                  i64, vp],
     "pie_hip_sample": [vp, i64, i64, i64, i64, vp, i32, vp, i32, vp, f32, vp, f32, vp, u64, u64, vp, vp],
     "pie_hip_scaled_softmax": [vp, i32, i64, i64, i64, vp, f32, vp, i64, vp],
     "pie_hip_group_begin": [],
@@ -63,7 +63,7 @@ SIGNATURES: dict[str, list] = {
     "pie_hip_get_seq_lens": [vp, vp, i64, i64, vp, vp],
     "pie_hip_get_batch_indices_positions": [vp, vp, i64, i64, vp, vp, vp],
 }
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib: C.CDLL | None = None
 

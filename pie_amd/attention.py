@@ -8,6 +8,10 @@ The API is flashinfer 0.6.1's, restated in pie/src/flashinfer_metal/ops.py:163-2
     BatchDecodeWithPagedKVCacheWrapper   one query token per request  -> pie_hip_attention_decode
     BatchPrefillWithPagedKVCacheWrapper  ragged query tokens, causal /
                                          custom-mask / full visibility -> pie_hip_attention_prefill
+    BatchAttentionWithAttentionSinkWrapper  gpt-oss: causal (optionally windowed) attention
+                                         whose softmax denominators hold a per-head sink logit
+                                         -> pie_hip_attention_decode (one query token per
+                                         request) or pie_hip_attention_prefill
 
 ``plan`` runs on the host and allocates nothing on the device; ``run`` launches kernels on the
 current stream and allocates only its output (unless ``out=`` is given), so it can be captured.
@@ -29,7 +33,8 @@ import torch
 from . import _lib
 from .ops import _cache_desc, _check, _stream
 
-__all__ = ["BatchDecodeWithPagedKVCacheWrapper", "BatchPrefillWithPagedKVCacheWrapper"]
+__all__ = ["BatchDecodeWithPagedKVCacheWrapper", "BatchPrefillWithPagedKVCacheWrapper",
+           "BatchAttentionWithAttentionSinkWrapper"]
 
 _BF16 = torch.bfloat16
 _CUS: dict = {}
@@ -128,7 +133,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
     def run(self, q: torch.Tensor,
             paged_kv_cache: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]], *args,
             q_scale=None, k_scale=None, v_scale=None, out: Optional[torch.Tensor] = None,
-            lse: Optional[torch.Tensor] = None, return_lse: bool = False, **_ignored):
+            lse: Optional[torch.Tensor] = None, return_lse: bool = False,
+            _sinks: Optional[torch.Tensor] = None, **_ignored):
         name = "BatchDecodeWithPagedKVCacheWrapper.run"
         p = self._plan
         if p is None:
@@ -157,7 +163,8 @@ class BatchDecodeWithPagedKVCacheWrapper:
         _lib.call("pie_hip_attention_decode", q.data_ptr(), q.stride(0), q.stride(1), kp, vp, ps,
                   ss, hs, npages, p["indptr"].data_ptr(), p["indices"].data_ptr(),
                   p["last_page_len"].data_ptr(), B, Hq, Hkv, D, P, float(p["sm_scale"]),
-                  p["window_left"], p["splits"], ws.data_ptr(), ws.numel() * ws.element_size(),
+                  p["window_left"], None if _sinks is None else _sinks.data_ptr(), p["splits"],
+                  ws.data_ptr(), ws.numel() * ws.element_size(),
                   out.data_ptr(),
                   out.stride(0), out.stride(1), _stream(q))
         return out
@@ -268,7 +275,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
     def run(self, q: torch.Tensor,
             paged_kv_cache: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]], *args,
             q_scale=None, k_scale=None, v_scale=None, out: Optional[torch.Tensor] = None,
-            lse: Optional[torch.Tensor] = None, return_lse: bool = False, **_ignored):
+            lse: Optional[torch.Tensor] = None, return_lse: bool = False,
+            _sinks: Optional[torch.Tensor] = None, **_ignored):
         name = "BatchPrefillWithPagedKVCacheWrapper.run"
         p = self._plan
         if p is None:
@@ -300,11 +308,88 @@ class BatchPrefillWithPagedKVCacheWrapper:
                   ss, hs, npages, p["qo_indptr"].data_ptr(), p["indptr"].data_ptr(),
                   p["indices"].data_ptr(), p["last_page_len"].data_ptr(), Hq, Hkv, D, P,
                   float(p["sm_scale"]), p["mode"], p["window_left"],
+                  None if _sinks is None else _sinks.data_ptr(),
                   packed.data_ptr() if packed is not None else None,
                   p["extent"].data_ptr() if p["extent"] is not None else None,
                   p["plan"].data_ptr(), p["items"], p["woff_word"], out.data_ptr(), out.stride(0),
                   out.stride(1), _stream(q))
         return out
+
+    forward = run
+
+    def end_forward(self) -> None:
+        pass
+
+
+class BatchAttentionWithAttentionSinkWrapper:
+    """flashinfer's BatchAttentionWithAttentionSinkWrapper as gpt-oss uses it
+    (pie/src/pie_worker/model/gpt_oss.py:420-438 construction, :839-870 plan, :693-697 run):
+    causal attention over the paged cache, optionally in a sliding window (``window_left``),
+    where each query head's softmax denominator also holds that head's sink logit ``sinks[h]``
+    (fp32, in the units of the scaled scores) and the sink contributes no value:
+        out = sum_t e^{s_t} v_t / (sum_t e^{s_t} + e^{sinks[h]}),  s_t = q . k_t * sm_scale.
+    A batch of one query token per request runs the decode kernel (split over the context),
+    any other batch the prefill kernel in causal mode; the sink enters both kernels' final
+    normalisation."""
+
+    def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD",
+                 window_left: int = -1, q_data_type=torch.bfloat16, kv_data_type=None,
+                 head_dim_qk: Optional[int] = None, head_dim_vo: Optional[int] = None,
+                 **_ignored) -> None:
+        if head_dim_vo not in (None, head_dim_qk):
+            raise NotImplementedError("BatchAttentionWithAttentionSinkWrapper: head_dim_vo != head_dim_qk")
+        self._window_left = -1 if window_left is None or window_left < 0 else int(window_left)
+        self._decode = BatchDecodeWithPagedKVCacheWrapper(float_workspace_buffer, kv_layout)
+        self._prefill = BatchPrefillWithPagedKVCacheWrapper(float_workspace_buffer, kv_layout)
+        self._use = None
+        self._Hq = 0
+
+    def plan(self, qo_indptr: torch.Tensor, paged_kv_indptr: torch.Tensor,
+             paged_kv_indices: torch.Tensor, paged_kv_last_page_len: torch.Tensor,
+             num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
+             causal: bool = True, window_left: Optional[int] = None, sm_scale: Optional[float] = None,
+             q_data_type=torch.bfloat16, kv_data_type=None, non_blocking: bool = True,
+             **_ignored) -> None:
+        name = "BatchAttentionWithAttentionSinkWrapper.plan"
+        if not causal:
+            raise NotImplementedError(f"{name}: causal=False")
+        wl = self._window_left if window_left is None else window_left
+        qo_h = qo_indptr.to("cpu", torch.int64)
+        single = qo_h.numel() > 1 and bool(((qo_h[1:] - qo_h[:-1]) == 1).all())
+        self._Hq = num_qo_heads
+        if single:
+            self._decode.plan(paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len,
+                              num_qo_heads, num_kv_heads, head_dim, page_size, window_left=wl,
+                              sm_scale=sm_scale, non_blocking=non_blocking)
+            self._use = self._decode
+        else:
+            self._prefill.plan(qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len,
+                               num_qo_heads, num_kv_heads, head_dim, page_size, causal=True,
+                               window_left=wl, sm_scale=sm_scale, non_blocking=non_blocking)
+            self._use = self._prefill
+
+    begin_forward = plan
+
+    def run(self, q: torch.Tensor,
+            paged_kv_cache: Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]],
+            sinks: torch.Tensor, sm_scale: Optional[float] = None,
+            out: Optional[torch.Tensor] = None, **_ignored) -> torch.Tensor:
+        name = "BatchAttentionWithAttentionSinkWrapper.run"
+        if self._use is None:
+            raise RuntimeError(f"{name}: plan() must be called before run()")
+        if not isinstance(sinks, torch.Tensor) or tuple(sinks.shape) != (self._Hq,):
+            raise ValueError(f"{name}: sinks must be a [{self._Hq}] tensor (one logit per query head)")
+        if not sinks.is_cuda or sinks.device != q.device:
+            raise RuntimeError(f"{name}: sinks must be on {q.device}")
+        s = sinks if sinks.dtype == torch.float32 and sinks.is_contiguous() else sinks.float().contiguous()
+        p = self._use._plan
+        if sm_scale is not None:
+            p = dict(p, sm_scale=float(sm_scale))
+        saved, self._use._plan = self._use._plan, p
+        try:
+            return self._use.run(q, paged_kv_cache, out=out, _sinks=s)
+        finally:
+            self._use._plan = saved
 
     forward = run
 

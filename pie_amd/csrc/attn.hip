@@ -58,6 +58,12 @@ __device__ __forceinline__ u32x4_t ld16v(const uint16_t* p) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// Attention sinks (gpt_oss.py:693-697): a per-head logit in the units of the scaled scores that
+// joins each row's softmax denominator and no value: the row's mass gains exp2(sink log2(e) - m)
+// relative to the row's running maximum m (0 when the row saw nothing).
+__device__ __forceinline__ float sink_mass(const float* sinks, int head, float m) {
+  return sinks ? fast_exp2(sinks[head] * 1.4426950408889634f - (m == -INFINITY ? 0.f : m)) : 0.f;
+}
 
 // Online softmax with a lazy maximum: a row's reference maximum (and with it the rescale of its
 // output accumulators and sum) moves only when a tile's scores exceed it by more than kLazyMax
@@ -318,7 +324,8 @@ template <int D>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv, int G, int Hq,
     float scale_log2, int splits, int window_left, uint16_t* __restrict__ out, int64_t o_ts,
-    int64_t o_hs, float* __restrict__ part_o, float* __restrict__ part_lse) {
+    int64_t o_hs, float* __restrict__ part_o, float* __restrict__ part_lse,
+    const float* __restrict__ sinks) {
   using W = WaveAttn<D>;
   constexpr int kVtile = kTileTokens * D;  // elements of one wave's V tile
   constexpr int kSmem = (4 * kVtile * 2 > 4 * 16 * (D + 2) * 4) ? 4 * kVtile * 2 : 4 * 16 * (D + 2) * 4;
@@ -426,10 +433,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         for (int e = 0; e < 8; ++e) acc[e] += src[e] * f;
       }
     }
+    const int hq = kvh * G + row;
+    // the sink joins the denominator once, after the splits are merged
+    if (splits == 1 && M != -INFINITY) L += sink_mass(sinks, hq, M);
     const float inv = L > 0.f ? 1.f / L : 0.f;
     #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] *= inv;
-    const int hq = kvh * G + row;
     if (splits == 1) {
       st16(out + (int64_t)b * o_ts + (int64_t)hq * o_hs + 8 * c, pack8(acc));
     } else {
@@ -447,7 +456,7 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(int B, int Hq, int split
                                                         const float* __restrict__ part_o,
                                                         const float* __restrict__ part_lse,
                                                         uint16_t* __restrict__ out, int64_t o_ts,
-                                                        int64_t o_hs) {
+                                                        int64_t o_hs, const float* __restrict__ sinks) {
   constexpr int CH = D / 8;
   const int b = blockIdx.x;
   const int hq = blockIdx.y * (64 / CH) + threadIdx.x / CH;
@@ -467,6 +476,7 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(int B, int Hq, int split
       for (int e = 0; e < 8; ++e) acc[e] += src[e] * f;
     }
   }
+  if (M != -INFINITY) L += sink_mass(sinks, hq, M);
   const float inv = L > 0.f ? 1.f / L : 0.f;
   #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] *= inv;
@@ -545,7 +555,7 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) vo
     int n_items, int n_kv_heads,
     int mode_in, int window_left, const uint32_t* __restrict__ packed,
     const int64_t* __restrict__ word_off, const int32_t* __restrict__ extent,
-    uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
+    uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs, const float* __restrict__ sinks) {
   using W = WaveAttn<D>;
   constexpr int NS = W::NS, NB = W::NB, CH = D / 8, RPI = 64 / CH;
   constexpr int RT = prefill_row_tiles<D>(), kPrefillRows = prefill_rows<D>();
@@ -773,7 +783,9 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) vo
   float inv[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    const float L = st[rt].row_sum(lane);
+    float L = st[rt].row_sum(lane);
+    const int R = row0 + 16 * RT * w + 16 * rt + n;
+    if (sinks && R < rows) L += sink_mass(sinks, kvh * G + R % G, st[rt].m);
     inv[rt] = L > 0.f ? 1.f / L : 0.f;
   }
   __syncthreads();
@@ -832,7 +844,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
     int n_items, int n_kv_heads,
     int mode_in, int window_left, const uint32_t* __restrict__ packed,
     const int64_t* __restrict__ word_off, const int32_t* __restrict__ extent,
-    uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
+    uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs, const float* __restrict__ sinks) {
   static_assert(D == 128, "32x32 prefill is built for head_dim 128");
   constexpr int NS = D / 16;  // QK k-steps
   constexpr int NB = D / 32;  // 32-dim output blocks
@@ -1070,7 +1082,8 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
   }
   // normalise and write: o[bb][i] is dim 32bb + 8(i/4) + 4kg + i%4 of row R; lanes r and r^32
   // together cover 8 consecutive dims
-  const float L = l_run + lane_read(l_run, lane ^ 32);
+  float L = l_run + lane_read(l_run, lane ^ 32);
+  if (valid) L += sink_mass(sinks, kvh * G + hg, m_run);
   const float inv = L > 0.f ? 1.f / L : 0.f;
   if (valid) {
     uint16_t* op = out + (int64_t)(q0 + tok) * o_ts + (int64_t)(kvh * G + hg) * o_hs;
@@ -1134,12 +1147,12 @@ template <int D>
 static void launch_decode(hipStream_t st, const uint16_t* q, int64_t q_ts, int64_t q_hs,
                           const PagedKV& kv, int G, int Hq, int Hkv, float sl2, int B, int splits,
                           int window_left, uint16_t* out, int64_t o_ts, int64_t o_hs, float* po,
-                          float* pl) {
+                          float* pl, const float* sinks) {
   hipLaunchKernelGGL(attn_decode_kernel<D>, dim3(B * splits, Hkv), dim3(256), 0, st, q, q_ts, q_hs, kv,
-                     G, Hq, sl2, splits, window_left, out, o_ts, o_hs, po, pl);
+                     G, Hq, sl2, splits, window_left, out, o_ts, o_hs, po, pl, sinks);
   if (splits > 1)
     hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(B, (Hq + 64 / (D / 8) - 1) / (64 / (D / 8))), dim3(64), 0,
-                       st, B, Hq, splits, po, pl, out, o_ts, o_hs);
+                       st, B, Hq, splits, po, pl, out, o_ts, o_hs, sinks);
 }
 
 static int attention_decode_impl(
@@ -1147,7 +1160,7 @@ static int attention_decode_impl(
     const pie_bf16* v_cache, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
     int64_t num_pages, const int32_t* kv_indptr, const int32_t* kv_indices,
     const int32_t* kv_last_page_len, int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
-    int64_t head_dim, int64_t page_size, float sm_scale, int64_t window_left, int64_t splits,
+    int64_t head_dim, int64_t page_size, float sm_scale, int64_t window_left, const float* sinks, int64_t splits,
     void* workspace, int64_t workspace_bytes, pie_bf16* out, int64_t o_tok_stride,
     int64_t o_head_stride, void* stream, const char* what) {
   PagedKV kv;
@@ -1182,11 +1195,11 @@ static int attention_decode_impl(
   const int W = window_left < 0 ? -1 : (int)std::min<int64_t>(window_left, 1 << 30);
   switch (head_dim) {
     case 64: launch_decode<64>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, W, out,
-                               o_tok_stride, o_head_stride, po, pl); break;
+                               o_tok_stride, o_head_stride, po, pl, sinks); break;
     case 128: launch_decode<128>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, W, out,
-                                 o_tok_stride, o_head_stride, po, pl); break;
+                                 o_tok_stride, o_head_stride, po, pl, sinks); break;
     default: launch_decode<256>(st, q, q_tok_stride, q_head_stride, kv, G, Hq, Hkv, sl2, B, S, W, out,
-                                o_tok_stride, o_head_stride, po, pl); break;
+                                o_tok_stride, o_head_stride, po, pl, sinks); break;
   }
   return check_launch(what);
 }
@@ -1196,13 +1209,13 @@ extern "C" int pie_hip_attention_decode(
     const pie_bf16* v_cache, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
     int64_t num_pages, const int32_t* kv_indptr, const int32_t* kv_indices,
     const int32_t* kv_last_page_len, int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
-    int64_t head_dim, int64_t page_size, float sm_scale, int64_t window_left, int64_t splits,
+    int64_t head_dim, int64_t page_size, float sm_scale, int64_t window_left, const float* sinks, int64_t splits,
     void* workspace, int64_t workspace_bytes, pie_bf16* out, int64_t o_tok_stride,
     int64_t o_head_stride, void* stream) {
   return attention_decode_impl(q, q_tok_stride, q_head_stride, k_cache, v_cache, page_stride,
                                slot_stride, head_stride, num_pages, kv_indptr, kv_indices,
                                kv_last_page_len, batch, num_qo_heads, num_kv_heads, head_dim,
-                               page_size, sm_scale, window_left, splits, workspace, workspace_bytes,
+                               page_size, sm_scale, window_left, sinks, splits, workspace, workspace_bytes,
                                out, o_tok_stride, o_head_stride, stream, "attention_decode");
 }
 
@@ -1242,7 +1255,7 @@ extern "C" int pie_hip_attention_decode_noalloc(
     const pie_bf16* v_cache, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
     int64_t num_pages, const int32_t* kv_indptr, const int32_t* kv_indices,
     const int32_t* kv_last_page_len, int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
-    int64_t head_dim, int64_t page_size, float sm_scale, int64_t window_left, int64_t splits,
+    int64_t head_dim, int64_t page_size, float sm_scale, int64_t window_left, const float* sinks, int64_t splits,
     pie_bf16* out, int64_t o_tok_stride, int64_t o_head_stride, void* stream) {
   const char* what = "attention_decode_noalloc";
   PIE_REQUIRE(batch >= 0 && splits >= 1 && splits <= 64 && num_qo_heads > 0 && head_dim > 0,
@@ -1260,7 +1273,7 @@ extern "C" int pie_hip_attention_decode_noalloc(
   return attention_decode_impl(q, q_tok_stride, q_head_stride, k_cache, v_cache, page_stride,
                                slot_stride, head_stride, num_pages, kv_indptr, kv_indices,
                                kv_last_page_len, batch, num_qo_heads, num_kv_heads, head_dim,
-                               page_size, sm_scale, window_left, splits, ws, kDecodeScratchBytes,
+                               page_size, sm_scale, window_left, sinks, splits, ws, kDecodeScratchBytes,
                                out, o_tok_stride, o_head_stride, stream, what);
 }
 
@@ -1349,18 +1362,18 @@ static void launch_prefill(hipStream_t st, dim3 grid, const uint16_t* q, int64_t
                            const PagedKV& kv, const int32_t* qo_indptr, int G, float sl2,
                            const int32_t* plan, int mode, int window_left, const uint32_t* packed,
                            const int64_t* woff, const int32_t* extent, uint16_t* out, int64_t o_ts,
-                           int64_t o_hs) {
+                           int64_t o_hs, const float* sinks) {
   // attn_prefill32_kernel scales raw scores inside the exponent, where a zero scale would turn a
   // hidden (-inf) score into NaN; 1e-30 gives the same result (every exponent rounds to 2^0).
   const dim3 xgrid(8 * ((grid.x * grid.y + 7) / 8));  // (kv head, item) units, padded to 8 XCDs
   if constexpr (D == 128 && PIE_PREFILL_MFMA32)
     hipLaunchKernelGGL(attn_prefill32_kernel<128>, xgrid, dim3(256), 0, st, q, q_ts, q_hs, kv, qo_indptr, G,
                        sl2 == 0.f ? 1e-30f : sl2, plan, (int)grid.x, (int)grid.y, mode, window_left, packed,
-                       woff, extent, out, o_ts, o_hs);
+                       woff, extent, out, o_ts, o_hs, sinks);
   else
     hipLaunchKernelGGL(attn_prefill_kernel<D>, xgrid, dim3(64 * prefill_waves<D>()), 0, st, q, q_ts, q_hs, kv,
                        qo_indptr, G, sl2, plan, (int)grid.x, (int)grid.y, mode, window_left, packed, woff,
-                       extent, out, o_ts, o_hs);
+                       extent, out, o_ts, o_hs, sinks);
 }
 
 // Visible extent of every query token under the packed mask: 1 + the last kv position whose bit
@@ -1387,7 +1400,7 @@ __global__ __launch_bounds__(256) void attn_mask_extent_kernel(const uint32_t* _
   for (int w = nw - 1; w >= 0; --w)
     if (row[w]) { e = 32 * w + 32 - __builtin_clz(row[w]); break; }
   // exactly causal: the extent is the causal one and every bit below it is set
-  bool causal = e == kv_len - (qo_indptr[b + 1] - qo_indptr[b]) + i + 1;
+  bool causal = e > 0 && e == kv_len - (qo_indptr[b + 1] - qo_indptr[b]) + i + 1;
   for (int w = 0; causal && 32 * w < e; ++w) {
     const int n = min(32, e - 32 * w);
     causal = row[w] == (n == 32 ? 0xffffffffu : (1u << n) - 1u);
@@ -1428,7 +1441,7 @@ extern "C" int pie_hip_attention_prefill(
     const pie_bf16* v_cache, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
     int64_t num_pages, const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
     const int32_t* kv_last_page_len, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
-    int64_t page_size, float sm_scale, int32_t mode, int64_t window_left,
+    int64_t page_size, float sm_scale, int32_t mode, int64_t window_left, const float* sinks,
     const uint32_t* packed_mask, const int32_t* mask_extent, const int32_t* plan, int64_t num_items,
     int64_t mask_offsets_word, pie_bf16* out,
     int64_t o_tok_stride, int64_t o_head_stride, void* stream) {
@@ -1461,11 +1474,11 @@ extern "C" int pie_hip_attention_prefill(
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (head_dim) {
     case 64: launch_prefill<64>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
-                                mode, Wl, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride); break;
+                                mode, Wl, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride, sinks); break;
     case 128: launch_prefill<128>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
-                                  mode, Wl, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride); break;
+                                  mode, Wl, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride, sinks); break;
     default: launch_prefill<256>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
-                                 mode, Wl, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride); break;
+                                 mode, Wl, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride, sinks); break;
   }
   return check_launch("attention_prefill");
 }

@@ -46,7 +46,7 @@ using namespace pie;
 
 extern "C" const char* pie_hip_last_error(void) { return g_err; }
 
-extern "C" int pie_hip_abi_version(void) { return 2; }
+extern "C" int pie_hip_abi_version(void) { return 3; }
 
 // Standard RoPE frequencies, f_i = 1 / (rope_scale * theta^(2i/rd)) (flashinfer's
 // apply_rope_pos_ids with rope_scale; metal_rope.metal:63-64 with rope_factor = 1).

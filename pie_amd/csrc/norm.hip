@@ -376,8 +376,12 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
   const bool large = PIE_NORM_LARGE_NT && in_bytes >= (int64_t)64 << 20;  // far larger than L2
   // (the residual-add form only: a plain norm, one input stream, keeps too few bytes in flight at
   // one vector per lane and stays on the row-loop kernel with 4 vectors per lane)
-  if (ADD && vec && large && a.set[1].rows == 0 && a.cols % 4096 == 0 && a.cols <= 3 * 4096 &&
-      rows < 0x7fffffff) {
+  static const bool forced_rowblock = [] {  // tuning override: PIE_HIP_NORM_ROWBLOCK=1
+    const char* e = getenv("PIE_HIP_NORM_ROWBLOCK");
+    return e && atoi(e) == 1;
+  }();
+  if ((ADD || forced_rowblock) && vec && large && a.set[1].rows == 0 && a.cols % 4096 == 0 &&
+      a.cols <= 3 * 4096 && rows < 0x7fffffff) {
     const dim3 grd((unsigned)rows), tb(512);
     switch (a.cols / 4096) {
       case 1: hipLaunchKernelGGL((rmsnorm_row_block<1, ADD, GEMMA>), grd, tb, 0, st, a); break;

@@ -46,7 +46,8 @@ HOT_PATH = (
     "apply_rope_with_cos_sin_cache_inplace",
 )
 # flashinfer's attention wrapper classes (llama3.py:293-313)
-ATTENTION = ("BatchDecodeWithPagedKVCacheWrapper", "BatchPrefillWithPagedKVCacheWrapper")
+ATTENTION = ("BatchDecodeWithPagedKVCacheWrapper", "BatchPrefillWithPagedKVCacheWrapper",
+             "BatchAttentionWithAttentionSinkWrapper")  # the last: gpt_oss.py:420-438
 
 
 class _Namespace(types.ModuleType):

@@ -44,7 +44,7 @@ void oracle_attention(const uint16_t*, int64_t, int64_t, const uint16_t*, const 
                       int64_t, int64_t, const int32_t*, const int32_t*, const int32_t*, const int32_t*,
                       const uint8_t*, const int64_t*, int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
                       double,
-                      uint16_t*, int64_t, int64_t, double*);
+                      uint16_t*, int64_t, int64_t, double*, const float*);
 void oracle_sample(const float*, int64_t, int64_t, int64_t, int, const int32_t*, const float*, const float*,
                    const double*, int32_t*, unsigned char*);
 void oracle_scaled_softmax(const float*, int64_t, int64_t, const float*, double, double*);
@@ -355,8 +355,13 @@ static void case_variants(int64_t T, int64_t H, int64_t Hq, int64_t Hkv, int64_t
 // ---------------------------------------------------------------------------- attention
 // Paged decode attention: contexts in [lo, hi], random page permutation of an exact-size pool,
 // NHD cache; `chunk` = splits per request (0 = the library's choice).
+static void fill_sinks(Buf<float>& sk) {
+  std::uniform_real_distribution<float> du(-3.f, 8.f);  // from negligible to dominant
+  for (size_t i = 0; i < sk.n; ++i) sk[i] = du(rng);
+}
+
 static void case_attn_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int lo, int hi,
-                             int64_t chunk, int64_t window = -1) {
+                             int64_t chunk, int64_t window = -1, bool with_sinks = false) {
   printf("attn_decode B=%lld Hq=%lld Hkv=%lld D=%lld P=%lld ctx=[%d,%d] chunk=%lld window=%lld\n", (long long)B,
          (long long)Hq, (long long)Hkv, (long long)D, (long long)P, lo, hi, (long long)chunk, (long long)window);
   std::vector<int32_t> len(B), indptr(B + 1, 0), last(B);
@@ -379,18 +384,23 @@ static void case_attn_decode(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int6
   Buf<uint16_t> cache(pages * page_elems), q(B * Hq * D), out(B * Hq * D), want(B * Hq * D);
   fill_normal(cache);
   fill_normal(q);
+  Buf<float> sk(Hq);
+  fill_sinks(sk);
+  const float* sinks_ptr = with_sinks ? sk.p : nullptr;
+  if (with_sinks) printf("  with attention sinks\n");
   int64_t splits = chunk;
   if (splits <= 0) rc_ok(pie_hip_attention_decode_plan(B, Hkv, hi, 4, &splits), "decode_plan");
   Buf<float> ws(std::max<int64_t>(B * splits * Hq * (D + 1), 1));
   rc_ok(pie_hip_attention_decode(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D,
                                  pages, ip.p, idx.p, ll.p, B, Hq, Hkv, D, P, 1.f / sqrtf((float)D),
-                                 window, splits, ws.p, (int64_t)(ws.n * 4), out.p, Hq * D, D, nullptr),
+                                 window, sinks_ptr, splits, ws.p, (int64_t)(ws.n * 4), out.p, Hq * D, D,
+                                 nullptr),
         "attention_decode");
   std::vector<int32_t> qo(B + 1);
   for (int64_t b = 0; b <= B; ++b) qo[b] = (int32_t)b;
   oracle_attention(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, qo.data(), ip.p,
                    idx.p, ll.p, nullptr, nullptr, 1, window, B, Hq, Hkv, D, P, 1.0 / sqrt((double)D), want.p, Hq * D,
-                   D, nullptr);
+                   D, nullptr, sinks_ptr);
   printf("  splits %lld\n", (long long)splits);
   check_close("decode attention", out.p, want.p, B * Hq * D);
   // tighter: attention outputs are averages (|o| < 1 here), so a dropped or doubled token
@@ -428,15 +438,15 @@ static void case_attn_decode_noalloc() {
     fill_normal(q);
     Buf<float> ws(B * S * Hq * (D + 1));
     rc_ok(pie_hip_attention_decode(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D,
-                                   pages, ip.p, idx.p, ll.p, B, Hq, Hkv, D, P, 0.09f, -1, S, ws.p,
+                                   pages, ip.p, idx.p, ll.p, B, Hq, Hkv, D, P, 0.09f, -1, nullptr, S, ws.p,
                                    (int64_t)(ws.n * 4), a.p, Hq * D, D, nullptr), "decode");
     rc_ok(pie_hip_attention_decode_noalloc(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems,
                                            Hkv * D, D, pages, ip.p, idx.p, ll.p, B, Hq, Hkv, D, P, 0.09f,
-                                           -1, S, b2.p, Hq * D, D, nullptr), "decode_noalloc");
+                                           -1, nullptr, S, b2.p, Hq * D, D, nullptr), "decode_noalloc");
     check_equal("noalloc decode == workspace decode", b2.p, a.p, a.n);
   }
   const int rc = pie_hip_attention_decode_noalloc(nullptr, 0, 0, nullptr, nullptr, 0, 0, 0, 1, nullptr,
-                                                  nullptr, nullptr, 256, 32, 8, 128, 16, 1.f, -1, 64,
+                                                  nullptr, nullptr, 256, 32, 8, 128, 16, 1.f, -1, nullptr, 64,
                                                   nullptr, 0, 0, nullptr);
   if (rc != PIE_HIP_EINVAL) { printf("  FAIL: oversize noalloc decode accepted\n"); ++failures; }
 }
@@ -509,7 +519,12 @@ static void case_group(int64_t B, int64_t H, int64_t I, int64_t V, bool gelu) {
 // Paged prefill attention: requests with ctx in [0, cmax] cached tokens and qo in [0, qmax] new
 // query tokens; mode 0 full, 1 causal, 2 a random custom mask.
 static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int cmax, int qmax,
-                              int mode, bool causal_mask = false, int64_t window = -1) {
+                              int mode, bool causal_mask = false, int64_t window = -1,
+                              bool with_sinks = false) {
+  Buf<float> sk(Hq);
+  fill_sinks(sk);
+  const float* sinks_ptr = with_sinks ? sk.p : nullptr;
+  if (with_sinks) printf("with attention sinks: ");
   printf("attn_prefill B=%lld Hq=%lld Hkv=%lld D=%lld P=%lld ctx<=%d qo<=%d mode=%d window=%lld\n", (long long)B,
          (long long)Hq, (long long)Hkv, (long long)D, (long long)P, cmax, qmax, mode, (long long)window);
   std::vector<int32_t> qo(B + 1, 0), indptr(B + 1, 0), last(B), kvl(B);
@@ -563,13 +578,15 @@ static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
           "pack_mask");
   rc_ok(pie_hip_attention_prefill(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, pages,
                                   qi.p, ip.p, idx.p, ll.p, Hq, Hkv, D, P, 1.f / sqrtf((float)D), mode, window,
+                                  sinks_ptr,
                                   mode == 2 ? packed.p : nullptr, mode == 2 ? extent.p : nullptr, plan.p, items,
                                   plan[4], out.p, Hq * D, D,
                                   nullptr),
         "attention_prefill");
   oracle_attention(q.p, Hq * D, D, cache.p, cache.p + P * Hkv * D, page_elems, Hkv * D, D, qi.p, ip.p, idx.p,
                    ll.p, mode == 2 ? mask.p : nullptr, mode == 2 ? moff.data() : nullptr, mode == 1, window, B, Hq,
-                   Hkv, D, P, 1.0 / sqrt((double)D), want.p, Hq * D, D, nullptr);
+                   Hkv, D, P, 1.0 / sqrt((double)D), want.p, Hq * D,
+                   D, nullptr, sinks_ptr);
   printf("  T=%lld items=%lld\n", (long long)T, (long long)items);
   check_close("prefill attention", out.p, want.p, T * Hq * D);
   float worst = 0.f;
@@ -737,6 +754,8 @@ int main(int argc, char** argv) {
     case_attn_decode(2, 16, 1, 128, 5, 20, 700, 5);   // G = 16, page size 5
     case_attn_decode(2, 4, 2, 64, 1, 600, 1500, 1);   // page size 1: several page-table windows
     case_attn_decode(3, 8, 2, 128, 16, 1, 700, 3, 100);  // sliding window of 100 (+ the query)
+    case_attn_decode(3, 8, 2, 128, 16, 1, 300, 1, -1, true);   // attention sinks, one split
+    case_attn_decode(3, 8, 2, 64, 16, 0, 500, 3, 60, true);    // sinks + merge + window
   }
   if (all || c == "sample") {
     for (int mode = 0; mode <= 4; ++mode) case_sample(mode == 4 ? 5 : 3, 301, mode, mode == 4);
@@ -769,6 +788,8 @@ int main(int argc, char** argv) {
     case_attn_prefill(3, 8, 2, 128, 16, 20, 120, 2, true);  // masks within the causal window
     case_attn_prefill(3, 8, 2, 128, 16, 200, 120, 1, false, 70);  // causal + sliding window
     case_attn_prefill(2, 8, 2, 128, 8, 100, 90, 2, false, 40);    // custom mask + sliding window
+    case_attn_prefill(3, 8, 2, 128, 16, 60, 70, 1, false, -1, true);  // causal + sinks (32-row kernel)
+    case_attn_prefill(2, 4, 2, 64, 16, 30, 40, 1, false, 20, true);   // D = 64 + window + sinks
   }
   if (all || c == "group") {
     case_group(5, 4096, 1536, 40, false);  // 8 norm vectors per lane pair (NJ = 2)

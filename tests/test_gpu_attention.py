@@ -436,3 +436,52 @@ def test_prefill_negative_and_zero_scale(dev, sm_scale):
                             N(pb.kv_indices), N(pb.kv_last_page_len), causal=True,
                             sm_scale=sm_scale)
     _tight(got, want, f"sm_scale {sm_scale}")
+
+
+# ----------------------------------------------------------------------------- attention sinks
+def _sink_run(dev, a, sinks, window_left=-1):
+    """gpt-oss's calls: BatchAttentionWithAttentionSinkWrapper construction, plan (causal, with the
+    layer's window), run(q, kv_cache_layer, sinks, scaling) (gpt_oss.py:420-438, :839-870, :693-697)."""
+    pb = a["batch"]
+    w = attention.BatchAttentionWithAttentionSinkWrapper(_workspace(dev), kv_layout=a["layout"],
+                                                         window_left=window_left,
+                                                         head_dim_qk=a["D"], head_dim_vo=a["D"])
+    w.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev),
+           pb.kv_last_page_len.to(dev), a["Hq"], a["Hkv"], a["D"], pb.page_size, causal=True,
+           window_left=window_left, q_data_type=torch.bfloat16, non_blocking=True)
+    o = w.run(a["q"].to(dev), a["cache"].to(dev), torch.as_tensor(sinks).to(dev), a["D"] ** -0.5)
+    torch.cuda.synchronize()
+    return o, w._use
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("window_left", [-1, 100])
+def test_sink_wrapper_decode_batch(dev, D, window_left):
+    print(f"sinks decode D={D} window={window_left}", flush=True)
+    g = torch.Generator().manual_seed(31 + D)
+    ctx = torch.randint(0, 900, (12,), generator=g).to(torch.int32)
+    a = wl.attn_batch(ctx, torch.ones(12, dtype=torch.int32), Hq=16, Hkv=2, D=D, page_size=16, seed=33)
+    sinks = torch.linspace(-3, 7, 16, dtype=torch.float32)
+    got, used = _sink_run(dev, a, sinks, window_left)
+    assert isinstance(used, attention.BatchDecodeWithPagedKVCacheWrapper)
+    pb = a["batch"]
+    want = oracle.attention(N(a["q"]), N(a["cache"]), N(pb.qo_indptr), N(pb.kv_indptr), N(pb.kv_indices),
+                            N(pb.kv_last_page_len), window_left=window_left, sinks=sinks.numpy())
+    assert_bf16_close(N(got), want, what="sink decode")
+    _tight(got, want, "sink decode")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_sink_wrapper_prefill_batch(dev, D):
+    print(f"sinks prefill D={D}", flush=True)
+    a = wl.attn_batch([37, 0, 5, 160], [1, 90, 12, 33], Hq=8, Hkv=2, D=D, page_size=16, seed=35)
+    sinks = torch.linspace(-2, 6, 8, dtype=torch.float32)
+    got, used = _sink_run(dev, a, sinks)
+    assert isinstance(used, attention.BatchPrefillWithPagedKVCacheWrapper)
+    pb = a["batch"]
+    want = oracle.attention(N(a["q"]), N(a["cache"]), N(pb.qo_indptr), N(pb.kv_indptr), N(pb.kv_indices),
+                            N(pb.kv_last_page_len), sinks=sinks.numpy())
+    assert_bf16_close(N(got), want, what="sink prefill")
+    _tight(got, want, "sink prefill")
+    plain = _want(a)
+    assert (oracle.bf16_to_f32(N(got)) != oracle.bf16_to_f32(plain)).mean() > 0.5  # the sinks matter

@@ -648,3 +648,55 @@ def test_scaled_softmax_vs_torch_reference():
     want = torch.where(temps[:, None] < 1e-5, greedy, soft)
     np.testing.assert_allclose(oracle.scaled_softmax(x.numpy(), temps.numpy()), want.numpy(),
                                rtol=1e-12, atol=1e-300)
+
+
+def _sink_reference(a, sinks, window_left=-1):
+    """The published gpt-oss form, in torch float64: the head's sink logit appended as one more
+    score column, softmax over the row, the sink column dropped, then the product with v."""
+    pb, q = a["batch"], a["q"].to(torch.float64)
+    G, D = a["Hq"] // a["Hkv"], a["D"]
+    out = torch.zeros_like(q)
+    for b in range(pb.seq_lens.numel()):
+        q0, q1 = int(pb.qo_indptr[b]), int(pb.qo_indptr[b + 1])
+        kv_len, qo_len = int(pb.seq_lens[b]), q1 - q0
+        if qo_len == 0:
+            continue
+        k, v = _gather_kv(a["cache"], pb, b, a["layout"])
+        k = k.repeat_interleave(G, dim=1).transpose(0, 1)  # [Hq, kv, D]
+        v = v.repeat_interleave(G, dim=1).transpose(0, 1)
+        s = q[q0:q1].transpose(0, 1) @ k.transpose(1, 2) / math.sqrt(D)  # [Hq, qo, kv]
+        m = torch.tensor([[t <= kv_len - qo_len + i and (window_left < 0 or t >= kv_len - qo_len + i - window_left)
+                           for t in range(kv_len)] for i in range(qo_len)], dtype=torch.bool)
+        s = s.masked_fill(~m, -math.inf)
+        col = torch.as_tensor(sinks, dtype=torch.float64)[:, None, None].expand(-1, qo_len, 1)
+        w = torch.softmax(torch.cat([s, col], -1), -1)[..., :-1]
+        out[q0:q1] = (w @ v).transpose(0, 1)
+    return out
+
+
+@pytest.mark.parametrize("window_left", [-1, 7])
+def test_attention_sinks_vs_gpt_oss_form(window_left):
+    a = wl.attn_batch([37, 0, 5, 60], [1, 19, 12, 3], Hq=8, Hkv=2, D=64, page_size=16, seed=21)
+    sinks = np.linspace(-3, 6, 8).astype(np.float32)
+    want = _sink_reference(a, sinks, window_left).to(torch.float32).numpy()
+    got = oracle.bf16_to_f32(_oracle_attn(a, sinks=sinks, window_left=window_left))
+    assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+    # the sinks change the result (by up to a factor e^6 / (sum of the row's weights))
+    assert np.abs(got - oracle.bf16_to_f32(_oracle_attn(a, window_left=window_left))).max() > 0.05
+
+
+def test_attention_sink_limits_and_closed_form():
+    a = wl.attn_batch([12, 30], [3, 1], Hq=4, Hkv=2, D=32, page_size=8, seed=22)
+    plain = _oracle_attn(a)
+    # a sink of -inf adds nothing: plain attention, bit for bit
+    assert_bits_equal(_oracle_attn(a, sinks=np.full(4, -np.inf, np.float32)), plain, "sink -inf")
+    # a dominant sink takes all the mass: the output vanishes
+    assert not oracle.bf16_to_f32(_oracle_attn(a, sinks=np.full(4, 1e4, np.float32))).any()
+    # one visible position with score s: out = v / (1 + e^(sink - s))
+    a = wl.attn_batch([0], [1], Hq=2, Hkv=1, D=16, page_size=4, seed=23)
+    k, v = _gather_kv(a["cache"], a["batch"], 0)
+    s = ((a["q"][0].to(torch.float64) * k[0]).sum(-1) / 4.0).numpy()
+    sk = np.array([0.5, -1.0], np.float32)
+    want = v[0, 0].numpy()[None, :] / (1 + np.exp(sk.astype(np.float64) - s))[:, None]
+    got = oracle.bf16_to_f32(_oracle_attn(a, sinks=sk))[0]
+    np.testing.assert_allclose(got, want, rtol=2 ** -8, atol=1e-6)

@@ -38,7 +38,7 @@ def _run(a, dev, splits, noalloc, ws=None):
     st = torch.cuda.current_stream().cuda_stream
     common = (q.data_ptr(), q.stride(0), q.stride(1), kp, vp, ps, ss, hs, npages, ip.data_ptr(),
               ix.data_ptr(), ll.data_ptr(), B, Hq, Hkv, D, a["batch"].page_size,
-              C.c_float(D ** -0.5), -1, splits)
+              C.c_float(D ** -0.5), -1, None, splits)
     if noalloc:
         _lib.call("pie_hip_attention_decode_noalloc", *common, out.data_ptr(), out.stride(0),
                   out.stride(1), st)
@@ -82,5 +82,5 @@ def test_noalloc_decode_rejects_oversize(dev):
     # 256 x 64 splits x 32 heads x 129 x 4 bytes = 270 MB > the 32 MiB array; rejected before launch
     lib = _lib.load()
     rc = lib.pie_hip_attention_decode_noalloc(16, 0, 0, 16, 16, 0, 0, 0, 1, 16, 16, 16, 256, 32, 8,
-                                              128, 16, C.c_float(1.0), -1, 64, 16, 0, 0, None)
+                                              128, 16, C.c_float(1.0), -1, None, 64, 16, 0, 0, None)
     assert rc == 1 and "static scratch" in lib.pie_hip_last_error().decode()
