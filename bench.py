@@ -272,8 +272,9 @@ def measure_ops(dev, cold_iters=20, only=None):
 
 
 def _ops_ceiling(dev, run):
-    """Measured ceilings for two access patterns (pie_amd/probe/probe.hip, no arithmetic and no
-    index logic): configuration 1's bytes as a plain copy (8 MiB read, 8 MiB written) and
+    """Measured ceilings for access patterns (pie_amd/probe/probe.hip, no arithmetic and no
+    index logic): configuration 1's bytes as a plain copy (8 MiB read, 8 MiB written), the
+    sampling softmax's bytes as a plain copy (one read and one write of [256, 128256] bf16), and
     configuration 3's paged append as a scatter of the same 2 KiB k / v rows from the same qkv
     rows to the same cache slots, the slot offsets computed beforehand (plus their 16 B per row)."""
     import ctypes as C
@@ -292,8 +293,16 @@ def _ops_ceiling(dev, run):
         a = torch.empty(n1, dtype=torch.uint8, device=dev)
         b = torch.empty_like(a)
         return lambda: lib.pie_probe_copy(a.data_ptr(), b.data_ptr(), n1, nt, st())
+    n_sm = 256 * 128256 * 2
+
+    def make_copy_sm():
+        a = torch.empty(n_sm, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        return lambda: lib.pie_probe_copy(a.data_ptr(), b.data_ptr(), n_sm, 1, st())
     res = [run("ceiling copy 8 MiB -> 8 MiB (cfg1 bytes), cached", 2 * n1, lambda: make_copy(0)),
-           run("ceiling copy 8 MiB -> 8 MiB (cfg1 bytes), non-temporal", 2 * n1, lambda: make_copy(1))]
+           run("ceiling copy 8 MiB -> 8 MiB (cfg1 bytes), non-temporal", 2 * n1, lambda: make_copy(1)),
+           run("ceiling copy 64 MB -> 64 MB (softmax bytes, [256,128256] bf16), non-temporal",
+               2 * n_sm, make_copy_sm)]
     c = wl.cfg3()
     pb, T = c["batch"], c["qkv"].shape[0]
     Hq, Hkv, D, P = 32, 8, 128, pb.page_size

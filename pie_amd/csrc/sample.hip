@@ -862,16 +862,68 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
       x[0] = __uint_as_float(q.x); x[1] = __uint_as_float(q.y); x[2] = __uint_as_float(q.z); x[3] = __uint_as_float(q.w);
     }
   };
-  float mx = xt;
+  // Online pass over this thread's elements in load order (loads complete in order, so each
+  // vector is consumed as it lands and the exponentials overlap the loads still in flight):
+  // running maximum m and s = sum of exp2((x - m) c), rescaled when m grows. Each vector's
+  // exponentials replace its logits in registers (bf16 rows: rounded to bf16, which with the
+  // final rounding stays within 2^-8 relative; fp32 rows: exact), with the reference maximum
+  // mref[j] they were taken against, so the output pass needs one exponential per vector
+  // (exp2((mref[j] - M) c)) instead of one per element. Rows of more than 16 vectors per thread
+  // keep their logits (no registers to spare for mref) and recompute the exponentials. Greedy
+  // rows need the maximum only.
+  constexpr bool kKeep = NV <= 16;
+  float m = -INFINITY, s = 0.f, mref[kKeep ? NV : 1];
+  float et = 0.f, mt = -INFINITY;  // the tail element's exponential and its reference
+  if constexpr (!kKeep) {  // the maximum first, the sum after the block maximum is known
+    m = xt;
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    if (threadIdx.x + j * kSampThreads >= nv) break;
-    float x[E];
-    unpack(d[j], x);
+    for (int j = 0; j < NV; ++j) {
+      if (threadIdx.x + j * kSampThreads >= nv) break;
+      float x[E];
+      unpack(d[j], x);
 #pragma unroll
-    for (int e = 0; e < E; ++e) mx = fmaxf(mx, x[e]);
+      for (int e = 0; e < E; ++e) m = fmaxf(m, x[e]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      mref[j] = -INFINITY;
+      if (threadIdx.x + j * kSampThreads >= nv) break;
+      float x[E];
+      unpack(d[j], x);
+      float mj = x[0];
+#pragma unroll
+      for (int e = 1; e < E; ++e) mj = fmaxf(mj, x[e]);
+      if (mj > m) {
+        s *= __builtin_amdgcn_exp2f((m - mj) * c);  // m = -inf: s is still 0
+        m = mj;
+      }
+      if (!greedy_row) {
+        const float mc = m * c;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          x[e] = __builtin_amdgcn_exp2f(fmaf(x[e], c, -mc));
+          s += x[e];
+        }
+        mref[j] = m;
+        if (BF16) d[j] = pack8(x);
+        else d[j] = make_uint4(__builtin_bit_cast(uint32_t, x[0]), __builtin_bit_cast(uint32_t, x[1]),
+                               __builtin_bit_cast(uint32_t, x[2]), __builtin_bit_cast(uint32_t, x[3]));
+      }
+    }
+    if (it < V) {
+      if (xt > m) {
+        s *= __builtin_amdgcn_exp2f((m - xt) * c);
+        m = xt;
+      }
+      mt = m;
+      if (!greedy_row) {
+        et = __builtin_amdgcn_exp2f(fmaf(xt, c, -m * c));
+        s += et;
+      }
+    }
   }
-  const float M = block_max_f(mx, red);
+  const float M = block_max_f(m, red);
   if (greedy_row) {
     int am = 0x7fffffff;  // first index holding the maximum
 #pragma unroll
@@ -898,14 +950,18 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
     if (it < V) IO::put(orow, it, it == A ? 1.f : 0.f);
     return;
   }
-  float s = it < V ? __builtin_amdgcn_exp2f((xt - M) * c) : 0.f;
+  if constexpr (kKeep) {
+    s = m == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f((m - M) * c);
+  } else {
+    s = it < V ? __builtin_amdgcn_exp2f((xt - M) * c) : 0.f;
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    if (threadIdx.x + j * kSampThreads >= nv) break;
-    float x[E];
-    unpack(d[j], x);
+    for (int j = 0; j < NV; ++j) {
+      if (threadIdx.x + j * kSampThreads >= nv) break;
+      float x[E];
+      unpack(d[j], x);
 #pragma unroll
-    for (int e = 0; e < E; ++e) s += __builtin_amdgcn_exp2f((x[e] - M) * c);
+      for (int e = 0; e < E; ++e) s += __builtin_amdgcn_exp2f((x[e] - M) * c);
+    }
   }
   const float inv = 1.f / block_sum_f(s, red);
 #pragma unroll
@@ -914,11 +970,19 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
     if (v >= nv) break;
     float x[E];
     unpack(d[j], x);
+    if constexpr (kKeep) {
+      const float f = __builtin_amdgcn_exp2f((mref[j] - M) * c) * inv;
 #pragma unroll
-    for (int e = 0; e < E; ++e) x[e] = __builtin_amdgcn_exp2f((x[e] - M) * c) * inv;
+      for (int e = 0; e < E; ++e) x[e] *= f;
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) x[e] = __builtin_amdgcn_exp2f((x[e] - M) * c) * inv;
+    }
     IO::store(orow, (int64_t)v * E, x);
   }
-  if (it < V) IO::put(orow, it, __builtin_amdgcn_exp2f((xt - M) * c) * inv);
+  if (it < V)
+    IO::put(orow, it, kKeep ? et * (__builtin_amdgcn_exp2f((mt - M) * c) * inv)
+                            : __builtin_amdgcn_exp2f((xt - M) * c) * inv);
 }
 
 }  // namespace pie
