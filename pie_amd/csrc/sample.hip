@@ -29,6 +29,9 @@
 
 namespace pie {
 
+#ifndef PIE_SAMPLE_STOP
+#define PIE_SAMPLE_STOP 0  // measurement switch: 1 / 2 / 3 end the kernel after the floor / the gather / the short-list thresholds
+#endif
 constexpr int kSampThreads = 1024;
 constexpr int kSampWaves = kSampThreads / 64;
 constexpr double kMassScale = 1099511627776.0;  // 2^40
@@ -245,6 +248,107 @@ struct SampleArgs {
   int32_t vec;  // rows are 16-byte aligned: 16-byte loads
 };
 
+// Short candidate lists (at most kSampThreads elements, in LDS): the top_k / top_p thresholds from
+// a bitonic sort of the keys (one per thread; compare-exchange partners within a wave through
+// ds_bpermute, across waves through LDS), a block scan of the sorted masses, and one thread
+// that sees the cut. Radix passes over such lists serialise on LDS atomics: the keys of a row's
+// largest probabilities share their top bits, so every count lands in one or two bins. Same
+// kept sets as the radix selects: top_k keeps keys >= the k-th largest (ties stay), top_p keeps
+// keys >= the smallest key whose strictly larger keys' mass is below top_p * mass (the maximal
+// key when that product is <= 0).
+__device__ __forceinline__ uint32_t sort_desc_keys(uint32_t v, uint32_t* buf) {
+  const int t = threadIdx.x, lane = t & 63;
+  for (int k = 2; k <= kSampThreads; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      uint32_t pv;
+      if (j >= 64) {
+        __syncthreads();
+        buf[t] = v;
+        __syncthreads();
+        pv = buf[t ^ j];
+      } else {
+        pv = (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ j) << 2, (int)v);
+      }
+      const bool desc = (t & k) == 0;     // this k-block sorts descending (the whole array at the end)
+      const bool first = (t & j) == 0;  // the lower position of the pair
+      v = (first == desc) ? max(v, pv) : min(v, pv);
+    }
+  }
+  return v;
+}
+
+// Returns lo for the list p[0, n) (n <= kSampThreads): the smallest kept key under the row's
+// top_k / top_p (modes 1, 2, 4), as sample_row's radix selects would give it.
+__device__ uint32_t list_threshold(const float* p, int n, const SampleArgs& a, int r, int64_t npos,
+                                   uint64_t row_tot, SampleShared& sh, uint32_t* buf) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  uint32_t v = t < n ? prob_key(p[t]) : 0u;
+  v = sort_desc_keys(v, buf);  // position t now holds the (t+1)-th largest key
+  const uint64_t m = v ? prob_mass(__builtin_bit_cast(float, v)) : 0ull;
+  // inclusive block scan of the masses in sorted order
+  uint64_t incl = m;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t y = shfl_u64(incl, lane >= o ? lane - o : lane);
+    if (lane >= o) incl += y;
+  }
+  __syncthreads();
+  if (lane == 63) sh.wsum[w] = incl;
+  buf[t] = v;
+  if (t == 0) { sh.u32a = 1u; sh.u32b = (uint32_t)n; sh.u64a = 0; }
+  __syncthreads();
+  for (int i = 0; i < w; ++i) incl += sh.wsum[i];
+  const uint64_t excl = incl - m;
+  uint32_t lo = 1u;
+  int lim = n;  // positions [0, lim) hold the keys >= lo
+  if (a.mode == 2 || a.mode == 4) {
+    const int32_t k = a.top_k ? a.top_k[r] : a.top_k_s;
+    int64_t np = npos;
+    if (np < 0) {  // the list's count of p > 0 (sorted: the first zero key's position)
+      if (t == 0) sh.pick = 0;
+      __syncthreads();
+      if (v != 0u && (t + 1 == kSampThreads || buf[t + 1] == 0u)) sh.pick = t + 1;
+      __syncthreads();
+      np = sh.pick;
+    }
+    if (k > 0 && k < n && (int64_t)k < np) {
+      lo = max(1u, buf[k - 1]);
+      // the top-k set: every position whose key is >= the k-th largest
+      if (v >= lo && (t + 1 == n || buf[t + 1] < lo)) { sh.u32b = (uint32_t)(t + 1); sh.u64a = incl; }
+      __syncthreads();
+      lim = (int)sh.u32b;
+    } else {
+      __syncthreads();
+    }
+  }
+  if (a.mode == 1 || a.mode == 4) {
+    const float tp = a.top_p ? a.top_p[r] : a.top_p_s;
+    uint64_t tot;
+    if (a.mode == 1 && row_tot) {
+      tot = row_tot;
+    } else if (lim < n) {
+      tot = sh.u64a;
+    } else {  // every key >= lo: the list's mass
+      __syncthreads();
+      if (t == kSampThreads - 1) sh.u64a = incl;
+      __syncthreads();
+      tot = sh.u64a;
+    }
+    const double thr = (double)tp * (double)tot;
+    __syncthreads();
+    if (t == 0) sh.u32a = 0u;
+    __syncthreads();
+    // the last position whose strictly-before mass is below thr (ties before it share its key)
+    if (t < lim && v != 0u && (double)excl < thr && (t + 1 == lim || !((double)incl < thr))) sh.u32a = v;
+    __syncthreads();
+    uint32_t tkey = sh.u32a;
+    if (tkey == 0u && lim > 0 && buf[0] != 0u) tkey = buf[0];  // thr <= 0: the maximal key
+    if (tkey > lo) lo = tkey;
+  }
+  __syncthreads();  // buf is reused by the caller
+  return lo;
+}
+
 // Draw for output row r from the values p[0, V): thresholds by radix select, then the inverse CDF
 // in order. idx (optional) maps a position in p to the vocabulary index (p is then the row's
 // candidate list, ascending in vocabulary index). npos: the row's count of p > 0 (-1: count it
@@ -253,14 +357,22 @@ struct SampleArgs {
 // decide it are the same as over the whole row.
 __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, int V, bool vec,
                                            const SampleArgs& a, int r, int64_t npos, uint64_t row_tot,
-                                           SampleShared& sh) {
+                                           SampleShared& sh, uint32_t* list_buf = nullptr) {
   if (V == 0) {  // nothing to draw from (an empty candidate list)
     if (threadIdx.x == 0) a.out[r] = -1;
     return;
   }
+
   // lower bound on kept keys (1 = every p > 0)
   uint32_t lo = 1u;
-  if (a.mode == 2 || a.mode == 4) {
+  const bool short_list = list_buf && idx && V <= kSampThreads && a.mode != 3;
+  if (short_list) {
+    lo = list_threshold(p, V, a, r, npos, row_tot, sh, list_buf);
+#if PIE_SAMPLE_STOP == 3
+    if (threadIdx.x == 0) a.out[r] = (int)lo;
+    return;
+#endif
+  } else if (a.mode == 2 || a.mode == 4) {
     const int32_t k = a.top_k ? a.top_k[r] : a.top_k_s;
     if (k > 0 && k < V) {
       if (npos < 0) {
@@ -271,7 +383,7 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
       if ((int64_t)k < npos) lo = max(1u, radix_threshold(p, V, vec, 1u, false, (uint32_t)k, 0.0, sh));
     }
   }
-  if (a.mode == 1 || a.mode == 4) {
+  if (!short_list && (a.mode == 1 || a.mode == 4)) {
     const float tp = a.top_p ? a.top_p[r] : a.top_p_s;
     uint64_t tot = 0;
     if (a.mode == 1 && row_tot) {
@@ -443,9 +555,10 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
 constexpr int kWaveCands = 512;
 constexpr int kCands = kWaveCands * kSampWaves;
 // The one-read top_k path: the floor comes from the row's first kHeadElems elements; it runs for
-// k <= kOnePassMaxK (about k * V / kHeadElems candidates, well inside kCands at V = 128256) and
+// k <= kOnePassMaxK (about k * V / kHeadElems candidates, well inside kCands at V = 128256, and
+// for k = 50 at V = 128256 about 400, inside the short-list path's 1024 for every row) and
 // rows of at least kOnePassMinV elements (shorter rows gain little from skipping a read).
-constexpr int kHeadElems = 8192;
+constexpr int kHeadElems = 16384;
 constexpr int kOnePassMaxK = 256;
 constexpr int kOnePassMinV = 65536;
 
@@ -506,18 +619,35 @@ __device__ int compact_segment(const float* p, int V, bool vec, P&& pred, CandSh
     const int seg = (nv + kSampWaves - 1) / kSampWaves;
     const int v0 = w * seg, v1 = min(nv, v0 + seg);
     int vb = v0;  // wave-uniform position: every lane runs the same trips (ballots need them all)
-    for (; vb + 4 * 64 <= v1; vb += 4 * 64) {
-      float4 x[4];
+    // batches of kU x 1 KiB per wave, the next batch's loads issued before the current one is
+    // compacted (two batches in flight: one memory round trip per two batches)
+#ifndef PIE_GATHER_U
+#define PIE_GATHER_U 4
+#endif
+    constexpr int kU = PIE_GATHER_U, kB = kU * 64;
+    if (vb + kB <= v1) {
+      float4 x[kU], y[kU];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) x[k] = *reinterpret_cast<const float4*>(p + 4 * (vb + lane + 64 * k));
+      for (int k = 0; k < kU; ++k) x[k] = *reinterpret_cast<const float4*>(p + 4 * (vb + lane + 64 * k));
+      for (;;) {
+        const bool more = vb + 2 * kB <= v1;
+        if (more) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float xe[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
-        const int i0 = 4 * (vb + lane + 64 * k);
-        uint32_t bits = 0;
+          for (int k = 0; k < kU; ++k) y[k] = *reinterpret_cast<const float4*>(p + 4 * (vb + kB + lane + 64 * k));
+        }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bits |= (uint32_t)pred(i0 + e, xe[e]) << e;
-        emit(bits, i0, xe, 1);
+        for (int k = 0; k < kU; ++k) {
+          const float xe[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+          const int i0 = 4 * (vb + lane + 64 * k);
+          uint32_t bits = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bits |= (uint32_t)pred(i0 + e, xe[e]) << e;
+          emit(bits, i0, xe, 1);
+        }
+        vb += kB;
+        if (!more) break;
+#pragma unroll
+        for (int k = 0; k < kU; ++k) x[k] = y[k];
       }
     }
     for (; vb < v1; vb += 64) {
@@ -614,14 +744,28 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
   // collects every element at or above it (about k * V / kHeadElems of them for exchangeable
   // rows) and counts the row's p > 0 on the way. Overflow falls back to the two passes below.
   if ((mode == 2 || mode == 4) && vec && k > 0 && k <= kOnePassMaxK && V >= kOnePassMinV) {
+    // the floor: the k-th largest of the threads' maxima over their kHeadElems / kSampThreads
+    // head elements (a subset of the head, so at most the head's k-th largest; the head's
+    // largest keys are nearly always their thread's maximum, so it is about as tight), from a
+    // bitonic sort of the 1024 maxima (no LDS atomics, which serialise on keys sharing their
+    // top bits). A floor from each wave's ceil(k/16)-th largest maximum (ballot counts, no
+    // sort) measured slower: looser, it lets some rows' lists outgrow the short-list path.
+    uint32_t hm = 0u;
 #pragma unroll
     for (int j = 0; j < kHeadElems / 4 / kSampThreads; ++j) {
-      const int v = threadIdx.x + j * kSampThreads;
-      *reinterpret_cast<float4*>(cs.val + 4 * v) = *reinterpret_cast<const float4*>(p + 4 * v);
+      const float4 x = *reinterpret_cast<const float4*>(p + 4 * (threadIdx.x + j * kSampThreads));
+      hm = max(max(hm, max(prob_key(x.x), prob_key(x.y))), max(prob_key(x.z), prob_key(x.w)));
     }
+    uint32_t* buf = reinterpret_cast<uint32_t*>(cs.val);
+    hm = sort_desc_keys(hm, buf);
+    if (threadIdx.x == k - 1) sh.u32a = hm;
     __syncthreads();
-    const uint32_t floor0 = radix_threshold(cs.val, kHeadElems, true, 1u, false, (uint32_t)k, 0.0, sh);
-    __syncthreads();  // the head copy is dead from here: its memory holds the candidates
+    const uint32_t floor0 = sh.u32a;
+    __syncthreads();  // the sort buffer is dead from here: its memory holds the candidates
+#if PIE_SAMPLE_STOP == 1
+    if (threadIdx.x == 0) a.out[r] = (int)floor0;
+    return;
+#endif
     if (floor0 > 1u) {
       uint32_t c = 0;
       listed = gather([&](int, float x) {
@@ -632,6 +776,10 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
       npos = (int64_t)block_sum_u64(c, sh);
       __syncthreads();
     }
+#if PIE_SAMPLE_STOP == 2
+    if (threadIdx.x == 0) a.out[r] = (int)npos + sV;
+    return;
+#endif
   }
   // plain sampling, and top_k with k outside (0, V), keep every p > 0: no candidate list
   if (!listed && !(mode == 0 || ((mode == 2 || mode == 4) && !(k > 0 && k < V)))) {
@@ -672,7 +820,8 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
     }
     __syncthreads();
   }
-  sample_row(sp, sidx, sV, svec, a, r, npos, row_tot, sh);
+  sample_row(sp, sidx, sV, svec, a, r, npos, row_tot, sh,
+             sidx ? reinterpret_cast<uint32_t*>(cs.val + kSampThreads) : nullptr);
 }
 
 // safe_scaled_softmax: probs = softmax(logits / T) per row, or the one-hot of the first maximum
