@@ -706,10 +706,13 @@ def main():
     step_bytes = b_add + b_silu
     achieved = b_silu / (silu_ms * 1e-3) / 1e9
 
-    traffic = None
+    # HBM bytes per launch from the committed counter runs (profiles/traffic.json records the
+    # command, the calibration, the date and the commit they were measured at)
+    traffic = traffic_src = None
     tf = ROOT / "profiles" / "traffic.json"
     if tf.exists():
-        traffic = json.loads(tf.read_text()).get("silu_and_mul_cfg2")
+        tj = json.loads(tf.read_text())
+        traffic, traffic_src = tj.get("silu_and_mul_cfg2"), tj.get("silu_and_mul_cfg2_source")
 
     line = {
         "metric": "achieved HBM GB/s (% of MI355X peak) per fused op; µs per decode-step layer chain",
@@ -724,7 +727,8 @@ def main():
                    "bytes_per_step": step_bytes, "parallelism": "single GPU"},
         "roofline": {"kernel": "silu_and_mul_vec", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "avg_launch_us": round(silu_ms * 1e3, 2),
+                     "traffic": traffic, "traffic_source": traffic_src,
+                     "avg_launch_us": round(silu_ms * 1e3, 2),
                      "algorithmic_bytes": b_silu},
         "cpu_baseline": None if args.no_cpu else cpu_baseline(),
     }
