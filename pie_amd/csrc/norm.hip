@@ -215,6 +215,62 @@ __global__ __launch_bounds__(512) void rmsnorm_row_block(NormArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- one wave per row, rows prefetched
+// Plain (no residual) norms of large row lists: each wave walks rows wave, wave + waves, ...
+// holding a row in registers (VPL vectors per lane: lane l owns vectors l + 64 j) and issuing the
+// next row's loads before it reduces and writes the current one, so the arithmetic of one row
+// (Gemma's fp64 sum and roundings) overlaps the next row's loads. Two register buffers alternate
+// (a copy between them would wait for the loads in flight). No LDS, no barrier.
+template <int VPL, bool GEMMA>
+__global__ __launch_bounds__(256) void rmsnorm_rows_pf(NormArgs a) {
+  const RowSet& s = a.set[0];
+  const int lane = threadIdx.x & 63;
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  uint4 wv[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) wv[j] = wprep8<GEMMA>(ld16(s.w + (int64_t)(lane + 64 * j) * 8));
+  auto load = [&](uint4 (&x)[VPL], int64_t row) {
+    int64_t oi, orr, os, oo;
+    row_offsets(s, row, oi, orr, os, oo);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) x[j] = row_ld<true>(s.in + oi, lane + 64 * j);
+  };
+  auto finish = [&](const uint4 (&x)[VPL], int64_t row) {
+    acc_t<GEMMA> ss = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float xf[8];
+      unpack8(x[j], xf);
+      accum8<GEMMA>(ss, xf);
+    }
+    const float rstd = nscale<GEMMA>(wave_sum(ss), (float)a.cols, a.eps);
+    int64_t oi, orr, os, oo;
+    row_offsets(s, row, oi, orr, os, oo);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float xf[8], wf[8];
+      unpack8(x[j], xf);
+      unpack8(wv[j], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xf[e] = napply<GEMMA>(xf[e], rstd, wf[e]);
+      row_st<true>(s.out + oo, lane + 64 * j, pack8(xf));
+    }
+  };
+  uint4 xa[VPL], xb[VPL];
+  if (r < s.rows) load(xa, r);
+  while (r < s.rows) {
+    const int64_t r1 = r + nw;
+    if (r1 < s.rows) load(xb, r1);
+    finish(xa, r);
+    if (r1 >= s.rows) break;
+    const int64_t r2 = r1 + nw;
+    if (r2 < s.rows) load(xa, r2);
+    finish(xb, r1);
+    r = r2;
+  }
+}
+
 // ---------------------------------------------------------------- 16 lanes per row (D = 16*EPL)
 // EPL elements per lane: 4 (D=64, 8-byte accesses), 8 (D=128), 16 (D=256, two vectors).
 template <int EPL>
@@ -387,6 +443,28 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
       case 1: hipLaunchKernelGGL((rmsnorm_row_block<1, ADD, GEMMA>), grd, tb, 0, st, a); break;
       case 2: hipLaunchKernelGGL((rmsnorm_row_block<2, ADD, GEMMA>), grd, tb, 0, st, a); break;
       default: hipLaunchKernelGGL((rmsnorm_row_block<3, ADD, GEMMA>), grd, tb, 0, st, a); break;
+    }
+    return check_launch(name);
+  }
+  // Gemma's plain norm of large row lists: the row-prefetching kernel, 2 work groups per CU
+  // ([8192, 4096]: 25.2 us against 26.6-28.5 for rows_reg; 1 per CU 26.4, 3 per CU 26.1; two
+  // rows ahead 26.9). The standard plain norm measured the same either way (24.0-24.1 us) and
+  // stays on rows_reg. Tuning override: PIE_HIP_NORM_PF=<work groups per CU> (0: off).
+  static const int pf_forced = [] {
+    const char* e = getenv("PIE_HIP_NORM_PF");
+    return e ? atoi(e) : -1;
+  }();
+  const int pf_blocks = pf_forced >= 0 ? pf_forced : (GEMMA ? 2 : 0);
+  if (!ADD && vec && large && pf_blocks > 0 && a.set[1].rows == 0 && a.cols % 512 == 0 &&
+      a.cols <= 8 * 512) {
+    int64_t blocks = (int64_t)num_cus() * pf_blocks;
+    const int64_t need = (rows + 3) / 4;
+    if (blocks > need) blocks = need;
+    const dim3 grd((unsigned)blocks), tb(256);
+    switch (a.cols / 512) {
+#define PIE_PF(n) case n: hipLaunchKernelGGL((rmsnorm_rows_pf<n, GEMMA>), grd, tb, 0, st, a); break;
+      PIE_PF(1) PIE_PF(2) PIE_PF(3) PIE_PF(4) PIE_PF(5) PIE_PF(6) PIE_PF(7) default: PIE_PF(8)
+#undef PIE_PF
     }
     return check_launch(name);
   }

@@ -35,6 +35,18 @@ def test_rmsnorm(dev, T, H):
         assert ulp_diff(N(y), want).max() <= 2
 
 
+@pytest.mark.parametrize("T,H", [(8192, 4096), (16384, 2048), (8200, 3584)])
+def test_rmsnorm_large_row_lists(dev, T, H):
+    """Plain norms of row lists past 64 MB (the non-temporal, row-prefetching paths)."""
+    print(f"rmsnorm large T={T} H={H}", flush=True)
+    x, w = wl.normal((T, H), 5), wl.normal((H,), 6, 1.0, 0.1)
+    y = ops.rmsnorm(x.to(dev), w.to(dev), 1e-5)
+    _sync()
+    want = oracle.rmsnorm(N(x), N(w), 1e-5)
+    assert_bf16_close(N(y), want, what=f"rmsnorm {T}x{H}")
+    assert ulp_diff(N(y), want).max() <= 2
+
+
 def test_rmsnorm_strided_and_misaligned(dev):
     H = 2048
     big = wl.normal((16, H + 8), 3).to(dev)

@@ -33,6 +33,17 @@ def test_gemma_rms_norm(dev, T, H):
     assert_bits_equal(N(out), oracle.gemma_rmsnorm(N(x), N(w), 1e-6), f"gemma {T}x{H}")
 
 
+@pytest.mark.parametrize("T,H", [(8192, 4096), (16384, 2304)])
+def test_gemma_rms_norm_large_row_lists(dev, T, H):
+    """Row lists past 64 MB take the row-prefetching kernel (rows_pf): bit-exact on the full
+    output."""
+    print(f"gemma_rms_norm large T={T} H={H}", flush=True)
+    x, w = wl.normal((T, H), 43), wl.normal((H,), 44, 0.0, 0.5)
+    out = ops.gemma_rms_norm(x.to(dev), w.to(dev), 1e-6)
+    torch.cuda.synchronize()
+    assert_bits_equal(N(out), oracle.gemma_rmsnorm(N(x), N(w), 1e-6), f"gemma {T}x{H}")
+
+
 def test_gemma_rms_norm_every_scale(dev):
     """Rows of one repeated value a, eps = 0: the variance is bf16(a^2) and the kernel's rsqrt
     meets t = bf16(a^2) for every bf16 a in [2^-40, 2^40) (10240 rows), so every correction step
