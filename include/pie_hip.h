@@ -357,7 +357,9 @@ int pie_hip_attention_decode_noalloc(const pie_bf16* q, int64_t q_tok_stride, in
  *   mask), :689 (run); API restated in pie/src/flashinfer_metal/ops.py:163-223.
  *
  * pie_hip_attention_prefill_plan runs on the host over host copies of qo_indptr, kv_indptr and
- * kv_last_page_len and writes the work list (`plan`, int32 words; *num_items work groups per kv
+ * kv_last_page_len and writes the work list (`plan`, int32 words: 16 header words, then 8 per
+ * work item, so plan_capacity >= 16 + 8 * (num_tokens * num_qo_heads / num_kv_heads / 64 +
+ * batch + 1) + 4 * (batch + 1) always suffices; *num_items work groups per kv
  * head; for mode 2 the int64 byte offsets of the mask blocks at word plan[3] and of their packed
  * words at plan[4], *mask_bytes = the mask's size, *mask_words = its packed size in uint32).
  * The caller copies the plan to device memory. For mode 2, pie_hip_attention_pack_mask (device,

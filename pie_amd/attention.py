@@ -227,7 +227,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         mode = 2 if mask is not None else (1 if causal else 0)
         G = num_qo_heads // num_kv_heads
         T = int(qo_h[-1]) if batch else 0
-        cap = 16 + 2 * (T * G // 64 + batch + 1) + 4 * batch + 8
+        cap = 16 + 8 * (T * G // 64 + batch + 1) + 4 * batch + 8  # header, 8-word items, mask offsets
         plan = np.zeros(cap, dtype=np.int32)
         words, items, mbytes, mwords = C.c_int64(0), C.c_int64(0), C.c_int64(0), C.c_int64(0)
         _lib.call("pie_hip_attention_prefill_plan", qo_h.data_ptr(), kv_h.data_ptr(), ll_h.data_ptr(),

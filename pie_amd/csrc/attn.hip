@@ -510,6 +510,10 @@ constexpr int prefill_min_waves() { return D == 256 ? 1 : 2; }
 template <int D>
 constexpr int prefill_rows() { return 16 * prefill_waves<D>() * prefill_row_tiles<D>(); }
 constexpr int kPlanHeader = 16;  // plan words before the items: [0] items, [1] batch, [2] rows per item
+// words per work item: request b, first packed row, and the request's q0 (first query token),
+// qo_len, kv_len and first page-table slot, so the kernels' prologue reads one 32-byte item
+// instead of chasing b through qo_indptr / kv_indptr / kv_last_page_len; two pad words
+constexpr int kPlanItemWords = 8;
 
 // XCD-aware order of the prefill grid: work groups are dispatched round-robin over the 8 XCDs
 // (id mod 8), each with its own L2, so XCD x takes the contiguous run [x * per, (x + 1) * per) of
@@ -522,7 +526,7 @@ __device__ __forceinline__ const int32_t* prefill_unit(const int32_t* plan, int 
   const int u = (int)(blockIdx.x & 7u) * per + (int)(blockIdx.x >> 3);
   if (u >= units) return nullptr;
   kvh = u / n_items;
-  return plan + kPlanHeader + 2 * (u - kvh * n_items);
+  return plan + kPlanHeader + kPlanItemWords * (u - kvh * n_items);
 }
 
 // attn_mask_extent_kernel marks a query token whose mask row is exactly causal (positions
@@ -570,13 +574,11 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) vo
   int kvh;
   const int32_t* item = prefill_unit(plan, n_items, n_kv_heads, kvh);
   if (!item) return;
-  const int b = item[0], row0 = item[1];
+  const int b = item[0], row0 = item[1], q0 = item[2], qo_len = item[3], kv_len = item[4];
+  const int page0 = item[5];
   const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int q0 = qo_indptr[b], qo_len = qo_indptr[b + 1] - q0;
-  const int kv_len = kv_length(kv, b);
   const int rows = qo_len * G;
-  const int page0 = kv.indptr[b];
   int mode = mode_in, mext = 0;  // a custom mask that is causal for all the rows: the causal path
   if (mode_in == 2) {
     bool causal;
@@ -859,13 +861,11 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
   int kvh;
   const int32_t* item = prefill_unit(plan, n_items, n_kv_heads, kvh);
   if (!item) return;
-  const int b = item[0], row0 = item[1];
+  const int b = item[0], row0 = item[1], q0 = item[2], qo_len = item[3], kv_len = item[4];
+  const int page0 = item[5];
   const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
   const int r32 = lane & 31, kg = lane >> 5;
-  const int q0 = qo_indptr[b], qo_len = qo_indptr[b + 1] - q0;
-  const int kv_len = kv_length(kv, b);
   const int rows = qo_len * G;
-  const int page0 = kv.indptr[b];
   int mode = mode_in, mext = 0;  // a custom mask that is causal for all the rows: the causal path
   if (mode_in == 2) {
     bool causal;
@@ -1026,12 +1026,13 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
       }
       const float m_use = m_run == -INFINITY ? 0.f : m_run;
       float sc[16];
-      float psum = 0.f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) sc[i] = fast_exp2(fmaf(sacc[i], scale_log2, -m_use));
+      // the row's partial sum as a tree (a chain of 16 dependent adds sat on the critical path)
+      float ps[4];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) psum += sc[i];
-      l_run += psum;
+      for (int i = 0; i < 4; ++i) ps[i] = (sc[4 * i] + sc[4 * i + 1]) + (sc[4 * i + 2] + sc[4 * i + 3]);
+      l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
       u32x4_t pb[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -1301,7 +1302,7 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
               "prefill_plan: head_dim %lld not in {64, 128, 256}", (long long)head_dim);
   const int64_t G = num_qo_heads / num_kv_heads;
   const int64_t kPrefillRows = head_dim == 256 ? prefill_rows<256>() : prefill_rows<128>();
-  struct Item { int32_t b, row0; int64_t work, req_work; };
+  struct Item { int32_t b, row0, q0, qo, kv, page0; int64_t work, req_work; };
   std::vector<Item> items;
   std::vector<int64_t> moff((size_t)batch + 1, 0), woff((size_t)batch + 1, 0);
   int64_t mtotal = 0, wtotal = 0;
@@ -1319,7 +1320,8 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
     for (int64_t r0 = 0; r0 < qo * G; r0 += kPrefillRows) {
       const int64_t last = std::min(qo * G, r0 + kPrefillRows) - 1;
       const int64_t seen = mode == 1 ? std::max<int64_t>(0, std::min(kv, kv - qo + last / G + 1)) : kv;
-      items.push_back(Item{(int32_t)b, (int32_t)r0, seen, kv * qo});
+      items.push_back(Item{(int32_t)b, (int32_t)r0, qo_indptr[b], (int32_t)qo, (int32_t)kv, kv_indptr[b],
+                           seen, kv * qo});
     }
   }
   // Each request's items stay together (they share its K/V prefix, which the kernels' XCD-aware
@@ -1330,7 +1332,7 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
     if (x.b != y.b) return x.b < y.b;
     return x.work > y.work;
   });
-  int64_t words = kPlanHeader + 2 * (int64_t)items.size();
+  int64_t words = kPlanHeader + kPlanItemWords * (int64_t)items.size();
   words = (words + 1) / 2 * 2;  // int64 mask offsets start 8-byte aligned
   moff[(size_t)batch] = mtotal;
   woff[(size_t)batch] = wtotal;
@@ -1349,7 +1351,10 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
   plan[3] = (int32_t)moff_word;  // mode 2: int64 byte offsets of the mask blocks [batch + 1]
   plan[4] = (int32_t)woff_word;  // mode 2: int64 offsets of the packed mask words [batch + 1]
   int32_t* p = plan + kPlanHeader;
-  for (const Item& it : items) { *p++ = it.b; *p++ = it.row0; }
+  for (const Item& it : items) {
+    const int32_t w8[kPlanItemWords] = {it.b, it.row0, it.q0, it.qo, it.kv, it.page0, 0, 0};
+    for (int i = 0; i < kPlanItemWords; ++i) *p++ = w8[i];
+  }
   if (mode == 2) {
     memcpy(plan + moff_word, moff.data(), sizeof(int64_t) * (size_t)(batch + 1));
     memcpy(plan + woff_word, woff.data(), sizeof(int64_t) * (size_t)(batch + 1));
