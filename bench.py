@@ -546,8 +546,20 @@ def _ops_sampling(dev, run):
     def make_sample():
         pr = probs0.clone()
         return lambda: sampling.top_k_top_p_sampling_from_probs(pr, k, p, seed=1, offset=0)
+    # rows whose large probabilities sit in the vocabulary's last quarter: the one-read top_k
+    # path's floor (from the row's head) is too low, its candidate list overflows, and the row
+    # takes the two-pass path after the wasted read (the fallback's cost, measured)
+    skew = torch.randn(B, V, generator=g) * 3
+    skew[:, : 3 * V // 4] -= 12.0
+    probs_skew = torch.softmax(skew.to(dev), -1)
+
+    def make_sample_skew():
+        pr = probs_skew.clone()
+        return lambda: sampling.top_k_top_p_sampling_from_probs(pr, k, p, seed=1, offset=0)
     return [run(f"safe_scaled_softmax bf16 [{B},{V}]", 2 * B * V * 2, make_softmax),
-            run(f"top_k_top_p sampling fp32 [{B},{V}] (k 50, p 0.9)", B * V * 4, make_sample)]
+            run(f"top_k_top_p sampling fp32 [{B},{V}] (k 50, p 0.9)", B * V * 4, make_sample),
+            run(f"top_k_top_p sampling fp32 [{B},{V}], mass in the last quarter (two-pass fallback)",
+                B * V * 4, make_sample_skew)]
 
 
 def _back_to_back(fn, n, reps=5):
