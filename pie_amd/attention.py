@@ -227,7 +227,10 @@ class BatchPrefillWithPagedKVCacheWrapper:
         mode = 2 if mask is not None else (1 if causal else 0)
         G = num_qo_heads // num_kv_heads
         T = int(qo_h[-1]) if batch else 0
-        cap = 16 + 8 * (T * G // 64 + batch + 1) + 4 * batch + 8  # header, 8-word items, mask offsets
+        n_items = T * G // 64 + batch + 1
+        # header, 8-word items, the persistent schedule (slot offsets, one word per (kv head,
+        # item) unit), mask offsets
+        cap = 16 + 8 * n_items + (4096 + n_items * num_kv_heads) + 4 * batch + 8
         plan = np.zeros(cap, dtype=np.int32)
         words, items, mbytes, mwords = C.c_int64(0), C.c_int64(0), C.c_int64(0), C.c_int64(0)
         _lib.call("pie_hip_attention_prefill_plan", qo_h.data_ptr(), kv_h.data_ptr(), ll_h.data_ptr(),

@@ -510,6 +510,9 @@ constexpr int prefill_min_waves() { return D == 256 ? 1 : 2; }
 template <int D>
 constexpr int prefill_rows() { return 16 * prefill_waves<D>() * prefill_row_tiles<D>(); }
 constexpr int kPlanHeader = 16;  // plan words before the items: [0] items, [1] batch, [2] rows per item
+// Plan words the head-dim-128 kernel uses as counters: the next unit of each XCD's queue, and
+// the work groups that have finished (the last one sets all nine back to zero).
+constexpr int kPlanQueueWord = 8, kPlanDoneWord = 7;
 // words per work item: request b, first packed row, and the request's q0 (first query token),
 // qo_len, kv_len and first page-table slot, so the kernels' prologue reads one 32-byte item
 // instead of chasing b through qo_indptr / kv_indptr / kv_last_page_len; two pad words
@@ -573,7 +576,7 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) vo
 
   int kvh;
   const int32_t* item = prefill_unit(plan, n_items, n_kv_heads, kvh);
-  if (!item) return;
+  if (!item || plan[2] != kPrefillRows) return;  // padding work group, or a plan made for another head_dim
   const int b = item[0], row0 = item[1], q0 = item[2], qo_len = item[3], kv_len = item[4];
   const int page0 = item[5];
   const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
@@ -858,9 +861,33 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
   __shared__ int window_bad;
   __shared__ uint32_t mwt[2][NT];
 
-  int kvh;
-  const int32_t* item = prefill_unit(plan, n_items, n_kv_heads, kvh);
-  if (!item) return;
+  // Persistent: each work group takes (kv head, item) units from its XCD's queue until every
+  // queue is empty. XCD x's queue is the contiguous run [x * per, (x + 1) * per) of the units, in
+  // plan order (each request's items together), so the work groups of one XCD share the K/V
+  // prefix they read through its L2; a work group whose queue is empty takes from the others.
+  if (plan[2] != kRows) return;  // a plan made for another head_dim
+  int32_t* counters = const_cast<int32_t*>(plan);
+  __shared__ int s_unit;
+  const int units = n_items * n_kv_heads, per = (units + 7) / 8;
+  const int xcd = (int)(__builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11)) & 7);  // HW_REG_XCC_ID
+  int queue = 0;
+  for (;;) {
+  __syncthreads();  // the previous unit's LDS use (and s_unit) is done
+  if (threadIdx.x == 0) {
+    int u = -1;
+    for (; queue < 8 && u < 0; ) {
+      const int x = (xcd + queue) & 7;
+      const int n = min(per, units - x * per);
+      const int i = atomicAdd(&counters[kPlanQueueWord + x], 1);
+      if (i < n) u = x * per + i; else ++queue;
+    }
+    s_unit = u;
+  }
+  __syncthreads();
+  const int u = s_unit;
+  if (u < 0) break;
+  const int kvh = u / n_items;
+  const int32_t* item = plan + kPlanHeader + kPlanItemWords * (u - kvh * n_items);
   const int b = item[0], row0 = item[1], q0 = item[2], qo_len = item[3], kv_len = item[4];
   const int page0 = item[5];
   const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
@@ -1096,6 +1123,12 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
                          pack_bf2(o[bb][4 * c + 2] * inv, o[bb][4 * c + 3] * inv)};
         *reinterpret_cast<uint2*>(op + 32 * bb + 8 * c + 4 * kg) = v;
       }
+  }
+  }
+  // the last work group out resets the counters for the next launch with this plan
+  if (threadIdx.x == 0 && atomicAdd(&counters[kPlanDoneWord], 1) == (int)gridDim.x - 1) {
+    for (int x = 0; x < 8; ++x) atomicExch(&counters[kPlanQueueWord + x], 0);
+    atomicExch(&counters[kPlanDoneWord], 0);
   }
 }
 
@@ -1350,6 +1383,7 @@ extern "C" int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const in
   plan[2] = (int32_t)kPrefillRows;
   plan[3] = (int32_t)moff_word;  // mode 2: int64 byte offsets of the mask blocks [batch + 1]
   plan[4] = (int32_t)woff_word;  // mode 2: int64 offsets of the packed mask words [batch + 1]
+  // [7] and [8, 16): the persistent kernel's work counters (zero between launches)
   int32_t* p = plan + kPlanHeader;
   for (const Item& it : items) {
     const int32_t w8[kPlanItemWords] = {it.b, it.row0, it.q0, it.qo, it.kv, it.page0, 0, 0};
@@ -1372,7 +1406,8 @@ static void launch_prefill(hipStream_t st, dim3 grid, const uint16_t* q, int64_t
   // hidden (-inf) score into NaN; 1e-30 gives the same result (every exponent rounds to 2^0).
   const dim3 xgrid(8 * ((grid.x * grid.y + 7) / 8));  // (kv head, item) units, padded to 8 XCDs
   if constexpr (D == 128 && PIE_PREFILL_MFMA32)
-    hipLaunchKernelGGL(attn_prefill32_kernel<128>, xgrid, dim3(256), 0, st, q, q_ts, q_hs, kv, qo_indptr, G,
+    hipLaunchKernelGGL(attn_prefill32_kernel<128>, dim3(8 * ((2 * num_cus() + 7) / 8)), dim3(256), 0, st, q, q_ts,
+                       q_hs, kv, qo_indptr, G,
                        sl2 == 0.f ? 1e-30f : sl2, plan, (int)grid.x, (int)grid.y, mode, window_left, packed,
                        woff, extent, out, o_ts, o_hs, sinks);
   else
@@ -1465,8 +1500,6 @@ extern "C" int pie_hip_attention_prefill(
                                                        mask_offsets_word % 2 == 0)),
               "attention_prefill: mode %d needs the packed mask and its plan offsets", mode);
   PIE_REQUIRE(num_items >= 0 && num_items * num_kv_heads < (1ll << 31), "attention_prefill: bad item count");
-  PIE_REQUIRE(plan[2] == (head_dim == 256 ? prefill_rows<256>() : prefill_rows<128>()),
-              "attention_prefill: the plan was made for another head_dim");
   PIE_REQUIRE(aligned16(q) && aligned16(out) && q_tok_stride % 8 == 0 && q_head_stride % 8 == 0 &&
                   o_tok_stride % 8 == 0 && o_head_stride % 8 == 0,
               "attention_prefill: q/out pointers and strides must be 16-byte aligned");

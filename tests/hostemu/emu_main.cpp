@@ -564,7 +564,7 @@ static void case_attn_prefill(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int
         for (int64_t t = 0; t < kvl[b]; ++t)
           if (t > kvl[b] - qn + i) mask[moff[b] + i * kvl[b] + t] = 0;
     }
-  const int64_t cap = 16 + 8 * (T * Hq / 32 + 2 * B + 2) + 4 * B + 8;
+  const int64_t cap = 16 + 8 * (T * Hq / 32 + 2 * B + 2) + 4 * B + 8 + (T * Hq / 32 + 2 * B + 2) * Hkv + 4096;
   Buf<int32_t> plan(cap);
   int64_t words = 0, items = 0, mb = 0, mw = 0;
   rc_ok(pie_hip_attention_prefill_plan(qi.p, ip.p, ll.p, B, P, Hq, Hkv, D, mode, plan.p, cap, &words, &items, &mb,

@@ -258,6 +258,7 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 #define __builtin_amdgcn_global_load_lds emu::global_load_lds
 #define __builtin_amdgcn_s_waitcnt(x) ((void)(x))
 #define __builtin_amdgcn_sched_barrier(x) ((void)(x))
+#define __builtin_amdgcn_s_getreg(x) ((void)(x), 0u)  // hardware registers (XCC_ID): XCD 0
 #define __builtin_amdgcn_sched_group_barrier(m, n, id) ((void)(m), (void)(n), (void)(id))
 // Hardware sine / cosine of x revolutions, and the fractional part.
 inline float __builtin_amdgcn_sinf(float x) { return (float)sin(6.283185307179586 * (double)x); }
@@ -287,6 +288,8 @@ inline int64_t min(int64_t a, int64_t b) { return a < b ? a : b; }
 // Atomics on block-shared memory (emulated threads of one block run concurrently).
 inline unsigned atomicAdd(unsigned* p, unsigned v) { return __atomic_fetch_add(p, v, __ATOMIC_RELAXED); }
 inline int atomicMax(int* p, int v) { return __atomic_fetch_max(p, v, __ATOMIC_RELAXED); }
+inline int atomicAdd(int* p, int v) { return __atomic_fetch_add(p, v, __ATOMIC_RELAXED); }
+inline int atomicExch(int* p, int v) { return __atomic_exchange_n(p, v, __ATOMIC_RELAXED); }
 inline int atomicOr(int* p, int v) { return __atomic_fetch_or(p, v, __ATOMIC_RELAXED); }
 inline unsigned atomicMax(unsigned* p, unsigned v) { return __atomic_fetch_max(p, v, __ATOMIC_RELAXED); }
 inline unsigned atomicMin(unsigned* p, unsigned v) { return __atomic_fetch_min(p, v, __ATOMIC_RELAXED); }

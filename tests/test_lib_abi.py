@@ -152,7 +152,7 @@ def test_prefill_plan_position_limits_without_a_gpu():
         qo = np.array([0, 1], dtype=np.int32)
         kv = np.array([0, pages], dtype=np.int32)
         last = np.array([kv_len - 16 * (pages - 1)], dtype=np.int32)
-        buf = np.zeros(64, dtype=np.int32)
+        buf = np.zeros(4096, dtype=np.int32)
         out = [C.c_int64(0) for _ in range(4)]
         return _rc("pie_hip_attention_prefill_plan", qo.ctypes.data, kv.ctypes.data, last.ctypes.data,
                    1, 16, 8, 2, 128, mode, buf.ctypes.data, buf.size, *[C.byref(o) for o in out])
