@@ -585,7 +585,10 @@ def measure_chain(dev, flush=None, cold_iters=20):
     layers of a decode pass in one graph (llama3.py:315-414); the instances' activations
     (~38 MB each) together exceed the 256 MB last-level cache, so each chain reads HBM.
     steady: back-to-back replays of a one-chain graph (bound by the host's graph-launch rate when
-    the chain is short); single: one replay between two events (includes the launch latency)."""
+    the chain is short); single: one replay between two events (includes the launch latency);
+    eager_steady: back-to-back run() calls (ops recorded and validated in Python each time);
+    saved_steady (grouped): back-to-back relaunches of recorded groups, one library call each,
+    over CHAINS_PER_GRAPH chains in turn like in_graph."""
     from pie_amd import workloads as wl
     from pie_amd.chain import DecodeChain
     c = wl.cfg5()
@@ -595,6 +598,18 @@ def measure_chain(dev, flush=None, cold_iters=20):
         fused = mode != "unfused"
         grouped = mode == "grouped"
         ch = DecodeChain(c, dev, fused=fused, grouped=grouped)
+        if grouped:
+            # recorded groups relaunched with one library call per chain, no graph: CHAINS_PER_GRAPH
+            # chains over their own activations in turn (as in_graph, so each reads HBM)
+            svs = [DecodeChain(c, dev, saved=True, share=ch) for _ in range(CHAINS_PER_GRAPH)]
+            for sv in svs:
+                sv.run()
+
+            def _saved_round():
+                for sv in svs:
+                    sv.run()
+            saved_steady = _back_to_back(_saved_round, 10) / len(svs)
+            del svs
         g = ch.capture()
         for _ in range(20):
             g.replay()
@@ -614,6 +629,8 @@ def measure_chain(dev, flush=None, cold_iters=20):
              "us_steady": round(steady, 2),
              "us_single_replay": round(single, 2),
              "us_eager_steady": round(_back_to_back(ch.run, 50), 2), "launches": launches}
+        if grouped:
+            e["us_saved_steady"] = round(saved_steady, 2)
         if flush is not None and grouped:
             e["us_single_replay_cold"] = round(statistics.median(_events(g.replay, cold_iters, flush)) * 1e3, 2)
         res.append(e)

@@ -262,6 +262,20 @@ int pie_hip_group_begin(void);
 int pie_hip_group_end(void* stream);
 
 /*
+ * A recorded group kept for relaunching: pie_hip_group_save closes the open group like
+ * pie_hip_group_end (same checks, same kernels) but launches nothing and returns a handle;
+ * pie_hip_group_launch(group, stream) launches what pie_hip_group_end would have, on `stream`,
+ * reading and writing the recorded buffers at launch time, as often as the caller likes (a decode
+ * loop whose ops keep their buffers from step to step: one call per step, no per-op argument
+ * validation). The caller keeps every recorded buffer alive and in place while the handle is
+ * used; pie_hip_group_free releases the handle (host memory only).
+ * No reference counterpart: it replaces the per-step re-issue of the grouped ops' launches.
+ */
+int pie_hip_group_save(void* stream, void** group);
+int pie_hip_group_launch(const void* group, void* stream);
+void pie_hip_group_free(void* group);
+
+/*
  * seq_lens[b] = (kv_indptr[b+1]-kv_indptr[b]-1)*page_size + last_page_len[b], or 0 when the
  * request holds no page. Replaces flashinfer.get_seq_lens (llama3.py:745-749;
  * spec pie/src/flashinfer_metal/ops.py:392-407).

@@ -60,6 +60,8 @@ SIGNATURES: dict[str, list] = {
     "pie_hip_scaled_softmax": [vp, i32, i64, i64, i64, vp, f32, vp, i64, vp],
     "pie_hip_group_begin": [],
     "pie_hip_group_end": [vp],
+    "pie_hip_group_save": [vp, vp],
+    "pie_hip_group_launch": [vp, vp],
     "pie_hip_get_seq_lens": [vp, vp, i64, i64, vp, vp],
     "pie_hip_get_batch_indices_positions": [vp, vp, i64, i64, vp, vp, vp],
 }
@@ -90,6 +92,8 @@ def load() -> C.CDLL:
     lib = C.CDLL(str(LIB_PATH))
     lib.pie_hip_last_error.restype = C.c_char_p
     lib.pie_hip_last_error.argtypes = []
+    lib.pie_hip_group_free.restype = None
+    lib.pie_hip_group_free.argtypes = [C.c_void_p]
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = C.c_int

@@ -11,6 +11,8 @@ out (they are not part of this path):
 grouped=True (implies the fused prologue) records the ops in ops.op_group(), so the whole chain
 is ONE kernel launch: the embedding gather runs fused into the residual add + RMSNorm, and the
 q/k prologue and SiLU-and-mul, which do not depend on them here, run in their own block ranges.
+saved=True (implies grouped) records the group once (ops.saved_group()) and relaunches it on
+every later ``run()`` with one library call, as a decode loop without graphs would.
 All buffers are preallocated, so ``run()`` launches kernels only and can be captured into a
 HIP graph (``capture()``), as the reference captures its decode layers (llama3.py:315-414).
 """
@@ -24,13 +26,15 @@ from . import workloads as wl
 
 class DecodeChain:
     def __init__(self, cfg: dict, device, fused: bool = True, grouped: bool = False,
-                 share: "DecodeChain | None" = None):
+                 share: "DecodeChain | None" = None, saved: bool = False):
         """share: take the embedding table and the paged cache of another chain (several chains
         over their own activations, as the layers of one decode step share a cache pool)."""
         d = device
         self.cfg = cfg
-        self.fused = fused or grouped
-        self.grouped = grouped
+        self.fused = fused or grouped or saved
+        self.grouped = grouped or saved
+        self.saved = saved
+        self._saved = None
         self.Hq, self.Hkv, self.D = cfg["Hq"], cfg["Hkv"], cfg["D"]
         self.eps, self.theta = cfg["eps"], cfg["theta"]
         pb = cfg["batch"]
@@ -60,7 +64,13 @@ class DecodeChain:
         self.cache.view(torch.int16).fill_(wl.SENTINEL_BITS)
 
     def run(self):
-        if self.grouped:
+        if self.saved:
+            if self._saved is None:
+                with ops.saved_group(self.hidden.device) as g:
+                    self._ops()
+                self._saved = g[0]
+            self._saved.launch()
+        elif self.grouped:
             with ops.op_group(self.hidden.device):
                 self._ops()
         else:

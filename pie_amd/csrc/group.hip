@@ -18,6 +18,8 @@
 // the norm, the same order of partial sums (64-vector wave partials added in order).
 #include <string.h>
 
+#include <new>
+
 #include "act_dev.h"
 #include "norm_dev.h"
 #include "rope_dev.h"
@@ -355,15 +357,32 @@ extern "C" int pie_hip_group_begin(void) {
   return PIE_HIP_OK;
 }
 
-extern "C" int pie_hip_group_end(void* stream) {
-  PIE_REQUIRE(g_group.open, "group_end: no group is open on this thread");
-  // Close first: the standalone launches below must not be recorded again.
+// What a group launches: the grouped kernel (blocks > 0) and the ops that run standalone, in
+// record order after it.
+struct GroupLaunch {
+  GroupArgs g{};
+  int nj = 1;
+  int64_t blocks = 0;
+  int n_alone = 0;
+  GroupOp alone[kMaxGroupOps];
+};
+
+static void keep_alone(GroupLaunch& L, const GroupOp& o) {
+  GroupOp& c = L.alone[L.n_alone++];
+  c = o;
+  c.q.inv_freq = c.freq;  // the copy's own inverse frequencies
+}
+
+// Closes the open group and works out its launches (nothing is launched).
+static int group_build(void* stream, GroupLaunch& L, const char* what) {
+  PIE_REQUIRE(g_group.open, "%s: no group is open on this thread", what);
+  // Close first: the standalone launches must not be recorded again.
   g_group.open = false;
   const int n = g_group.n;
   g_group.n = 0;
   GroupOp* ops = g_group.ops;
   for (int i = 0; i < n; ++i)
-    PIE_REQUIRE(ops[i].stream == stream, "group_end: op %d was recorded on another stream", i);
+    PIE_REQUIRE(ops[i].stream == stream, "%s: op %d was recorded on another stream", what, i);
   int rc = check_hazards(ops, n);
   if (rc) return rc;
 
@@ -391,13 +410,12 @@ extern "C" int pie_hip_group_end(void* stream) {
   const int pieces = (iq >= 0) + (in >= 0) + (ia >= 0);
   if ((pn >= 0 && !pair_fused) || (pieces < 2 && !pair_fused)) {
     // nothing to gain, or the producer/consumer pair cannot run fused: record order
-    for (int i = 0; i < n; ++i)
-      if ((rc = launch_alone(ops[i]))) return rc;
+    for (int i = 0; i < n; ++i) keep_alone(L, ops[i]);
     return PIE_HIP_OK;
   }
 
-  GroupArgs g{};
-  int nj = 1;
+  GroupArgs& g = L.g;
+  int& nj = L.nj;
   if (iq >= 0) {
     g.qk = qa;
     g.qk.r.wpt = 4;  // one token per 256-thread block
@@ -438,17 +456,62 @@ extern "C" int pie_hip_group_end(void* stream) {
     g.act_blocks = (int32_t)((nvec + 256 * kActU - 1) / (256 * kActU));
     g.act_gelu = r.gelu;
   }
-  const int64_t blocks = (int64_t)g.qk_blocks + g.nm_blocks + g.act_blocks;
-  PIE_REQUIRE(blocks < (1ll << 31), "group_end: %lld blocks", (long long)blocks);
-  if (blocks > 0) {
-    const hipStream_t st = static_cast<hipStream_t>(stream);
-    if (nj == 2) hipLaunchKernelGGL((decode_group_kernel<2, kActU>), dim3((unsigned)blocks), dim3(256), 0, st, g);
-    else hipLaunchKernelGGL((decode_group_kernel<1, kActU>), dim3((unsigned)blocks), dim3(256), 0, st, g);
-    if ((rc = check_launch("group_end"))) return rc;
-  }
+  L.blocks = (int64_t)g.qk_blocks + g.nm_blocks + g.act_blocks;
+  PIE_REQUIRE(L.blocks < (1ll << 31), "%s: %lld blocks", what, (long long)L.blocks);
   for (int i = 0; i < n; ++i) {
     if (i == iq || i == in || i == ia || (pair_fused && i == pe)) continue;
-    if ((rc = launch_alone(ops[i]))) return rc;
+    keep_alone(L, ops[i]);
   }
   return PIE_HIP_OK;
 }
+
+static int group_launch(const GroupLaunch& L, void* stream, const char* what) {
+  int rc;
+  if (L.blocks > 0) {
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (L.nj == 2)
+      hipLaunchKernelGGL((decode_group_kernel<2, kActU>), dim3((unsigned)L.blocks), dim3(256), 0, st, L.g);
+    else
+      hipLaunchKernelGGL((decode_group_kernel<1, kActU>), dim3((unsigned)L.blocks), dim3(256), 0, st, L.g);
+    if ((rc = check_launch(what))) return rc;
+  }
+  for (int i = 0; i < L.n_alone; ++i) {
+    GroupOp o = L.alone[i];
+    o.q.inv_freq = o.freq;
+    o.stream = stream;
+    if ((rc = launch_alone(o))) return rc;
+  }
+  return PIE_HIP_OK;
+}
+
+
+extern "C" int pie_hip_group_end(void* stream) {
+  GroupLaunch L;
+  int rc = group_build(stream, L, "group_end");
+  return rc ? rc : group_launch(L, stream, "group_end");
+}
+
+extern "C" int pie_hip_group_save(void* stream, void** group) {
+  PIE_REQUIRE(group, "group_save: null handle pointer");
+  *group = nullptr;
+  GroupLaunch* L = new (std::nothrow) GroupLaunch();
+  if (!L) {
+    g_group.open = false;
+    g_group.n = 0;
+    return set_error(PIE_HIP_EINVAL, "group_save: out of host memory");
+  }
+  const int rc = group_build(stream, *L, "group_save");
+  if (rc) {
+    delete L;
+    return rc;
+  }
+  *group = L;
+  return PIE_HIP_OK;
+}
+
+extern "C" int pie_hip_group_launch(const void* group, void* stream) {
+  PIE_REQUIRE(group, "group_launch: null group");
+  return group_launch(*static_cast<const GroupLaunch*>(group), stream, "group_launch");
+}
+
+extern "C" void pie_hip_group_free(void* group) { delete static_cast<GroupLaunch*>(group); }

@@ -97,6 +97,58 @@ def op_group(device: Optional[torch.device] = None):
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
+class SavedGroup:
+    """A recorded op group kept for relaunching (pie_hip_group_save / pie_hip_group_launch):
+    ``launch()`` enqueues what the group's block would have launched, on the current stream, in
+    one library call, reading and writing the recorded tensors as they are at launch time. It
+    holds those tensors (so they stay allocated and in place); write new inputs into them in place
+    between launches."""
+
+    def __init__(self, handle: int, keep: list, device_index: int):
+        self._h, self._keep, self._dev = handle, keep, device_index
+        self._free = _lib.load().pie_hip_group_free
+        self._launch = _lib.load().pie_hip_group_launch
+
+    def launch(self) -> None:
+        st = _raw_stream(self._dev) if _raw_stream is not None else \
+            torch.cuda.current_stream(self._dev).cuda_stream
+        if self._launch(self._h, st) != 0:
+            _lib.call("pie_hip_group_launch", self._h, st)  # raises with the library's message
+
+    def __del__(self):
+        h, self._h = getattr(self, "_h", None), None
+        if h:
+            self._free(h)
+
+
+@contextlib.contextmanager
+def saved_group(device: Optional[torch.device] = None):
+    """Like op_group(), but the block's ops are not launched: the yielded list receives ONE
+    SavedGroup whose ``launch()`` runs them (same kernels, same results) as often as needed."""
+    global _group_keep
+    if _group_keep is not None:
+        raise RuntimeError("saved_group: groups do not nest")
+    _lib.call("pie_hip_group_begin")
+    _group_keep = []
+    out: list = []
+    ok = False
+    try:
+        yield out
+        ok = True
+    finally:
+        keep, _group_keep = _group_keep, None
+        idx = torch.cuda.current_device() if device is None else torch.device(device).index
+        st = _raw_stream(idx) if _raw_stream is not None else torch.cuda.current_stream(idx).cuda_stream
+        h = C.c_void_p(0)
+        if ok:
+            _lib.call("pie_hip_group_save", st, C.byref(h))
+            out.append(SavedGroup(h.value, keep, idx))
+        else:  # close the group; the block's own exception is the one to report
+            _lib.load().pie_hip_group_save(st, C.byref(h))
+            if h.value:
+                _lib.load().pie_hip_group_free(h.value)
+
+
 def _stream(t: torch.Tensor) -> int:
     """The current torch stream of t's device as a raw handle (the raw accessor skips building a
     Stream object: ~0.2 µs against ~2 µs per call)."""

@@ -507,6 +507,22 @@ static void case_group(int64_t B, int64_t H, int64_t I, int64_t V, bool gelu) {
   check_equal("group k", b.ko.p, a.ko.p, a.ko.n);
   check_equal("group cache", b.cache.p, a.cache.p, a.cache.n);
   check_equal("group act", b.act.p, a.act.p, a.act.n);
+  // the same group saved and launched twice (the second over cleared outputs)
+  Out c(T, H, Hq, Hkv, D, pg.pool, page_elems, I);
+  void* saved = nullptr;
+  rc_ok(pie_hip_group_begin(), "group_begin");
+  run(c);
+  rc_ok(pie_hip_group_save(nullptr, &saved), "group_save");
+  for (int rep = 0; rep < 2; ++rep) {
+    for (size_t i = 0; i < c.act.n; ++i) c.act[i] = 0;
+    for (size_t i = 0; i < c.y.n; ++i) c.y[i] = 0;
+    for (size_t i = 0; i < c.cache.n; ++i) c.cache[i] = 0x7fa5;
+    rc_ok(pie_hip_group_launch(saved, nullptr), "group_launch");
+    check_equal("saved group normed", c.y.p, a.y.p, a.y.n);
+    check_equal("saved group cache", c.cache.p, a.cache.p, a.cache.n);
+    check_equal("saved group act", c.act.p, a.act.p, a.act.n);
+  }
+  pie_hip_group_free(saved);
   // a hazard (the activation writes the norm's residual input) is rejected without launching
   rc_ok(pie_hip_group_begin(), "group_begin");
   rc_ok(pie_hip_fused_add_rmsnorm(b.hid.p, H, res.p, H, b.s.p, H, b.y.p, H, wn.p, T, H, 1e-6f, nullptr), "n");

@@ -94,3 +94,26 @@ def test_chain_graph_replays(dev, cfg, grouped):
         for key in eager:
             assert_bits_equal(got[key], eager[key], f"replay {i} {key}")
         del junk
+
+
+def test_chain_saved_group_relaunches(dev, cfg):
+    """The chain recorded once (ops.saved_group) and relaunched: every relaunch equals the
+    one-off grouped launch bit for bit, the inputs reset in place between relaunches (the saved
+    launch reads the recorded buffers when it runs)."""
+    print("chain saved group relaunches", flush=True)
+    a = DecodeChain(cfg, dev, grouped=True)
+    a.reset()
+    a.run()
+    want = _snap(a)
+    s = DecodeChain(cfg, dev, saved=True)
+    for i in range(3):
+        s.reset()  # restores the residual stream and the cache in place
+        if i == 1:
+            s.residual.add_(1.0)  # a changed input: the relaunch must see it
+        s.run()
+        got = _snap(s)
+        if i == 1:
+            assert not (got["residual"] == want["residual"]).all(), "relaunch ignored new inputs"
+            continue
+        for key in want:
+            assert_bits_equal(got[key], want[key], f"relaunch {i} {key}")
