@@ -299,7 +299,24 @@ def _ops_ceiling(dev, run):
         a = torch.empty(n_sm, dtype=torch.uint8, device=dev)
         b = torch.empty_like(a)
         return lambda: lib.pie_probe_copy(a.data_ptr(), b.data_ptr(), n_sm, 1, st())
-    res = [run("ceiling copy 8 MiB -> 8 MiB (cfg1 bytes), cached", 2 * n1, lambda: make_copy(0)),
+    lib.pie_probe_read.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    sink = torch.empty(1 << 16, dtype=torch.int32, device=dev)
+
+    def make_read(nbytes, threads, vpt):
+        a = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        return lambda: lib.pie_probe_read(a.data_ptr(), nbytes, threads, vpt, sink.data_ptr(), st())
+    # read-only ceilings (all of a work group's loads issued before any is used): the softmax's
+    # read phase (one 1024-thread work group per 256 KB row, 16 vectors per thread) and the best
+    # read-only shape measured (256-thread groups, 16 vectors each), over the softmax's bytes and
+    # over the sampler's fp32 rows
+    n_rd = 256 * 1024 * 256  # 256 rows of 256 KiB (softmax rows are 250.5 KiB)
+    n_rd2 = 2 * n_rd
+    res = [run("ceiling read 64 MiB, 1 work group x 1024 threads x 16 vectors per 256 KiB (softmax read phase)",
+               n_rd, lambda: make_read(n_rd, 1024, 16)),
+           run("ceiling read 64 MiB, 256 threads x 16 vectors per work group", n_rd, lambda: make_read(n_rd, 256, 16)),
+           run("ceiling read 128 MiB (sampler rows' bytes), 256 threads x 16 vectors per work group", n_rd2,
+               lambda: make_read(n_rd2, 256, 16))]
+    res += [run("ceiling copy 8 MiB -> 8 MiB (cfg1 bytes), cached", 2 * n1, lambda: make_copy(0)),
            run("ceiling copy 8 MiB -> 8 MiB (cfg1 bytes), non-temporal", 2 * n1, lambda: make_copy(1)),
            run("ceiling copy 64 MB -> 64 MB (softmax bytes, [256,128256] bf16), non-temporal",
                2 * n_sm, make_copy_sm)]

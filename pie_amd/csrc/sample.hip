@@ -626,28 +626,38 @@ __device__ int compact_segment(const float* p, int V, bool vec, P&& pred, CandSh
 #endif
     constexpr int kU = PIE_GATHER_U, kB = kU * 64;
     if (vb + kB <= v1) {
+      // two register buffers in turn (no copy between them, which would wait for the younger
+      // batch's loads): while one batch is compacted the next one's loads are in flight
       float4 x[kU], y[kU];
+      auto load = [&](float4 (&d)[kU], int at) {
 #pragma unroll
-      for (int k = 0; k < kU; ++k) x[k] = *reinterpret_cast<const float4*>(p + 4 * (vb + lane + 64 * k));
-      for (;;) {
-        const bool more = vb + 2 * kB <= v1;
-        if (more) {
-#pragma unroll
-          for (int k = 0; k < kU; ++k) y[k] = *reinterpret_cast<const float4*>(p + 4 * (vb + kB + lane + 64 * k));
-        }
+        for (int k = 0; k < kU; ++k) d[k] = *reinterpret_cast<const float4*>(p + 4 * (at + lane + 64 * k));
+      };
+      auto scan = [&](const float4 (&d)[kU], int at) {
 #pragma unroll
         for (int k = 0; k < kU; ++k) {
-          const float xe[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
-          const int i0 = 4 * (vb + lane + 64 * k);
+          const float xe[4] = {d[k].x, d[k].y, d[k].z, d[k].w};
+          const int i0 = 4 * (at + lane + 64 * k);
           uint32_t bits = 0;
 #pragma unroll
           for (int e = 0; e < 4; ++e) bits |= (uint32_t)pred(i0 + e, xe[e]) << e;
           emit(bits, i0, xe, 1);
         }
+      };
+      load(x, vb);
+      if (vb + 2 * kB <= v1) load(y, vb + kB);
+      for (;;) {
+        // x holds batch vb, y (if vb + 2 kB <= v1) batch vb + kB
+        const bool has_y = vb + 2 * kB <= v1;
+        scan(x, vb);
+        if (has_y && vb + 3 * kB <= v1) load(x, vb + 2 * kB);
         vb += kB;
-        if (!more) break;
-#pragma unroll
-        for (int k = 0; k < kU; ++k) x[k] = y[k];
+        if (!has_y) break;
+        const bool has_x = vb + 2 * kB <= v1;
+        scan(y, vb);
+        if (has_x && vb + 3 * kB <= v1) load(y, vb + 2 * kB);
+        vb += kB;
+        if (!has_x) break;
       }
     }
     for (; vb < v1; vb += 64) {

@@ -7,6 +7,10 @@
 //                       src + src_off[t] bytes goes to dst + dst_off[t] bytes (offsets computed
 //                       beforehand, so no page-table reads), one 16-byte vector per thread,
 //                       non-temporal loads and stores.
+//   pie_probe_read:     reads n 16-byte vectors, each work group a contiguous chunk of
+//                       threads x vpt vectors with all of a thread's vpt loads issued before any
+//                       is used (the resident softmax's pattern at 1024 threads and vpt 16),
+//                       one xor per work group written out.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -34,6 +38,37 @@ __global__ __launch_bounds__(256) void probe_scatter_kernel(const char* __restri
   const uint32_t row = i / vpr, c = i - row * vpr;
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + src_off[row]) + c);
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst + dst_off[row]) + c);
+}
+
+template <int VPT>
+__global__ __launch_bounds__(1024) void probe_read_kernel(const u32x4* __restrict__ src, uint32_t* __restrict__ out) {
+  const u32x4* p = src + (size_t)blockIdx.x * blockDim.x * VPT;
+  u32x4 v[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) v[j] = __builtin_nontemporal_load(p + threadIdx.x + j * blockDim.x);
+  uint32_t x = 0;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) x ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  __shared__ uint32_t acc;
+  if (threadIdx.x == 0) acc = 0;
+  __syncthreads();
+  atomicXor(&acc, x);
+  __syncthreads();
+  if (threadIdx.x == 0) out[blockIdx.x] = acc;
+}
+
+extern "C" int pie_probe_read(const void* src, int64_t bytes, int threads, int vpt, uint32_t* out, void* stream) {
+  const int64_t chunk = (int64_t)threads * vpt * 16;
+  if (threads < 64 || threads > 1024 || threads % 64 || bytes % chunk || (reinterpret_cast<uintptr_t>(src) & 15))
+    return 1;
+  const dim3 g((unsigned)(bytes / chunk)), b((unsigned)threads);
+  switch (vpt) {
+    case 4: hipLaunchKernelGGL(probe_read_kernel<4>, g, b, 0, (hipStream_t)stream, (const u32x4*)src, out); break;
+    case 8: hipLaunchKernelGGL(probe_read_kernel<8>, g, b, 0, (hipStream_t)stream, (const u32x4*)src, out); break;
+    case 16: hipLaunchKernelGGL(probe_read_kernel<16>, g, b, 0, (hipStream_t)stream, (const u32x4*)src, out); break;
+    default: return 1;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
 extern "C" int pie_probe_copy(const void* src, void* dst, int64_t bytes, int nt, void* stream) {
