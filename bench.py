@@ -309,9 +309,28 @@ def _ops_ceiling(dev, run):
     # read phase (one 1024-thread work group per 256 KB row, 16 vectors per thread) and the best
     # read-only shape measured (256-thread groups, 16 vectors each), over the softmax's bytes and
     # over the sampler's fp32 rows
+    # the dense bf16 MFMA rate a kernel can reach (32x32x16, 2 work groups of 4 waves per CU,
+    # 4 independent accumulator chains per wave), alone and with as much independent fp32 VALU
+    # work interleaved: the matrix pipe's practical ceiling, and whether vector work overlaps it
+    lib.pie_probe_mfma.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]
+    mf_out = torch.empty(1 << 20, dtype=torch.float32, device=dev)
+    mf_blocks, mf_iters = 2 * 256, 2000
+    mf_flops = mf_blocks * 4 * mf_iters * 16 * 32768
+
+    def make_mfma(valu):
+        return lambda: lib.pie_probe_mfma(mf_out.data_ptr(), mf_blocks, mf_iters, valu, st())
+    mf = []
+    for valu, what in ((0, "alone"), (1, "with 128 independent fp32 fma per 16 MFMAs")):
+        e = run(f"ceiling mfma 32x32x16 bf16, {what}", 1 << 30, lambda v=valu: make_mfma(v))
+        for key in ("bytes", "gbs", "frac", "gbs_cold_single"):
+            e[key] = None  # no memory traffic to speak of
+        e["flops"] = mf_flops
+        e["tflops"] = round(mf_flops / e["us"] / 1e6, 1)
+        e["mfma_frac"] = round(mf_flops / e["us"] / 1e6 / 2500.0, 3)
+        mf.append(e)
     n_rd = 256 * 1024 * 256  # 256 rows of 256 KiB (softmax rows are 250.5 KiB)
     n_rd2 = 2 * n_rd
-    res = [run("ceiling read 64 MiB, 1 work group x 1024 threads x 16 vectors per 256 KiB (softmax read phase)",
+    res = mf + [run("ceiling read 64 MiB, 1 work group x 1024 threads x 16 vectors per 256 KiB (softmax read phase)",
                n_rd, lambda: make_read(n_rd, 1024, 16)),
            run("ceiling read 64 MiB, 256 threads x 16 vectors per work group", n_rd, lambda: make_read(n_rd, 256, 16)),
            run("ceiling read 128 MiB (sampler rows' bytes), 256 threads x 16 vectors per work group", n_rd2,

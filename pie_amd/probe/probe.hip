@@ -11,6 +11,10 @@
 //                       threads x vpt vectors with all of a thread's vpt loads issued before any
 //                       is used (the resident softmax's pattern at 1024 threads and vpt 16),
 //                       one xor per work group written out.
+//   pie_probe_mfma:     dense bf16 v_mfma_f32_32x32x16 throughput: 4 independent accumulator
+//                       chains per wave, 2 work groups of 4 waves per CU; with valu = 1, 128
+//                       independent fp32 fma per 16 MFMAs interleaved (does vector work overlap
+//                       the matrix pipe?).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -55,6 +59,47 @@ __global__ __launch_bounds__(1024) void probe_read_kernel(const u32x4* __restric
   atomicXor(&acc, x);
   __syncthreads();
   if (threadIdx.x == 0) out[blockIdx.x] = acc;
+}
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+template <bool VALU>
+__global__ __launch_bounds__(256, 2) void probe_mfma_kernel(float* out, int iters) {
+  f32x16 acc0 = {}, acc1 = {}, acc2 = {}, acc3 = {};
+  bf16x8 a, b;
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (__bf16)(threadIdx.x * 0.001f + i);
+    b[i] = (__bf16)(i * 0.5f);
+  }
+  float v[8];
+  for (int i = 0; i < 8; ++i) v[i] = threadIdx.x + i;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc1, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc2, 0, 0, 0);
+      acc3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc3, 0, 0, 0);
+      if constexpr (VALU) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] = fmaf(v[i], 1.0001f, 0.5f);
+      }
+    }
+  }
+  float s = 0.f;
+  for (int i = 0; i < 8; ++i) s += v[i];
+  for (int i = 0; i < 16; ++i) s += acc0[i] + acc1[i] + acc2[i] + acc3[i];
+  out[blockIdx.x * 256 + threadIdx.x] = s;
+}
+
+// flops of one launch: blocks * 4 waves * iters * 16 MFMAs * 32768
+extern "C" int pie_probe_mfma(float* out, int blocks, int iters, int valu, void* stream) {
+  if (blocks <= 0 || iters <= 0) return 1;
+  if (valu) hipLaunchKernelGGL(probe_mfma_kernel<true>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
+  else hipLaunchKernelGGL(probe_mfma_kernel<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, iters);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
 extern "C" int pie_probe_read(const void* src, int64_t bytes, int threads, int vpt, uint32_t* out, void* stream) {
