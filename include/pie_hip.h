@@ -381,7 +381,9 @@ int pie_hip_attention_decode_noalloc(const pie_bf16* q, int64_t q_tok_stride, in
  * position 32w+j; 0 past kv_len) in a caller buffer of mask_words uint32, and writes every query
  * token's visible extent (1 + its last visible position; int32 [num_tokens]) so the run skips kv
  * tiles no row of a work group can see. The run reads both with the plan, num_items and plan[4]
- * (mask_offsets_word).
+ * (mask_offsets_word). For head_dim 128 the run also writes the device copy of the plan: header
+ * words 7-15 count the work taken (one queue per XCD) and are back to zero when the run ends, so
+ * two runs with one plan must not overlap in time (on one stream they never do).
  */
 int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
                                    const int32_t* kv_last_page_len, int64_t batch,
