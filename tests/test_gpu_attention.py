@@ -293,6 +293,47 @@ def test_prefill_config3_sampled(dev):
         _tight(got[q0:q1], want, f"request {b}")
 
 
+@pytest.mark.parametrize("custom", [False, True])
+def test_prefill_repeated_runs_and_graph_replays(dev, custom):
+    """One plan, many runs: the head-dim-128 kernel counts its work in the plan's header and
+    leaves the counters at zero, so every eager run and every replay of a captured run gives the
+    first run's output bit for bit (with eager work between replays)."""
+    print(f"prefill repeated runs custom={custom}", flush=True)
+    a = wl.attn_batch([30, 0, 200, 5], [90, 64, 300, 40], Hq=32, Hkv=8, D=128, page_size=16, seed=121)
+    pb = a["batch"]
+    w = attention.BatchPrefillWithPagedKVCacheWrapper(_workspace(dev), a["layout"])
+    mask = _brle_causal_mask(pb).to(dev) if custom else None
+    w.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev), pb.kv_last_page_len.to(dev),
+           32, 8, 128, 16, custom_mask=mask, causal=not custom)
+    q, cache = a["q"].to(dev), a["cache"].to(dev)
+    out = torch.empty_like(q)
+    w.run(q, cache, out=out)
+    torch.cuda.synchronize()
+    first = out.clone()
+    for i in range(3):
+        out.zero_()
+        w.run(q, cache, out=out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, first), f"eager run {i + 1} differs"
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            w.run(q, cache, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for i in range(3):
+        out.zero_()
+        junk = torch.randn(1 << 20, device=dev).sum()  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first), f"replay {i} differs"
+        del junk
+    want = _want(a, custom=_brle_causal_mask(pb).numpy() if custom else None, causal=not custom)
+    assert_bf16_close(N(first), want, what="first run vs oracle")
+
+
 def test_prefill_rejects_bad_input(dev):
     a = wl.attn_batch([5, 0], [3, 4], Hq=8, Hkv=2, D=128, page_size=16, seed=102)
     pb = a["batch"]
