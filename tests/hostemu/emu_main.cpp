@@ -799,6 +799,9 @@ int main(int argc, char** argv) {
     case_attn_prefill(3, 6, 2, 128, 8, 30, 30, 2);    // custom mask, G = 3
     case_attn_prefill(2, 2, 1, 256, 16, 10, 20, 1);   // D = 256
     case_attn_prefill(2, 4, 1, 64, 1, 600, 10, 1);    // page size 1: several page-table windows
+    case_attn_prefill(2, 8, 2, 128, 5, 60, 50, 1);    // D = 128, page size 5: a tile's rows on several pages
+    case_attn_prefill(2, 4, 2, 128, 1, 600, 30, 2);   // D = 128, page size 1, custom mask, windows
+    case_attn_prefill(2, 8, 2, 128, 4, 70, 40, 0);    // D = 128, page size 4, full (non-causal)
     case_attn_prefill(2, 8, 2, 128, 16, 50, 100, 1);  // up to 400 rows: several items per request
     case_attn_prefill(2, 8, 2, 128, 16, 50, 100, 2);
     case_attn_prefill(3, 8, 2, 128, 16, 20, 120, 2, true);  // masks within the causal window
