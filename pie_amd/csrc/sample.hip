@@ -248,30 +248,61 @@ struct SampleArgs {
   int32_t vec;  // rows are 16-byte aligned: 16-byte loads
 };
 
+// min and max of v and the v of lane ^ j (j < 64), in registers: DPP within 16-lane rows
+// (quad_perm for j = 1, 2; row_shl:4 / row_shr:4 for j = 4; row_ror:8 for j = 8), and across
+// rows v_permlane16_swap / v_permlane32_swap, which leave {v, partner} in their two results.
+__device__ __forceinline__ void lane_pair(uint32_t v, int j, uint32_t& lo, uint32_t& hi) {
+  uint32_t a = v, b;
+  if (j == 1) {
+    b = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+  } else if (j == 2) {
+    b = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+  } else if (j == 4) {
+    const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xf, 0xf, false);  // lane + 4
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false);  // lane - 4
+    b = (threadIdx.x & 4) ? dn : up;
+  } else if (j == 8) {
+    b = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);  // row_ror:8
+  } else if (j == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+  }
+  lo = min(a, b);
+  hi = max(a, b);
+}
+
 // Short candidate lists (at most kSampThreads elements, in LDS): the top_k / top_p thresholds from
-// a bitonic sort of the keys (one per thread; compare-exchange partners within a wave through
-// ds_bpermute, across waves through LDS), a block scan of the sorted masses, and one thread
+// a bitonic sort of the keys (one per thread; compare-exchange partners within a wave in registers
+// by lane_pair, across waves through LDS), a block scan of the sorted masses, and one thread
 // that sees the cut. Radix passes over such lists serialise on LDS atomics: the keys of a row's
 // largest probabilities share their top bits, so every count lands in one or two bins. Same
 // kept sets as the radix selects: top_k keeps keys >= the k-th largest (ties stay), top_p keeps
 // keys >= the smallest key whose strictly larger keys' mass is below top_p * mass (the maximal
 // key when that product is <= 0).
 __device__ __forceinline__ uint32_t sort_desc_keys(uint32_t v, uint32_t* buf) {
-  const int t = threadIdx.x, lane = t & 63;
+  const int t = threadIdx.x;
+#pragma unroll
   for (int k = 2; k <= kSampThreads; k <<= 1) {
+#pragma unroll
     for (int j = k >> 1; j > 0; j >>= 1) {
-      uint32_t pv;
+      const bool desc = (t & k) == 0;     // this k-block sorts descending (the whole array at the end)
+      const bool first = (t & j) == 0;  // the lower position of the pair
       if (j >= 64) {
         __syncthreads();
         buf[t] = v;
         __syncthreads();
-        pv = buf[t ^ j];
+        const uint32_t pv = buf[t ^ j];
+        v = (first == desc) ? max(v, pv) : min(v, pv);
       } else {
-        pv = (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ j) << 2, (int)v);
+        uint32_t lo, hi;
+        lane_pair(v, j, lo, hi);
+        v = (first == desc) ? hi : lo;
       }
-      const bool desc = (t & k) == 0;     // this k-block sorts descending (the whole array at the end)
-      const bool first = (t & j) == 0;  // the lower position of the pair
-      v = (first == desc) ? max(v, pv) : min(v, pv);
     }
   }
   return v;

@@ -81,14 +81,19 @@ inline uint32_t exchange_read(uint32_t v, int src) {
 }
 
 inline int update_dpp(int old, int src, int ctrl, int, int, bool) {
-  (void)old;
   const int lane = ctx->lane;
   int from;
   if (ctrl < 0x100) {
     from = (lane & ~3) + ((ctrl >> (2 * (lane & 3))) & 3);
-  } else if (ctrl > 0x120 && ctrl < 0x130) {
+  } else if (ctrl > 0x120 && ctrl < 0x130) {  // row_ror:n, lane i reads lane i - n (mod 16)
     const int n = ctrl - 0x120;
     from = (lane & ~15) + (((lane & 15) - n + 16) & 15);
+  } else if ((ctrl > 0x100 && ctrl < 0x110) || (ctrl > 0x110 && ctrl < 0x120)) {
+    // row_shl:n (lane i reads lane i + n) and row_shr:n (lane i - n) within the row; a lane
+    // whose source lies outside its row keeps `old` (bound_ctrl off)
+    const int n = ctrl & 15, s = ctrl < 0x110 ? (lane & 15) + n : (lane & 15) - n;
+    const uint32_t r = exchange_read((uint32_t)src, s >= 0 && s < 16 ? (lane & ~15) + s : lane);
+    return s >= 0 && s < 16 ? (int)r : old;
   } else {
     fprintf(stderr, "emu: unsupported dpp ctrl 0x%x\n", ctrl);
     abort();
@@ -120,6 +125,20 @@ inline uint64_t ballot(bool v) {
 }
 
 inline int bpermute(int addr, int v) { return (int)exchange_read((uint32_t)v, (addr >> 2) & 63); }
+
+// v_permlane16_swap_b32 / v_permlane32_swap_b32: the odd 16-lane rows (32-lane halves) of `old`
+// trade places with the even rows (halves) of `src`; element 0 is the new `old`, 1 the new `src`.
+struct Swap2 {
+  uint32_t v[2];
+  uint32_t operator[](int i) const { return v[i]; }
+};
+inline Swap2 permlane_swap(uint32_t old, uint32_t src, int span) {
+  const bool even = (ctx->lane & span) == 0;
+  const uint32_t x = exchange_read(even ? src : old, ctx->lane ^ span);
+  return even ? Swap2{{old, x}} : Swap2{{x, src}};
+}
+inline Swap2 permlane16_swap(uint32_t old, uint32_t src, bool, bool) { return permlane_swap(old, src, 16); }
+inline Swap2 permlane32_swap(uint32_t old, uint32_t src, bool, bool) { return permlane_swap(old, src, 32); }
 
 
 inline float bf16_bits_to_float(uint16_t h) {
@@ -252,6 +271,8 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 #define __builtin_amdgcn_exp2f exp2f
 #define __builtin_amdgcn_ballot_w64 emu::ballot
 #define __builtin_amdgcn_ds_bpermute emu::bpermute
+#define __builtin_amdgcn_permlane16_swap emu::permlane16_swap
+#define __builtin_amdgcn_permlane32_swap emu::permlane32_swap
 #define __builtin_amdgcn_mfma_f32_16x16x32_bf16 emu::mfma_16x16x32_bf16
 #define __builtin_amdgcn_mfma_f32_32x32x16_bf16 emu::mfma_32x32x16_bf16
 #define __builtin_amdgcn_ds_read_tr16_b64_v4i16 emu::ds_read_tr16_b64
