@@ -29,9 +29,6 @@
 
 namespace pie {
 
-#ifndef PIE_SAMPLE_STOP
-#define PIE_SAMPLE_STOP 0  // measurement switch: 1 / 2 / 3 end the kernel after the floor / the gather / the short-list thresholds
-#endif
 constexpr int kSampThreads = 1024;
 constexpr int kSampWaves = kSampThreads / 64;
 constexpr double kMassScale = 1099511627776.0;  // 2^40
@@ -399,10 +396,6 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
   const bool short_list = list_buf && idx && V <= kSampThreads && a.mode != 3;
   if (short_list) {
     lo = list_threshold(p, V, a, r, npos, row_tot, sh, list_buf);
-#if PIE_SAMPLE_STOP == 3
-    if (threadIdx.x == 0) a.out[r] = (int)lo;
-    return;
-#endif
   } else if (a.mode == 2 || a.mode == 4) {
     const int32_t k = a.top_k ? a.top_k[r] : a.top_k_s;
     if (k > 0 && k < V) {
@@ -652,10 +645,7 @@ __device__ int compact_segment(const float* p, int V, bool vec, P&& pred, CandSh
     int vb = v0;  // wave-uniform position: every lane runs the same trips (ballots need them all)
     // batches of kU x 1 KiB per wave, the next batch's loads issued before the current one is
     // compacted (two batches in flight: one memory round trip per two batches)
-#ifndef PIE_GATHER_U
-#define PIE_GATHER_U 4
-#endif
-    constexpr int kU = PIE_GATHER_U, kB = kU * 64;
+    constexpr int kU = 4, kB = kU * 64;  // 4 measured best (2, 8 and 16 slower)
     if (vb + kB <= v1) {
       // two register buffers in turn (no copy between them, which would wait for the younger
       // batch's loads): while one batch is compacted the next one's loads are in flight
@@ -803,10 +793,6 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
     __syncthreads();
     const uint32_t floor0 = sh.u32a;
     __syncthreads();  // the sort buffer is dead from here: its memory holds the candidates
-#if PIE_SAMPLE_STOP == 1
-    if (threadIdx.x == 0) a.out[r] = (int)floor0;
-    return;
-#endif
     if (floor0 > 1u) {
       uint32_t c = 0;
       listed = gather([&](int, float x) {
@@ -817,10 +803,6 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
       npos = (int64_t)block_sum_u64(c, sh);
       __syncthreads();
     }
-#if PIE_SAMPLE_STOP == 2
-    if (threadIdx.x == 0) a.out[r] = (int)npos + sV;
-    return;
-#endif
   }
   // plain sampling, and top_k with k outside (0, V), keep every p > 0: no candidate list
   if (!listed && !(mode == 0 || ((mode == 2 || mode == 4) && !(k > 0 && k < V)))) {
@@ -920,7 +902,8 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_kernel(const void
       mx = x;
       am = i;
     }
-    s += __builtin_amdgcn_exp2f((x - mx) * c);
+    // a masked (-inf) logit adds 0; with mx still -inf, (x - mx) would be NaN
+    s += x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((x - mx) * c);
   };
   const int nv = vec ? V / E : 0;
   int v = threadIdx.x;
@@ -1089,7 +1072,9 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
         m = mj;
       }
       if (!greedy_row) {
-        const float mc = m * c;
+        // while every logit so far is -inf (masked), m is -inf: the reference 0 keeps
+        // fmaf(-inf, c, -mc) at -inf (exponential 0) instead of NaN
+        const float mc = m == -INFINITY ? 0.f : m * c;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
           x[e] = __builtin_amdgcn_exp2f(fmaf(x[e], c, -mc));
@@ -1108,7 +1093,7 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
       }
       mt = m;
       if (!greedy_row) {
-        et = __builtin_amdgcn_exp2f(fmaf(xt, c, -m * c));
+        et = __builtin_amdgcn_exp2f(fmaf(xt, c, m == -INFINITY ? 0.f : -m * c));
         s += et;
       }
     }

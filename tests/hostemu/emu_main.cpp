@@ -661,12 +661,20 @@ static void case_sample(int64_t B, int64_t V, int mode, bool row_map, bool peake
   check_equal("sample", out.p, want.p, B);
 }
 
-static void case_softmax(int64_t B, int64_t V, bool bf16) {
-  printf("scaled_softmax B=%lld V=%lld bf16=%d\n", (long long)B, (long long)V, (int)bf16);
+// masked: rows carry -inf logits (padding / banned tokens): row 1 its first 3/4, row 2 every
+// other 16-byte vector, row 3 everything but one token (B >= 4); the rest random.
+static void case_softmax(int64_t B, int64_t V, bool bf16, bool masked = false) {
+  printf("scaled_softmax B=%lld V=%lld bf16=%d masked=%d\n", (long long)B, (long long)V, (int)bf16, (int)masked);
   Buf<float> x(B * V), temps(B), out(B * V);
   Buf<uint16_t> xb(B * V), ob(B * V);
   std::normal_distribution<float> d(0.f, 3.f);
-  for (int64_t i = 0; i < B * V; ++i) { xb[i] = f2bf(d(rng)); x[i] = bf2f(xb[i]); }
+  for (int64_t i = 0; i < B * V; ++i) {
+    const int64_t r = i / V, c = i % V;
+    const bool m = masked && ((r == 1 && c < 3 * V / 4) || (r == 2 && (c / (bf16 ? 8 : 4)) % 2 == 0) ||
+                              (r == 3 && c != V / 3));
+    xb[i] = m ? (uint16_t)0xff80 : f2bf(d(rng));
+    x[i] = bf2f(xb[i]);
+  }
   for (int64_t r = 0; r < B; ++r) temps[r] = r == 0 ? 0.f : 0.3f + 0.4f * (float)r;
   if (bf16) rc_ok(pie_hip_scaled_softmax(xb.p, 1, V, B, V, temps.p, 1e-5f, ob.p, V, nullptr), "softmax");
   else rc_ok(pie_hip_scaled_softmax(x.p, 0, V, B, V, temps.p, 1e-5f, out.p, V, nullptr), "softmax");
@@ -792,6 +800,9 @@ int main(int argc, char** argv) {
     case_softmax(3, 1000, false);
     case_softmax(3, 777, true);
     case_softmax(2, 70003, false);   // rows not 16-byte aligned: the streaming kernel
+    case_softmax(4, 1000, false, true);   // -inf logits, register-resident kernel
+    case_softmax(4, 4096, true, true);
+    case_softmax(4, 70003, false, true);  // -inf logits, streaming kernel
   }
   if (all || c == "prefill") {
     case_attn_prefill(3, 8, 2, 128, 16, 40, 45, 1);   // causal, chunked prefill over cached context

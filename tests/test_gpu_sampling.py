@@ -199,6 +199,38 @@ def test_safe_scaled_softmax(dev, dtype, V, pad):
     np.testing.assert_allclose(gotf[2:].sum(-1), 1.0, rtol=2e-2 if dtype == torch.bfloat16 else 1e-5)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("V", [4096, 128256, 151936, 200003])
+def test_safe_scaled_softmax_masked_logits(dev, dtype, V):
+    """-inf logits (padding, banned tokens) get probability 0, as in the reference's Triton
+    kernel and torch.softmax: whole leading 16-byte groups of a thread masked (row 1: the first
+    3/4 of the row), every other 16-byte group (row 2), everything but one token (row 3, which
+    must come out exactly 1), a greedy row with masked entries (row 0). Register-resident sizes
+    and the streaming kernel (200003)."""
+    print(f"safe_scaled_softmax masked V={V} {dtype}", flush=True)
+    B, E = 6, (8 if dtype == torch.bfloat16 else 4)
+    g = torch.Generator().manual_seed(22)
+    x = torch.randn(B, V, generator=g) * 4
+    col = torch.arange(V)
+    x[0, : V // 2] = -float("inf")
+    x[1, : 3 * V // 4] = -float("inf")
+    x[2, (col // E) % 2 == 0] = -float("inf")
+    x[3, :] = -float("inf")
+    x[3, V // 3] = 1.5
+    x[4, -E * 3:] = -float("inf")
+    x = x.to(dtype)
+    temps = torch.tensor([0.0, 0.7, 1.0, 1.3, 0.5, 2.0])
+    got = sampling.safe_scaled_softmax(x.to(dev), temps.to(dev)).float().cpu().numpy().astype(np.float64)
+    want = oracle.scaled_softmax(x.float().numpy(), temps.numpy())
+    assert np.isfinite(got).all(), f"{(~np.isfinite(got)).sum()} non-finite entries"
+    assert (got[x.float().numpy() == -np.inf] == 0).all(), "masked logits must get probability 0"
+    assert got[3, V // 3] == 1.0 and got[3].sum() == 1.0
+    assert (got[0] == want[0]).all(), "greedy row"
+    rel = 2 ** -7 if dtype == torch.bfloat16 else 1e-5
+    bad = np.abs(got - want) > rel * np.abs(want) + 1e-30
+    assert not bad.any(), f"{bad.sum()} entries off, first {np.argwhere(bad)[:3]}"
+
+
 def test_sampling_chain_like_pie(dev):
     """Pie's order (common.py:226-283): softmax with temperatures, then a sampler per group."""
     B, V = 6, 32000

@@ -641,6 +641,9 @@ def test_scaled_softmax_vs_torch_reference():
     """Against Pie's own torch form (_safe_scaled_softmax_impl_torch, common.py:38-59) in fp64."""
     g = torch.Generator().manual_seed(32)
     x = torch.randn(4, 500, generator=g) * 4
+    x[1, :300] = -float("inf")  # masked logits (padding, banned tokens): probability 0
+    x[2, ::2] = -float("inf")
+    x[0, :10] = -float("inf")
     temps = torch.tensor([0.0, 0.5, 1.0, 2.5])
     safe = torch.where(temps[:, None] < 1e-5, 1.0, temps[:, None].double())
     soft = torch.softmax(x.double() / safe, -1)
