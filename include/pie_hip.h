@@ -28,6 +28,8 @@ enum {
   PIE_HIP_OK = 0,
   PIE_HIP_EINVAL = 1,  /* bad size, stride, null pointer or unsupported parameter */
   PIE_HIP_ELAUNCH = 2, /* the HIP runtime rejected the launch */
+  PIE_HIP_EBUSY = 3,   /* shared device state (static scratch, a prefill plan) still in use by
+                          a launch on another stream */
 };
 
 /* Message describing the last nonzero return on this thread ("" if none). */
@@ -343,7 +345,10 @@ int pie_hip_attention_decode(const pie_bf16* q, int64_t q_tok_stride, int64_t q_
  * process ends (need = batch * splits * num_qo_heads * (head_dim + 1) * 4 bytes when splits > 1;
  * larger requests return PIE_HIP_EINVAL). Results equal pie_hip_attention_decode's bit for bit.
  * No counterpart in the reference: it is for callers that cannot allocate (code under HIP graph
- * capture, tight serving loops). Calls that overlap on one GPU share the array and race.
+ * capture, tight serving loops). Calls that overlap on one GPU share the array and race, so
+ * use it from one stream per GPU: an eager call (splits > 1) made while the previous one is
+ * still running on a different stream returns PIE_HIP_EBUSY instead of racing. Calls recorded
+ * under graph capture are not checked; replays of such graphs must not overlap other users.
  */
 int pie_hip_attention_decode_noalloc(const pie_bf16* q, int64_t q_tok_stride, int64_t q_head_stride,
                                      const pie_bf16* k_cache, const pie_bf16* v_cache,
@@ -383,7 +388,10 @@ int pie_hip_attention_decode_noalloc(const pie_bf16* q, int64_t q_tok_stride, in
  * tiles no row of a work group can see. The run reads both with the plan, num_items and plan[4]
  * (mask_offsets_word). For head_dim 128 the run also writes the device copy of the plan: header
  * words 7-15 count the work taken (one queue per XCD) and are back to zero when the run ends, so
- * two runs with one plan must not overlap in time (on one stream they never do).
+ * the device plan is mutable state: two runs with one plan must not overlap in time (on one
+ * stream they never do). An eager run whose plan is still in use by a run on another stream
+ * returns PIE_HIP_EBUSY; runs recorded under graph capture are not checked. A plan made for
+ * head_dim 256 run with head_dim 64/128 (or the reverse) fills the output with NaN.
  */
 int pie_hip_attention_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
                                    const int32_t* kv_last_page_len, int64_t batch,

@@ -497,10 +497,7 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(int B, int Hq, int split
 // w (kv positions 32w..32w+31) at packed + word_off[b] + i * ceil(kv_len / 32) + w.
 // Work-group shape of attn_prefill_kernel: 4 waves of two 16-row MFMA row tiles (one for D = 256,
 // whose accumulators would not fit twice). Head dim 128 runs attn_prefill32_kernel (32 rows per
-// wave, same 128-row work items) unless PIE_PREFILL_MFMA32=0 selects this kernel for comparison.
-#ifndef PIE_PREFILL_MFMA32
-#define PIE_PREFILL_MFMA32 1
-#endif
+// wave, same 128-row work items).
 template <int D>
 constexpr int prefill_waves() { return 4; }
 template <int D>
@@ -555,6 +552,23 @@ __device__ __forceinline__ void mask_rows_extent(const int32_t* __restrict__ ext
   causal = s_mixed == 0;
 }
 
+// A plan made for another head_dim (its rows per item differ) cannot drive this kernel: every
+// work group fills the whole output (the plan's tokens, all q heads) with NaN instead, so the
+// mistake shows in the result rather than leaving the output unwritten.
+template <int D>
+__device__ void prefill_plan_mismatch(const int32_t* __restrict__ plan, const int32_t* __restrict__ qo_indptr,
+                                      int Hq, uint16_t* __restrict__ out, int64_t o_ts, int64_t o_hs) {
+  const int t0 = qo_indptr[0], T = qo_indptr[plan[1]] - t0;
+  constexpr int CH = D / 8;  // 16-byte chunks per head row
+  const int64_t n = (int64_t)T * Hq * CH;
+  const uint4 nan4 = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / (Hq * CH);
+    const int h = (int)(i / CH % Hq), c = (int)(i % CH);
+    *reinterpret_cast<uint4*>(out + (t0 + t) * o_ts + (int64_t)h * o_hs + 8 * c) = nan4;
+  }
+}
+
 template <int D>
 __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv,
@@ -574,9 +588,13 @@ __global__ __launch_bounds__(64 * prefill_waves<D>(), prefill_min_waves<D>()) vo
   __shared__ __attribute__((aligned(16))) char smem[kSmem];
   __shared__ int32_t ptab[kPageWin];
 
+  if (plan[2] != kPrefillRows) {
+    prefill_plan_mismatch<D>(plan, qo_indptr, G * n_kv_heads, out, o_ts, o_hs);
+    return;
+  }
   int kvh;
   const int32_t* item = prefill_unit(plan, n_items, n_kv_heads, kvh);
-  if (!item || plan[2] != kPrefillRows) return;  // padding work group, or a plan made for another head_dim
+  if (!item) return;  // padding work group
   const int b = item[0], row0 = item[1], q0 = item[2], qo_len = item[3], kv_len = item[4];
   const int page0 = item[5];
   const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
@@ -865,7 +883,10 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
   // queue is empty. XCD x's queue is the contiguous run [x * per, (x + 1) * per) of the units, in
   // plan order (each request's items together), so the work groups of one XCD share the K/V
   // prefix they read through its L2; a work group whose queue is empty takes from the others.
-  if (plan[2] != kRows) return;  // a plan made for another head_dim
+  if (plan[2] != kRows) {
+    prefill_plan_mismatch<D>(plan, qo_indptr, G * n_kv_heads, out, o_ts, o_hs);
+    return;
+  }
   int32_t* counters = const_cast<int32_t*>(plan);
   __shared__ int s_unit;
   const int units = n_items * n_kv_heads, per = (units + 7) / 8;
@@ -1125,7 +1146,9 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
       }
   }
   }
-  // the last work group out resets the counters for the next launch with this plan
+  // the last work group out resets the counters for the next launch with this plan; the fence
+  // orders this group's queue atomics before its done count
+  __threadfence();
   if (threadIdx.x == 0 && atomicAdd(&counters[kPlanDoneWord], 1) == (int)gridDim.x - 1) {
     for (int x = 0; x < 8; ++x) atomicExch(&counters[kPlanQueueWord + x], 0);
     atomicExch(&counters[kPlanDoneWord], 0);
@@ -1301,14 +1324,18 @@ extern "C" int pie_hip_attention_decode_noalloc(
               what, (long long)need, (long long)kDecodeScratchBytes);
   void* ws = nullptr;
   if (need > 0) {
-    const int rc = decode_scratch(&ws);
+    int rc = decode_scratch(&ws);
+    if (rc) return rc;
+    rc = inflight_check(ws, stream, what);
     if (rc) return rc;
   }
-  return attention_decode_impl(q, q_tok_stride, q_head_stride, k_cache, v_cache, page_stride,
+  const int rc = attention_decode_impl(q, q_tok_stride, q_head_stride, k_cache, v_cache, page_stride,
                                slot_stride, head_stride, num_pages, kv_indptr, kv_indices,
                                kv_last_page_len, batch, num_qo_heads, num_kv_heads, head_dim,
                                page_size, sm_scale, window_left, sinks, splits, ws, kDecodeScratchBytes,
                                out, o_tok_stride, o_head_stride, stream, what);
+  if (rc == PIE_HIP_OK && need > 0) inflight_mark(ws, stream);
+  return rc;
 }
 
 // Host: the prefill work list. Reads host copies of qo_indptr, kv_indptr and kv_last_page_len
@@ -1405,7 +1432,7 @@ static void launch_prefill(hipStream_t st, dim3 grid, const uint16_t* q, int64_t
   // attn_prefill32_kernel scales raw scores inside the exponent, where a zero scale would turn a
   // hidden (-inf) score into NaN; 1e-30 gives the same result (every exponent rounds to 2^0).
   const dim3 xgrid(8 * ((grid.x * grid.y + 7) / 8));  // (kv head, item) units, padded to 8 XCDs
-  if constexpr (D == 128 && PIE_PREFILL_MFMA32)
+  if constexpr (D == 128)
     hipLaunchKernelGGL(attn_prefill32_kernel<128>, dim3(8 * ((2 * num_cus() + 7) / 8)), dim3(256), 0, st, q, q_ts,
                        q_hs, kv, qo_indptr, G,
                        sl2 == 0.f ? 1e-30f : sl2, plan, (int)grid.x, (int)grid.y, mode, window_left, packed,
@@ -1510,6 +1537,9 @@ extern "C" int pie_hip_attention_prefill(
   const int Wl = window_left < 0 ? -1 : (int)std::min<int64_t>(window_left, 1 << 30);
   const dim3 grid((unsigned)num_items, (unsigned)num_kv_heads);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // the head-dim-128 kernel counts its work in the plan's header words
+  const bool counters = head_dim == 128;
+  if (counters && (rc = inflight_check(plan, stream, "attention_prefill")) != PIE_HIP_OK) return rc;
   switch (head_dim) {
     case 64: launch_prefill<64>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
                                 mode, Wl, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride, sinks); break;
@@ -1518,7 +1548,9 @@ extern "C" int pie_hip_attention_prefill(
     default: launch_prefill<256>(st, grid, q, q_tok_stride, q_head_stride, kv, qo_indptr, G, sl2, plan,
                                  mode, Wl, packed_mask, woff, mask_extent, out, o_tok_stride, o_head_stride, sinks); break;
   }
-  return check_launch("attention_prefill");
+  rc = check_launch("attention_prefill");
+  if (rc == PIE_HIP_OK && counters) inflight_mark(plan, stream);
+  return rc;
 }
 
 extern "C" int pie_hip_attention_pack_mask(const uint8_t* custom_mask, const int32_t* plan,

@@ -6,6 +6,7 @@
 #include <stdio.h>
 
 #include <mutex>
+#include <unordered_map>
 
 #include "common.h"
 
@@ -38,6 +39,49 @@ int num_cus() {
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
   cached[dev] = n;
   return n;
+}
+
+namespace {
+struct Inflight {
+  hipStream_t stream;
+  hipEvent_t done;
+};
+std::mutex g_inflight_mu;
+std::unordered_map<const void*, Inflight> g_inflight;
+
+bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+}  // namespace
+
+int inflight_check(const void* key, void* stream, const char* what) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (capturing(st)) return PIE_HIP_OK;
+  std::lock_guard<std::mutex> lk(g_inflight_mu);
+  auto it = g_inflight.find(key);
+  if (it == g_inflight.end() || it->second.stream == st) return PIE_HIP_OK;
+  if (hipEventQuery(it->second.done) == hipErrorNotReady)
+    return set_error(PIE_HIP_EBUSY,
+                     "%s: a launch on another stream still uses the same device state (the "
+                     "static scratch or the prefill plan); synchronise first, or give each stream "
+                     "its own",
+                     what);
+  return PIE_HIP_OK;
+}
+
+void inflight_mark(const void* key, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (capturing(st)) return;
+  std::lock_guard<std::mutex> lk(g_inflight_mu);
+  auto it = g_inflight.find(key);
+  if (it == g_inflight.end()) {
+    hipEvent_t ev = nullptr;
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) return;
+    it = g_inflight.emplace(key, Inflight{st, ev}).first;
+  }
+  it->second.stream = st;
+  (void)hipEventRecord(it->second.done, st);
 }
 
 }  // namespace pie

@@ -17,6 +17,15 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 int num_cus();  // compute units of the current device (cached per device)
 
+// Device state that overlapping launches would race on (the allocation-free decode's static
+// scratch, a prefill plan's work counters), keyed by its address. inflight_check refuses a
+// launch (PIE_HIP_EBUSY) while the last launch that used `key` is still running on another
+// stream; launches on the same stream are ordered by it and pass. inflight_mark records the
+// launch just made. Launches recorded under stream capture are neither checked nor recorded:
+// they run at replay, which the host does not see.
+int inflight_check(const void* key, void* stream, const char* what);
+void inflight_mark(const void* key, void* stream);
+
 // ---------------------------------------------------------------- grouped launch (host)
 // Between pie_hip_group_begin and pie_hip_group_end (group.hip) the groupable entry points
 // validate their arguments, then hand them to group_add_* instead of launching; the group's

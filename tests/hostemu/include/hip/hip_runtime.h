@@ -8,6 +8,7 @@
 // gathers), global_load_lds (a per-lane copy), the fp builtins used, hipLaunchKernelGGL and the few runtime calls made.
 #pragma once
 
+#include <atomic>
 #include <barrier>
 #include <cmath>
 #include <cstdint>
@@ -38,6 +39,17 @@ inline const char* hipGetErrorString(hipError_t) { return "emulated"; }
 inline hipError_t hipGetDevice(int* d) { *d = 0; return hipSuccess; }
 inline hipError_t hipGetSymbolAddress(void** p, const void* sym) { *p = const_cast<void*>(sym); return hipSuccess; }
 #define HIP_SYMBOL(x) (&(x))
+// streams and events: the emulator runs every launch synchronously, so nothing is ever in flight
+typedef void* hipEvent_t;
+enum { hipErrorNotReady = 600, hipEventDisableTiming = 2 };
+enum hipStreamCaptureStatus { hipStreamCaptureStatusNone = 0, hipStreamCaptureStatusActive = 1 };
+inline hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus* s) {
+  *s = hipStreamCaptureStatusNone;
+  return hipSuccess;
+}
+inline hipError_t hipEventCreateWithFlags(hipEvent_t* e, unsigned) { *e = (hipEvent_t)1; return hipSuccess; }
+inline hipError_t hipEventRecord(hipEvent_t, hipStream_t) { return hipSuccess; }
+inline hipError_t hipEventQuery(hipEvent_t) { return hipSuccess; }
 inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
   const char* e = getenv("EMU_CUS");
   *v = e ? atoi(e) : 1;  // few "CUs" so grid caps engage and grid-stride loops iterate
@@ -265,6 +277,7 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 #define blockDim (emu::ctx->bdim)
 #define gridDim (emu::ctx->gdim)
 #define __syncthreads() (emu::ctx->block->arrive_and_wait())
+#define __threadfence() std::atomic_thread_fence(std::memory_order_seq_cst)
 #define __builtin_amdgcn_update_dpp emu::update_dpp
 #define __builtin_amdgcn_readlane emu::readlane
 #define __builtin_amdgcn_readfirstlane emu::readfirstlane

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from pie_amd import attention
+from pie_amd import _lib, attention
 from pie_amd import workloads as wl
 from tests._util import assert_bf16_close
 
@@ -332,6 +332,49 @@ def test_prefill_repeated_runs_and_graph_replays(dev, custom):
         del junk
     want = _want(a, custom=_brle_causal_mask(pb).numpy() if custom else None, causal=not custom)
     assert_bf16_close(N(first), want, what="first run vs oracle")
+
+
+def test_prefill_plan_in_use_on_another_stream_is_refused(dev):
+    """The head-dim-128 kernel counts its work in the device plan, so two runs sharing a plan
+    must not overlap: an eager run while the plan is still in use on another stream is refused
+    (PIE_HIP_EBUSY), runs on the same stream queue as usual, and after a synchronisation the
+    other stream runs and gives the same output bit for bit."""
+    a = wl.attn_batch([0, 0, 0, 0], [4096, 4096, 4096, 4096], Hq=32, Hkv=8, D=128, page_size=16, seed=131)
+    pb = a["batch"]
+    w = attention.BatchPrefillWithPagedKVCacheWrapper(_workspace(dev), "NHD")
+    w.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev), pb.kv_last_page_len.to(dev),
+           32, 8, 128, 16, causal=True)
+    q, cache = a["q"].to(dev), a["cache"].to(dev)
+    out1, out2 = torch.empty_like(q), torch.empty_like(q)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(s1):
+        for _ in range(4):  # ~1 ms of queued work on s1
+            w.run(q, cache, out=out1)
+    with torch.cuda.stream(s2):
+        with pytest.raises(_lib.PieHipError, match="another stream"):
+            w.run(q, cache, out=out2)
+    s1.synchronize()
+    with torch.cuda.stream(s2):
+        w.run(q, cache, out=out2)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+
+
+def test_prefill_plan_for_another_head_dim_gives_nan(dev):
+    """A device plan made for head_dim 256 (other rows per item) driving the head-dim-128 kernel
+    through the C ABI: the kernel cannot use it and fills the whole output with NaN instead of
+    returning with the output unwritten."""
+    a = wl.attn_batch([20, 3], [40, 9], Hq=8, Hkv=2, D=128, page_size=16, seed=132)
+    pb = a["batch"]
+    w = attention.BatchPrefillWithPagedKVCacheWrapper(_workspace(dev), "NHD")
+    w.plan(pb.qo_indptr.to(dev), pb.kv_indptr.to(dev), pb.kv_indices.to(dev), pb.kv_last_page_len.to(dev),
+           8, 2, 256, 16, causal=True)
+    w._plan["D"] = 128  # bypass the wrapper's own shape check to reach the kernel
+    out = torch.zeros_like(a["q"], device=dev)
+    w.run(a["q"].to(dev), a["cache"].to(dev), out=out)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()
 
 
 def test_prefill_rejects_bad_input(dev):

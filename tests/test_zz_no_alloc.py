@@ -84,3 +84,26 @@ def test_noalloc_decode_rejects_oversize(dev):
     rc = lib.pie_hip_attention_decode_noalloc(16, 0, 0, 16, 16, 0, 0, 0, 1, 16, 16, 16, 256, 32, 8,
                                               128, 16, C.c_float(1.0), -1, None, 64, 16, 0, 0, None)
     assert rc == 1 and "static scratch" in lib.pie_hip_last_error().decode()
+
+
+def test_noalloc_decode_refuses_overlap_on_another_stream(dev):
+    """The static scratch is shared by every call on a GPU: an eager call (splits > 1) while a
+    call on another stream is still running is refused (PIE_HIP_EBUSY) instead of racing; the
+    same stream queues as usual, and after a synchronisation the other stream runs."""
+    a = wl.attn_decode_cfg()
+    keep, q, kp, vp, ps, ss, hs, npages, (ip, ix, ll) = _args(a, dev)
+    B, Hq, Hkv, D = q.shape[0], a["Hq"], a["Hkv"], a["D"]
+    out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=dev)
+    common = (q.data_ptr(), q.stride(0), q.stride(1), kp, vp, ps, ss, hs, npages, ip.data_ptr(),
+              ix.data_ptr(), ll.data_ptr(), B, Hq, Hkv, D, a["batch"].page_size,
+              C.c_float(D ** -0.5), -1, None, 2, out.data_ptr(), out.stride(0), out.stride(1))
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(4):  # ~1.6 ms queued on s1
+        _lib.call("pie_hip_attention_decode_noalloc", *common, s1.cuda_stream)
+    with pytest.raises(_lib.PieHipError, match="another stream"):
+        _lib.call("pie_hip_attention_decode_noalloc", *common, s2.cuda_stream)
+    s1.synchronize()
+    _lib.call("pie_hip_attention_decode_noalloc", *common, s2.cuda_stream)
+    torch.cuda.synchronize()
+    del keep
