@@ -24,6 +24,13 @@ def assert_bf16_close(got, want, rtol=RTOL, atol=ATOL, what=""):
         raise AssertionError(f"{what}: {int((~ok).sum())} of {ok.size} outside tolerance; {detail}")
 
 
+def assert_bf16_close_rows(got, want, chunk=1024, what="", **kw):
+    """assert_bf16_close over the leading dimension in chunks (bounded temporaries at full size)."""
+    assert got.shape == want.shape, f"{what}: shape {got.shape} != {want.shape}"
+    for r0 in range(0, got.shape[0], chunk):
+        assert_bf16_close(got[r0:r0 + chunk], want[r0:r0 + chunk], what=f"{what} rows {r0}+", **kw)
+
+
 def assert_bits_equal(got, want, what=""):
     got, want = np.asarray(got), np.asarray(want)
     assert got.shape == want.shape, f"{what}: shape {got.shape} != {want.shape}"

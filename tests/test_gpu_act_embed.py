@@ -8,7 +8,7 @@ import torch
 import oracle
 from pie_amd import ops
 from pie_amd import workloads as wl
-from tests._util import assert_bf16_close, assert_bits_equal, ulp_diff
+from tests._util import assert_bf16_close, assert_bf16_close_rows, assert_bits_equal, ulp_diff
 
 pytestmark = pytest.mark.gpu
 N = oracle.to_np
@@ -42,11 +42,13 @@ def test_silu_and_mul_matches_torch_expression(dev):
 
 
 def test_silu_and_mul_full_config2(dev):
+    """Llama-3-8B prefill shape, every element against the oracle (1e-2 / 2e-2 and <= 2 ulp)."""
     c = wl.cfg2(H=8)
-    out = ops.silu_and_mul(c["gate_up"].to(dev))
-    rows = torch.randperm(8192, generator=torch.Generator().manual_seed(1))[:48]
-    assert_bf16_close(N(out.cpu()[rows]), oracle.silu_and_mul(N(c["gate_up"][rows])),
-                      what="cfg2 silu rows")
+    out = N(ops.silu_and_mul(c["gate_up"].to(dev)))
+    want = oracle.silu_and_mul(N(c["gate_up"]))
+    assert_bf16_close_rows(out, want, what="cfg2 silu")
+    for r0 in range(0, out.shape[0], 1024):
+        assert ulp_diff(out[r0:r0 + 1024], want[r0:r0 + 1024]).max() <= 2, f"rows {r0}+"
 
 
 @pytest.mark.parametrize("V,H,T", [(1000, 64, 300), (50, 4096, 7), (300, 100, 40), (10, 8, 0)])

@@ -12,7 +12,7 @@ import torch
 import oracle
 from pie_amd import ops
 from pie_amd import workloads as wl
-from tests._util import assert_bf16_close, assert_bits_equal, ulp_diff
+from tests._util import assert_bf16_close, assert_bf16_close_rows, assert_bits_equal, ulp_diff
 
 pytestmark = pytest.mark.gpu
 N = oracle.to_np
@@ -99,14 +99,17 @@ def test_fused_add_rmsnorm_inplace(dev):
 
 
 def test_add_rmsnorm_full_config2(dev):
-    """Llama-3-8B prefill shape: s bit-exact everywhere, y vs the oracle on sampled rows."""
+    """Llama-3-8B prefill shape: s bit-exact everywhere (against the IEEE add and the oracle),
+    every row of y against the oracle."""
     c = wl.cfg2(I=8)
     x, r, w = c["x"].to(dev), c["r"].to(dev), c["w"].to(dev)
     y, s = ops.add_rms_norm(x, r, w, 1e-5)
     assert torch.equal(s.view(torch.int16), (r + x).view(torch.int16))  # IEEE add + RNE
-    rows = torch.randperm(8192, generator=torch.Generator().manual_seed(0))[:96]
-    wy, _ = oracle.add_rmsnorm(N(c["x"][rows]), N(c["r"][rows]), N(c["w"]), 1e-5)
-    assert_bf16_close(N(y.cpu()[rows]), wy, what="cfg2 y rows")
+    wy, ws = oracle.add_rmsnorm(N(c["x"]), N(c["r"]), N(c["w"]), 1e-5)
+    assert_bits_equal(N(s), ws, "cfg2 s")
+    gy = N(y)
+    assert_bf16_close_rows(gy, wy, what="cfg2 y")
+    assert ulp_diff(gy, wy).max() <= 2
 
 
 @pytest.mark.parametrize("D", [128, 64, 256, 96])

@@ -10,7 +10,7 @@ import torch
 import oracle
 from pie_amd import ops
 from pie_amd import workloads as wl
-from tests._util import assert_bf16_close, assert_bits_equal
+from tests._util import assert_bf16_close, assert_bf16_close_rows, assert_bits_equal
 
 pytestmark = pytest.mark.gpu
 N = oracle.to_np
@@ -162,7 +162,7 @@ def test_fused_rope_append_equals_separate(dev, interleave, rd):
 
 def test_config3_full(dev):
     """Llama-3 prefill batch (64 ragged requests, T ~ 65k): append bit-exact on the whole
-    8192-page pool; RoPE vs the oracle on sampled tokens; fused == separate."""
+    8192-page pool; RoPE vs the oracle on every token; fused == separate."""
     c = wl.cfg3()
     pb, T = c["batch"], c["qkv"].shape[0]
     q0, k0, v0 = wl.split_qkv(c["qkv"], 32, 8, 128)
@@ -179,11 +179,11 @@ def test_config3_full(dev):
     assert oracle.append(kr, N(v0), N(pb.batch_indices), N(pb.positions), want,
                          N(pb.kv_indices), N(pb.kv_indptr)) == T
     assert_bits_equal(N(cache), want, "cfg3 cache")
-    rows = torch.randperm(T, generator=torch.Generator().manual_seed(2))[:512]
     f = oracle.inv_freq_llama31(128, 8.0, 5e5, 1.0, 4.0, 8192)
-    wq, wk = _oracle_rope(q0[rows], k0[rows], pb.positions[rows], f)
-    assert_bf16_close(N(q)[rows.numpy()], wq, what="cfg3 q rows")
-    assert_bf16_close(kr[rows.numpy()], wk, what="cfg3 k rows")
+    wq, wk = _oracle_rope(q0, k0, pb.positions, f)  # every token
+    assert_bf16_close_rows(N(q), wq, chunk=4096, what="cfg3 q")
+    assert_bf16_close_rows(kr, wk, chunk=4096, what="cfg3 k")
+    del wq, wk
     b = c["qkv"].to(dev)
     qb, kb, vb = wl.split_qkv(b, 32, 8, 128)
     cb = _cache(c["cache_shape"], "NHD", dev)
