@@ -320,16 +320,7 @@ def _ops_ceiling(dev, run):
     def make_mfma(valu):
         return lambda: lib.pie_probe_mfma(mf_out.data_ptr(), mf_blocks, mf_iters, valu, st())
     mf = []
-    for valu, what in ((0, "alone"), (1, "with 128 independent fp32 fma per 16 MFMAs"),
-                       (2, "one dependent accumulator chain"),
-                       (3, "attention tile shape: chain of 8 -> bf16 pack -> 8 MFMAs on 4 accumulators"),
-                       (4, "attention tile shape with the softmax's max, 16 exp2 and sum"),
-                       (5, "attention tile shape, softmax, K and V operands from LDS"),
-                       (6, "attention tile shape, softmax, operands from LDS, a barrier per tile"),
-                       (7, "attention tile shape, softmax, K operands (ds_read_b128) from LDS"),
-                       (8, "attention tile shape, softmax, V operands (ds_read_b64_tr_b16) from LDS"),
-                       (9, "attention tile shape, softmax, operands from LDS, 64 rows per wave, 1 wave per SIMD"),
-                       (10, "attention tile shape, softmax, operands from LDS (V transposed, ds_read_b128), a barrier per tile")):
+    for valu, what in ((0, "alone"), (1, "with 128 independent fp32 fma per 16 MFMAs")):
         e = run(f"ceiling mfma 32x32x16 bf16, {what}", 1 << 30, lambda v=valu: make_mfma(v))
         for key in ("bytes", "gbs", "frac", "gbs_cold_single"):
             e[key] = None  # no memory traffic to speak of

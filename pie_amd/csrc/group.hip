@@ -147,11 +147,8 @@ __global__ __launch_bounds__(256) void decode_group_kernel(GroupArgs g) {
   else act_and_mul_block<AU, kSilu>(g.act, (uint32_t)b);
 }
 
-// 16-byte output vectors per thread in the activation's block range (measurement switch).
-#ifndef PIE_GROUP_ACT_U
-#define PIE_GROUP_ACT_U 1
-#endif
-constexpr int kActU = PIE_GROUP_ACT_U;
+// 16-byte output vectors per thread in the activation's block range (2 and 4 measured slower).
+constexpr int kActU = 1;
 
 // ---------------------------------------------------------------- host: recording
 enum { kOpEmbed = 0, kOpAddNorm = 1, kOpAct = 2, kOpQk = 3 };

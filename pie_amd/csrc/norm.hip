@@ -56,10 +56,7 @@ __device__ __forceinline__ void row_offsets(const RowSet& s, int64_t r, int64_t&
 
 // Rows per wave group in flight at once. 1 measured best on configuration 2 (steady state:
 // 2 rows equal, 4 rows 6% slower: the extra registers cost more occupancy than they gain).
-#ifndef PIE_NORM_RPG
-#define PIE_NORM_RPG 1
-#endif
-constexpr int kRowsPerGroup = PIE_NORM_RPG;
+constexpr int kRowsPerGroup = 1;
 
 // ---------------------------------------------------------------- W waves per row, VPL*512*W cols
 // A row is held in registers by a group of W wavefronts (VPL 16-byte vectors per lane); lane l
@@ -415,12 +412,8 @@ bool rowset_vec_ok(const RowSet& s, bool add) {
   return ok;
 }
 
-// Measurement switch: 0 keeps large row lists on the cached row-loop kernel (configuration 2,
-// same box: per op 47.8 us against 44.1 us; in the back-to-back add-norm + SiLU step, whose
-// SiLU then drains the norm's cached writes, 6.44 against 6.35 TB/s).
-#ifndef PIE_NORM_LARGE_NT
-#define PIE_NORM_LARGE_NT 1
-#endif
+// Large row lists (past 64 MB) take the non-temporal one-row-per-block kernel: on configuration
+// 2 it measured 44.1 us per op against 47.8 us for the cached row-loop kernel.
 template <bool ADD, bool GEMMA>
 int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
   const int64_t rows = a.set[0].rows + a.set[1].rows;
@@ -429,7 +422,7 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
                    (a.set[1].rows == 0 || rowset_vec_ok(a.set[1], ADD));
   const dim3 blk(256);
   const int64_t in_bytes = rows * a.cols * 2;
-  const bool large = PIE_NORM_LARGE_NT && in_bytes >= (int64_t)64 << 20;  // far larger than L2
+  const bool large = in_bytes >= (int64_t)64 << 20;  // far larger than L2
   // (the residual-add form only: a plain norm, one input stream, keeps too few bytes in flight at
   // one vector per lane and stays on the row-loop kernel with 4 vectors per lane)
   static const bool forced_rowblock = [] {  // tuning override: PIE_HIP_NORM_ROWBLOCK=1
@@ -503,7 +496,7 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
       // 4.72 us against 6.05 us cached; a plain copy of the same bytes takes 3.79 us
       // non-temporal, 4.42 cached). Decode-sized lists keep their outputs in L2 for the next kernel.
       const bool nt = forced_nt == 0 || forced_nt == 1 ? forced_nt == 1
-                                                       : PIE_NORM_LARGE_NT && in_bytes >= (int64_t)8 << 20;
+                                                       : in_bytes >= (int64_t)8 << 20;
       switch ((n512 / W) * 2 + (nt ? 1 : 0)) {
 #define PIE_NV(n)                                                                                      \
   case 2 * n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, kRowsPerGroup, ADD, GEMMA, false>), grd, tb, 0, st, a, W); \

@@ -19,10 +19,15 @@ The model files also call ``torch.nn.functional`` inline, bound as ``fun`` at im
 and ``patch_mlp(cls)`` replaces a Llama-style ``ForwardPass.mlp`` (llama3.py:543-586,
 qwen3.py:526-571) with one that runs ``fun.silu(gate) * up`` as one SiLU-and-mul kernel. Neither
 edits the model files.
+
+``PIE_HIP_OPS=0`` in the environment turns all three into no-ops, so the same launch script runs
+the reference path (the real flashinfer and torch) for A/B comparisons; the kernels themselves
+never fall back to anything.
 """
 from __future__ import annotations
 
 import importlib
+import os
 import sys
 import types
 
@@ -48,6 +53,12 @@ HOT_PATH = (
 # flashinfer's attention wrapper classes (llama3.py:293-313)
 ATTENTION = ("BatchDecodeWithPagedKVCacheWrapper", "BatchPrefillWithPagedKVCacheWrapper",
              "BatchAttentionWithAttentionSinkWrapper")  # the last: gpt_oss.py:420-438
+
+
+def enabled() -> bool:
+    """False when PIE_HIP_OPS=0: install(), install_functional() and patch_mlp() leave the
+    reference path in place."""
+    return os.environ.get("PIE_HIP_OPS", "1").strip() != "0"
 
 
 class _Namespace(types.ModuleType):
@@ -76,8 +87,16 @@ class _Namespace(types.ModuleType):
 
 def install(name: str = "flashinfer", forward_unserved: bool = False) -> types.ModuleType:
     """Make ``import <name>`` return the pie_amd namespace; returns that module. With
-    forward_unserved=True, names this package does not serve come from the real package."""
+    forward_unserved=True, names this package does not serve come from the real package. With
+    PIE_HIP_OPS=0 nothing is installed and the real package (None if absent) is returned."""
     cur = sys.modules.get(name)
+    if not enabled():
+        if isinstance(cur, _Namespace):
+            return cur
+        try:
+            return cur if cur is not None else importlib.import_module(name)
+        except ImportError:
+            return None
     if isinstance(cur, _Namespace):
         cur._forward = forward_unserved
         return cur
@@ -153,7 +172,10 @@ functional = _Functional()
 
 def install_functional(*modules) -> None:
     """Rebind ``fun`` (torch.nn.functional) in the given model modules to ``functional``; loads
-    the kernel library first, so a missing library fails here, not on the first call."""
+    the kernel library first, so a missing library fails here, not on the first call. With
+    PIE_HIP_OPS=0 the modules keep torch.nn.functional."""
+    if not enabled():
+        return
     _lib.load()
     for m in modules:
         if getattr(m, "fun", None) is not _F and getattr(m, "fun", None) is not functional:
@@ -187,7 +209,9 @@ def _mlp(self, hidden_states: torch.Tensor, layer_idx: int) -> torch.Tensor:
 
 def patch_mlp(cls) -> None:
     """Replace ``cls.mlp`` (a Llama-style ForwardPass: llama3, qwen2, qwen3, mistral3) with _mlp;
-    ``unpatch_mlp`` restores it."""
+    ``unpatch_mlp`` restores it. With PIE_HIP_OPS=0 the class keeps its own mlp."""
+    if not enabled():
+        return
     _lib.load()
     if getattr(cls, "_pie_amd_mlp", None) is None:
         cls._pie_amd_mlp = cls.mlp

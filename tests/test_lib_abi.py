@@ -144,6 +144,37 @@ def test_integration_does_not_forward_unserved_names_by_default(monkeypatch):
     assert sys.modules["flashinfer"] is real
 
 
+def test_pie_hip_ops_0_leaves_the_reference_path(monkeypatch):
+    """PIE_HIP_OPS=0 (the A/B switch): install() keeps the real flashinfer (or none), the
+    model modules keep torch.nn.functional and the Llama-style mlp stays the model's own."""
+    import sys
+    import types
+    import torch.nn.functional as F
+    from pie_amd import integration
+    monkeypatch.setenv("PIE_HIP_OPS", "0")
+    assert not integration.enabled()
+    real = types.ModuleType("flashinfer")
+    monkeypatch.setitem(sys.modules, "flashinfer", real)
+    assert integration.install() is real and sys.modules["flashinfer"] is real
+    monkeypatch.delitem(sys.modules, "flashinfer")
+    assert integration.install() is None and "flashinfer" not in sys.modules  # no real package here
+    model = types.ModuleType("fake_model")
+    model.fun = F
+    integration.install_functional(model)
+    assert model.fun is F
+
+    class FP:
+        def mlp(self):
+            return "own"
+    integration.patch_mlp(FP)
+    assert FP().mlp() == "own"
+    monkeypatch.setenv("PIE_HIP_OPS", "1")
+    assert integration.enabled()
+    integration.install_functional(model)
+    assert model.fun is integration.functional
+    integration.uninstall_functional(model)
+
+
 def test_prefill_plan_position_limits_without_a_gpu():
     """The prefill plan (host code) takes requests of up to 2^31 - 1 positions, and up to
     2^30 - 1 under a custom mask (the extent kernel marks exactly causal rows in bit 30)."""
