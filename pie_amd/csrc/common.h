@@ -227,6 +227,40 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Compiler-only fences on values (no instruction is emitted). keep_s: x is materialised in
+// scalar registers here, so the loads it comes from are waited for at this point and not later.
+// opaque_v: x passes through a vector register the compiler cannot see into, so what is computed
+// from it cannot be hoisted above this point. The tests' CPU emulator of these kernels (which
+// defines PIE_HOST_EMULATION) has no registers to name and gives the identity.
+#ifdef PIE_HOST_EMULATION
+__device__ __forceinline__ void keep_s(uint32_t) {}
+__device__ __forceinline__ int opaque_v(int x) { return x; }
+#else
+__device__ __forceinline__ void keep_s(uint32_t x) { asm volatile("" ::"s"(x)); }
+__device__ __forceinline__ int opaque_v(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+#endif
+
+// Kernel arguments sit in memory that the scalar cache fetches on first use, one 64-byte line at
+// a time, and the compiler loads each field where it is first needed, often behind a branch that
+// waits for an earlier field: for a large argument block that is a chain of cache-miss round
+// trips before the first load of real data. Touching one dword of every line of the block at
+// kernel entry requests all of its lines at once (one round trip); later field loads hit.
+// Bytes: the leading part of the block that scalar loads read (large arrays read by vector loads
+// go last in the argument structs and are left out).
+template <int Bytes, typename T>
+__device__ __forceinline__ void prefetch_kernarg(const T& args) {
+  static_assert(Bytes > 0 && Bytes <= (int)sizeof(T), "prefetch within the argument block");
+  constexpr int kLines = (Bytes + 63) / 64;
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(&args);
+  uint32_t x = 0;
+#pragma unroll
+  for (int i = 0; i < kLines; ++i) x ^= p[16 * i];
+  keep_s(x);
+}
+
 // Unsigned 32-bit division by a runtime-constant divisor with a host-computed multiplier
 // (round-up method: q = (mulhi(n, m) + n) >> l with l = ceil(log2 d),
 // m = floor(2^32 (2^l - d) / d) + 1); exact for every 32-bit n.

@@ -124,14 +124,16 @@ __device__ __forceinline__ void gather_add_norm_block(const GatherNormArgs& a, i
 }
 
 struct GroupArgs {
-  QkNormArgs qk;
   GatherNormArgs nm;
   SiluArgs act;
   int32_t qk_blocks, nm_blocks, act_blocks, act_gelu;
+  QkNormArgs qk;  // last: its inverse-frequency array ends the block
 };
+constexpr int kGroupScalarBytes = (int)offsetof(GroupArgs, qk) + kQkScalarBytes;
 
 template <int NJ, int AU>
 __global__ __launch_bounds__(256) void decode_group_kernel(GroupArgs g) {
+  prefetch_kernarg<kGroupScalarBytes>(g);
   int b = blockIdx.x;  // block-uniform dispatch: every branch below is taken by whole blocks
   if (b < g.qk_blocks) {
     qk_norm_rope_append_block(g.qk, b);

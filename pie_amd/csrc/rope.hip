@@ -193,6 +193,7 @@ __global__ __launch_bounds__(256) void rope_append_vec(RopeAppendArgs a) {
 }
 
 __global__ __launch_bounds__(1024) void qk_norm_rope_append_d128(QkNormArgs qa) {
+  prefetch_kernarg<kQkScalarBytes>(qa);
   qk_norm_rope_append_block(qa, blockIdx.x);
 }
 

@@ -35,12 +35,13 @@ struct RopeAppendArgs {
   int64_t T;
   int32_t wpt;         // waves per token (vector kernel)
   int32_t interleave;  // pair layout (scalar kernel)
-  float inv_freq[kMaxPairs];
   // Precomputed table instead of inv_freq (flashinfer's apply_rope_with_cos_sin_cache_inplace):
   // row p holds cos(angle_i) at [i] and sin(angle_i) at [rd/2 + i]; positions outside
   // [0, cs_rows) rotate by the identity.
   const float* cs;
   int64_t cs_rows, cs_ld;
+  // last: read by vector loads, so the scalar fields above fit in the first few cache lines
+  float inv_freq[kMaxPairs];
 };
 
 // (cos, sin) of the angle p * f for position p and frequency f, by the hardware sine / cosine,
@@ -98,30 +99,73 @@ __device__ __forceinline__ int64_t slot_offset(const CacheDesc& c, int64_t t) {
 // same instruction sequence (stores are predicated), so the DPP exchanges never sit in
 // divergent code.
 struct QkNormArgs {
-  RopeAppendArgs r;  // q/k/v inputs, cache, pos, T, wpt, inv_freq
   uint16_t* q_out;
   uint16_t* k_out;
   int64_t qo_ts, qo_hs, ko_ts, ko_hs;
   const uint16_t* qw;
   const uint16_t* kw;
   float eps;
+  RopeAppendArgs r;  // q/k/v inputs, cache, pos, T, wpt, inv_freq (last, see RopeAppendArgs)
 };
+// Bytes of a QkNormArgs before its inverse-frequency array (the scalar part).
+constexpr int kQkScalarBytes = (int)(offsetof(QkNormArgs, r) + offsetof(RopeAppendArgs, inv_freq));
 
 __device__ __forceinline__ uint32_t dpp_ror8(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
 }
 
+// The page lookup of slot_offset in two steps, so the loads that do not depend on each other are
+// all in flight before anything waits: issue() requests the token's batch index and position
+// together with the page range of request t, on the guess b == t (a decode batch: token t is
+// request t's one new token); resolve() checks the guess (loading the range again when it was
+// wrong) and requests the page id. Same result as slot_offset.
+struct SlotLookup {
+  int b, p, lo, hi;
+};
+__device__ __forceinline__ SlotLookup slot_issue(const CacheDesc& c, int64_t t) {
+  SlotLookup s{-1, -1, 0, 0};
+  if (c.batch_size <= 0) return s;
+  const int64_t ts = t < c.batch_size ? t : c.batch_size - 1;
+  s.b = c.batch_indices[t];
+  s.p = c.positions[t];
+  s.lo = c.kv_indptr[ts];
+  s.hi = c.kv_indptr[ts + 1];
+  return s;
+}
+// Returns the element offset of the slot (or -1 when the token is skipped); *page receives the
+// page id load, still in flight, for slot_finish.
+__device__ __forceinline__ int64_t slot_resolve(const CacheDesc& c, int64_t t, SlotLookup s, int* page) {
+  *page = -1;
+  if (s.b < 0 || (int64_t)s.b >= c.batch_size || s.p < 0) return -1;
+  const int64_t ts = t < c.batch_size ? t : c.batch_size - 1;
+  if (s.b != ts) {
+    s.lo = c.kv_indptr[s.b];
+    s.hi = c.kv_indptr[s.b + 1];
+  }
+  const int64_t logical = (int64_t)s.lo + s.p / c.page_size;
+  if (logical >= s.hi) return -1;
+  *page = c.kv_indices[logical];
+  return (int64_t)(s.p % c.page_size) * c.slot_stride;
+}
+// The cache offset once the page id has landed: -1 for a page outside the pool.
+__device__ __forceinline__ int64_t slot_finish(const CacheDesc& c, int64_t slot_off, int page) {
+  if (slot_off < 0 || page < 0 || (int64_t)page >= c.num_pages) return -1;
+  return (int64_t)page * c.page_stride + slot_off;
+}
+
 // Work of block `bid` (threadIdx.x as in a launch of blockDim.x = max(64 wpt, 256) threads).
+// Every wave works alone (no LDS, no barrier): each lane evaluates the cos/sin of its own 8
+// pairs, so nothing waits for the page lookup except the cache stores, and the q/k outputs are
+// stored as soon as the rows have landed.
 __device__ __forceinline__ void qk_norm_rope_append_block(const QkNormArgs& qa, int bid) {
   const RopeAppendArgs& a = qa.r;
-  __shared__ float2 tab[4][64];
   const int wpt = a.wpt;                 // 1, 2, 4 (256-thread blocks) or up to 16 (one token)
   const int tpb = wpt >= 4 ? 1 : 4 / wpt;
   const int slot = (threadIdx.x >> 6) / wpt;
   const int gt = threadIdx.x - slot * wpt * 64;
   const int gsize = wpt * 64;
   const int64_t t = (int64_t)bid * tpb + slot;
-  const bool live = t < a.T;
+  if (t >= a.T) return;  // whole token groups (waves) leave together
   const HeadsDesc& h = a.h;
 
   const int sub = gt & 15;            // lane within the head row
@@ -129,15 +173,11 @@ __device__ __forceinline__ void qk_norm_rope_append_block(const QkNormArgs& qa, 
   const bool is_x = sub < 8;          // holds the x half (dims < 64) of its pairs
   const int sg = gt >> 4, nsg = gsize >> 4;
   const int nrows = h.Hq + 2 * h.Hkv;  // q heads, k heads, v heads
-  // Wave-uniform token index (clamped for the padding slot of the last block): the per-token
-  // position and page lookup become scalar loads, which complete on their own counter instead
-  // of behind the vector data loads.
-  const int64_t tq = uniform((int)(live ? t : 0));
+  // Wave-uniform token index: the per-token position and page lookup run on scalar loads,
+  // which complete on their own counter instead of behind the vector data loads.
+  const int64_t tq = uniform((int)t);
 
-  // Latency order: position and the first batch of rows are requested before the page
-  // lookup chain and the cos/sin table, which then overlap the loads in flight.
   constexpr int UB = 4;  // head rows per 16-lane group per batch
-  const int p = a.pos[tq];
   struct Batch {
     uint4 X[UB], Wt[UB];
     int kind[UB], hd[UB];  // kind: 0 q, 1 k, 2 v, 3 none
@@ -159,22 +199,28 @@ __device__ __forceinline__ void qk_norm_rope_append_block(const QkNormArgs& qa, 
                           : kd == 2 ? vrow + (int64_t)hh * h.v_hs
                           : kd == 0 ? qrow + (int64_t)hh * h.q_hs
                                     : (h.Hq > 0 ? qrow : krow);
-      b.kind[i] = live ? kd : 3;
+      b.kind[i] = kd;
       b.hd[i] = hh;
       b.X[i] = ld_nt(src + sub * 8);
       b.Wt[i] = ld16((kd == 1 || h.Hq == 0 ? qa.kw : qa.qw) + sub * 8);
     }
     return b;
   };
-  // this lane's frequency is requested before the rows: vector loads complete in order, so a
-  // frequency requested after them would hold the table until every row had landed
-  const float f0 = (live && gt < 64) ? a.inv_freq[gt] : 0.f;
+  // Latency order: every load that does not wait for another goes out first: the position and
+  // the first step of the page lookup (scalar loads), this lane's 8 frequencies and the first
+  // batch of rows (vector loads). Then the page id is requested; only the cache stores wait for
+  // it (the q/k outputs are stored as soon as the rows have landed).
+  const int p = a.pos[tq];
+  const SlotLookup sl = slot_issue(a.c, tq);
+  float fq[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) fq[e] = a.inv_freq[lo * 8 + e];
   Batch b = load_batch(sg);
-  const int64_t kc = live ? slot_offset(a.c, tq) : -1;
-  if (live && gt < 64) tab[slot][gt] = rope_pos_cs(p, f0);
-  __syncthreads();
-  if (!live) return;  // whole token groups (waves) leave together
-  const float2* tb = tab[slot] + lo * 8;
+  int page;
+  const int64_t soff = slot_resolve(a.c, tq, sl, &page);
+  float2 tb[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) tb[e] = rope_pos_cs(p, fq[e]);
 
   // uniform trip count over the wave: all 64 lanes execute every DPP exchange
   const int nbatch = (nrows + nsg * UB - 1) / (nsg * UB);
@@ -206,11 +252,13 @@ __device__ __forceinline__ void qk_norm_rope_append_block(const QkNormArgs& qa, 
       const uint4 o = pack8(own);
       if (kind[i] == 0) {
         st16(qa.q_out + tq * qa.qo_ts + (int64_t)hd[i] * qa.qo_hs + sub * 8, o);
-      } else if (kind[i] == 1) {
-        st16(qa.k_out + tq * qa.ko_ts + (int64_t)hd[i] * qa.ko_hs + sub * 8, o);
-        if (kc >= 0) st_nt(a.c.k_cache + kc + (int64_t)hd[i] * a.c.head_stride + sub * 8, o);
-      } else if (kind[i] == 2 && kc >= 0) {
-        st_nt(a.c.v_cache + kc + (int64_t)hd[i] * a.c.head_stride + sub * 8, X[i]);
+      } else {
+        if (kind[i] == 1) st16(qa.k_out + tq * qa.ko_ts + (int64_t)hd[i] * qa.ko_hs + sub * 8, o);
+        // the page id is first needed here; opaque_v keeps its wait (and the offset) from being
+        // hoisted ahead of the q stores
+        const int64_t kc = slot_finish(a.c, soff, opaque_v(page));
+        if (kind[i] == 1 && kc >= 0) st_nt(a.c.k_cache + kc + (int64_t)hd[i] * a.c.head_stride + sub * 8, o);
+        if (kind[i] == 2 && kc >= 0) st_nt(a.c.v_cache + kc + (int64_t)hd[i] * a.c.head_stride + sub * 8, X[i]);
       }
     }
   }

@@ -30,6 +30,8 @@ struct float4 { float x, y, z, w; };
 inline uint4 make_uint4(unsigned a, unsigned b, unsigned c, unsigned d) { return uint4{a, b, c, d}; }
 inline float2 make_float2(float a, float b) { return float2{a, b}; }
 
+#define PIE_HOST_EMULATION 1  // the kernels' compiler-only register fences become identities
+
 typedef void* hipStream_t;
 typedef int hipError_t;
 enum { hipSuccess = 0 };
