@@ -19,7 +19,10 @@
 // in vocabulary order, and the radix selects and the draw run over that short list. top_k with a
 // small k over a long row needs one read: the k-th largest of the row's first 8192 entries is
 // already a floor, so the list is built in the same pass that counts the row's p > 0. Plain
-// sampling, and rows whose list would not fit, take the direct passes over the row.
+// sampling, and rows whose list would not fit, take the direct passes over the row. top_p runs
+// in its own kernel instantiation: a histogram pass (mass per eighth of a binade of the key)
+// finds the bin holding the threshold, one gather collects every key from that bin up (or, for
+// large kept sets, the bin's keys alone), and a radix search inside the bin gives the threshold.
 // Draw: inverse CDF in index order over the kept tokens, target u * kept mass, with u from
 // Philox4x32-10 (counter = (offset, row), key = seed) or caller-given uniforms; the kept-mass
 // pass sums chunks of the row so that only the chunk holding the target is scanned.
@@ -105,26 +108,55 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, SampleShared& sh) 
   return t;
 }
 
-// Visits every element of the row as (index, value); 16-byte loads where the row allows.
+// Visits every element of the row as (index, value); 16-byte loads where the row allows. The row
+// goes in batches of kRowU vectors per thread, two batches in flight: the next batch's loads are
+// issued before the current one is used (two register buffers in turn, no copies, which would
+// wait for the younger loads), so a thread keeps 2 kRowU 16-byte loads outstanding.
+constexpr int kRowU = 2;  // 2 measured faster than 4 (more registers, slower passes)
 template <typename F>
 __device__ __forceinline__ void for_row(const float* p, int V, bool vec, F&& f) {
   if (vec) {
-    // four 16-byte loads in flight per thread before any is used
     const int nv = V >> 2;
-    int i = threadIdx.x;
-    for (; i + 3 * kSampThreads < nv; i += 4 * kSampThreads) {
-      float4 x[4];
+    constexpr int S = kRowU * kSampThreads;  // vectors per batch
+    const int nb = nv / S;                   // full batches (no bounds tests)
+    auto load = [&](float4 (&d)[kRowU], int at) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) x[k] = *reinterpret_cast<const float4*>(p + 4 * (i + k * kSampThreads));
+      for (int k = 0; k < kRowU; ++k) d[k] = *reinterpret_cast<const float4*>(p + 4 * (at + threadIdx.x + k * kSampThreads));
+    };
+    auto use = [&](const float4 (&d)[kRowU], int at) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int j = 4 * (i + k * kSampThreads);
-        f(j, x[k].x); f(j + 1, x[k].y); f(j + 2, x[k].z); f(j + 3, x[k].w);
+      for (int k = 0; k < kRowU; ++k) {
+        const int j = 4 * (at + threadIdx.x + k * kSampThreads);
+        f(j, d[k].x); f(j + 1, d[k].y); f(j + 2, d[k].z); f(j + 3, d[k].w);
+      }
+    };
+    if (nb > 0) {
+      float4 x[kRowU], y[kRowU];
+      load(x, 0);
+      if (nb > 1) load(y, S);
+      for (int bi = 0;;) {
+        use(x, bi * S);
+        if (bi + 2 < nb) load(x, (bi + 2) * S);
+        if (++bi >= nb) break;
+        use(y, bi * S);
+        if (bi + 2 < nb) load(y, (bi + 2) * S);
+        if (++bi >= nb) break;
       }
     }
-    for (; i < nv; i += kSampThreads) {
-      const float4 x = *reinterpret_cast<const float4*>(p + 4 * i);
-      f(4 * i, x.x); f(4 * i + 1, x.y); f(4 * i + 2, x.z); f(4 * i + 3, x.w);
+    // the last partial batch: every load issued before any is used
+    {
+      const int at = nb * S;
+      float4 d[kRowU];
+#pragma unroll
+      for (int k = 0; k < kRowU; ++k) {
+        const int v = min(at + (int)threadIdx.x + k * kSampThreads, nv - 1);
+        if (nv > 0) d[k] = *reinterpret_cast<const float4*>(p + 4 * v);
+      }
+#pragma unroll
+      for (int k = 0; k < kRowU; ++k) {
+        const int v = at + threadIdx.x + k * kSampThreads;
+        if (v < nv) { f(4 * v, d[k].x); f(4 * v + 1, d[k].y); f(4 * v + 2, d[k].z); f(4 * v + 3, d[k].w); }
+      }
     }
     for (int i = 4 * nv + threadIdx.x; i < V; i += kSampThreads) f(i, p[i]);
   } else {
@@ -137,12 +169,15 @@ __device__ __forceinline__ void for_row(const float* p, int V, bool vec, F&& f) 
 // by_mass = true: the smallest key v such that the mass of keys strictly above v is below thr
 // (top-p threshold; the maximal key when thr <= 0); 0 if no key >= lo exists. Each pass counts
 // the digits of the keys under the current prefix; wave 0 then scans the 256 digits from the top
-// (4 per lane) to pick the next one.
+// (4 per lane) to pick the next one. prefix0 / pmask0 / shift0: the search starts inside the
+// bucket of keys k with (k & pmask0) == prefix0 (every key the caller passes lies in it), at the
+// 8-bit digit that starts at bit shift0; the last digit (shift 0) may overlap bits already fixed.
 __device__ uint32_t radix_threshold(const float* p, int V, bool vec, uint32_t lo, bool by_mass,
-                                    uint32_t need, double thr, SampleShared& sh) {
-  uint32_t prefix = 0, pmask = 0;
+                                    uint32_t need, double thr, SampleShared& sh, uint32_t prefix0 = 0u,
+                                    uint32_t pmask0 = 0u, int shift0 = 24) {
+  uint32_t prefix = prefix0, pmask = pmask0;
   uint64_t above = 0;  // mass of keys above the current prefix bucket (by_mass)
-  for (int shift = 24; shift >= 0; shift -= 8) {
+  for (int shift = shift0;; shift = shift > 8 ? shift - 8 : 0) {
     for (int i = threadIdx.x; i < 256; i += kSampThreads) { sh.cnt[i] = 0; sh.mass[i] = 0; }
     if (threadIdx.x == 0) sh.u32a = 0xffffffffu;
     __syncthreads();
@@ -222,6 +257,7 @@ __device__ uint32_t radix_threshold(const float* p, int V, bool vec, uint32_t lo
     if (by_mass) above = sh.u64a;
     pmask |= 255u << shift;
     __syncthreads();
+    if (shift == 0) break;
   }
   return prefix;
 }
@@ -382,19 +418,23 @@ __device__ uint32_t list_threshold(const float* p, int n, const SampleArgs& a, i
 // candidate list, ascending in vocabulary index). npos: the row's count of p > 0 (-1: count it
 // here over p). row_tot: the row's total mass for top_p (0: sum it here over p). Candidate lists
 // hold every element at or above the threshold being searched, so the counts and masses that
-// decide it are the same as over the whole row.
+// decide it are the same as over the whole row. lo_given > 0: the kept keys' lower bound is
+// already known (top_p resolved from the row's histogram): no threshold search here.
 __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, int V, bool vec,
                                            const SampleArgs& a, int r, int64_t npos, uint64_t row_tot,
-                                           SampleShared& sh, uint32_t* list_buf = nullptr) {
+                                           SampleShared& sh, uint32_t* list_buf = nullptr,
+                                           uint32_t lo_given = 0u) {
   if (V == 0) {  // nothing to draw from (an empty candidate list)
     if (threadIdx.x == 0) a.out[r] = -1;
     return;
   }
 
   // lower bound on kept keys (1 = every p > 0)
-  uint32_t lo = 1u;
-  const bool short_list = list_buf && idx && V <= kSampThreads && a.mode != 3;
-  if (short_list) {
+  uint32_t lo = lo_given ? lo_given : 1u;
+  const bool given = lo_given != 0u;
+  const bool short_list = !given && list_buf && idx && V <= kSampThreads && a.mode != 3;
+  if (given) {
+  } else if (short_list) {
     lo = list_threshold(p, V, a, r, npos, row_tot, sh, list_buf);
   } else if (a.mode == 2 || a.mode == 4) {
     const int32_t k = a.top_k ? a.top_k[r] : a.top_k_s;
@@ -407,7 +447,7 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
       if ((int64_t)k < npos) lo = max(1u, radix_threshold(p, V, vec, 1u, false, (uint32_t)k, 0.0, sh));
     }
   }
-  if (!short_list && (a.mode == 1 || a.mode == 4)) {
+  if (!given && !short_list && (a.mode == 1 || a.mode == 4)) {
     const float tp = a.top_p ? a.top_p[r] : a.top_p_s;
     uint64_t tot = 0;
     if (a.mode == 1 && row_tot) {
@@ -451,21 +491,62 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
   };
   int last = -1;
   uint64_t acc = 0;
-  for (int t0 = 0; t0 < ntiles; t0 += 4) {  // four 16-byte loads in flight
-    float x[4][4];
+  auto visit = [&](int i, float x) {
+    const uint64_t m = kept_mass(x);
+    acc += m;
+    if (m) last = max(last, i);
+  };
+  auto chunk_done = [&](int t) {  // this wave's share of tile t is in acc
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (t0 + u < ntiles) load4((t0 + u) * kTile + 4 * threadIdx.x, x[u]);
+    for (int o = 32; o >= 1; o >>= 1) acc += shfl_u64(acc, lane ^ o);
+    if (lane == 0 && acc) atomicAdd((unsigned long long*)&sh.mass[t / tpc], (unsigned long long)acc);
+    acc = 0;
+  };
+  if (vec) {
+    // Wave w takes whole tiles w, w + 16, ...: a tile is 1024 16-byte vectors, 16 per lane, read
+    // as four quarters of 4 loads with the next quarter's loads issued before the current quarter
+    // is used, and its mass is reduced once per wave and tile.
+    const int nv = V >> 2;
+    constexpr int kQuarter = kTile / 16;  // vectors per quarter tile
+    // (loads past the last vector re-read it, unused: every load is issued unconditionally)
+    const int nh = w < ntiles && nv > 0 ? 4 * ((ntiles - w + kSampWaves - 1) / kSampWaves) : 0;
+    auto hbase = [&](int h) { return (w + kSampWaves * (h >> 2)) * (kTile / 4) + (h & 3) * kQuarter; };
+    auto load = [&](float4 (&d)[4], int h) {
+      const int v0 = hbase(h) + lane;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int t = t0 + u;
-      if (t >= ntiles) break;
-      const int i0 = t * kTile + 4 * threadIdx.x;
+      for (int k = 0; k < 4; ++k) d[k] = *reinterpret_cast<const float4*>(p + 4 * min(v0 + 64 * k, nv - 1));
+    };
+    auto use = [&](const float4 (&d)[4], int h) {
+      const int v0 = hbase(h) + lane;
 #pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int v = v0 + 64 * k;
+        if (v < nv) { visit(4 * v, d[k].x); visit(4 * v + 1, d[k].y); visit(4 * v + 2, d[k].z); visit(4 * v + 3, d[k].w); }
+      }
+      if ((h & 3) == 3) chunk_done(w + kSampWaves * (h >> 2));
+    };
+    if (nh > 0) {
+      float4 x[4], y[4];
+      load(x, 0);
+      load(y, 1);
+      for (int h = 0;;) {
+        use(x, h);
+        if (h + 2 < nh) load(x, h + 2);
+        if (++h >= nh) break;
+        use(y, h);
+        if (h + 2 < nh) load(y, h + 2);
+        if (++h >= nh) break;
+      }
+    }
+    if (4 * nv < V && w == (ntiles - 1) % kSampWaves) {  // the last < 4 elements, in the last tile
+      if (lane < V - 4 * nv) visit(4 * nv + lane, p[4 * nv + lane]);
+      chunk_done(ntiles - 1);
+    }
+  } else {
+    for (int t = 0; t < ntiles; ++t) {
       for (int e = 0; e < 4; ++e) {
-        const uint64_t m = kept_mass(x[u][e]);
-        acc += m;
-        if (m) last = max(last, i0 + e);
+        const int i = t * kTile + 4 * threadIdx.x + e;
+        if (i < V) visit(i, p[i]);
       }
       if ((t + 1) % tpc == 0 || t == ntiles - 1) {  // chunk t / tpc ends here
 #pragma unroll
@@ -616,6 +697,19 @@ __device__ __forceinline__ uint64_t thread_tops(const float* p, int V, bool vec,
 
 // Appends this wave's candidates (pred(i, x)) to val/idx[w * kWaveCands ...] in index order and
 // returns their count (which may exceed kWaveCands; only the first kWaveCands are stored).
+// Which elements a candidate list keeps: kind 0 key >= lo; 1 p > 0 and x >= mthr (min_p);
+// 2 keys in bin `bin` of the top_p histogram. count_pos: also count the p > 0 seen.
+struct ListPred {
+  int kind;
+  uint32_t lo;
+  uint32_t bin;
+  double mthr;
+  __device__ __forceinline__ bool operator()(int, float x) const {
+    const uint32_t key = prob_key(x);
+    return kind == 0 ? key >= lo : kind == 1 ? (key != 0u && (double)x >= mthr) : (key >> 20) == bin;
+  }
+};
+
 template <typename P>
 __device__ int compact_segment(const float* p, int V, bool vec, P&& pred, CandShared& cs) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -709,6 +803,161 @@ __device__ int compact_segment(const float* p, int V, bool vec, P&& pred, CandSh
   return n;
 }
 
+// top_p over rows whose kept set is too large for the two-read candidate path: a histogram of the
+// row's mass by the top 11 bits of the key (sign 0, exponent, 3 mantissa bits: 2048 bins, each an
+// eighth of a binade) locates the bin holding the threshold in one pass; then either every key
+// from that bin up is gathered (when they fit), or only that bin's keys, whose radix search over
+// the 20 remaining bits gives the exact threshold. Bins spread the LDS atomics over many
+// addresses (an 8-bit first radix digit puts nearly every key of a row in a handful of bins).
+constexpr int kBinShift = 20, kBins = 2048;
+struct HistShared {
+  uint32_t cnt[kBins];
+  uint64_t mass[kBins];
+  uint64_t above;    // mass of the keys in bins above the selected one
+  uint32_t bin;      // the selected bin (0xffffffff: the row has no p > 0)
+  uint32_t n_ge;     // keys in bins >= the selected one
+  uint32_t n_bin;    // keys in the selected bin
+};
+
+// The bin holding the top_p threshold for thr = top_p * row mass: the lowest non-empty bin whose
+// mass above it (the bins above) is below thr, or the highest non-empty bin when none is (thr <=
+// 0: the threshold is the maximal key). Wave 0 scans 32 bins per lane from the top.
+__device__ void select_bin(double thr, HistShared& hs) {
+  if (threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
+  uint64_t lm = 0;
+  uint32_t lc = 0;
+#pragma unroll 4
+  for (int e = 0; e < 32; ++e) {
+    const int d = kBins - 1 - 32 * lane - e;
+    lm += hs.mass[d];
+    lc += hs.cnt[d];
+  }
+  uint64_t im = lm;
+  uint32_t ic = lc;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t ym = shfl_u64(im, lane >= o ? lane - o : lane);
+    const uint32_t yc = (uint32_t)__builtin_amdgcn_ds_bpermute((lane >= o ? lane - o : lane) << 2, (int)ic);
+    if (lane >= o) { im += ym; ic += yc; }
+  }
+  // this lane's lowest qualifying bin and its highest non-empty bin
+  uint64_t a = im - lm;
+  int low = kBins, high = -1;
+#pragma unroll 4
+  for (int e = 0; e < 32; ++e) {
+    const int d = kBins - 1 - 32 * lane - e;
+    if (hs.cnt[d]) {
+      if ((double)a < thr) low = d;
+      high = max(high, d);
+    }
+    a += hs.mass[d];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    low = min(low, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, low));
+    high = max(high, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, high));
+  }
+  const int dsel = low < kBins ? low : high;
+  if (dsel < 0) {
+    if (lane == 0) hs.bin = 0xffffffffu;
+    return;
+  }
+  if ((kBins - 1 - dsel) / 32 == lane) {  // the owner records the mass and counts above dsel
+    uint64_t ma = im - lm;
+    uint32_t ca = ic - lc;
+  #pragma unroll 4
+  for (int e = 0; e < 32; ++e) {
+      const int d = kBins - 1 - 32 * lane - e;
+      if (d == dsel) break;
+      ma += hs.mass[d];
+      ca += hs.cnt[d];
+    }
+    hs.bin = (uint32_t)dsel;
+    hs.above = ma;
+    hs.n_ge = ca + hs.cnt[dsel];
+    hs.n_bin = hs.cnt[dsel];
+  }
+}
+
+// Copies the elements that satisfy pred into cs.val / cs.idx in vocabulary order (each wave its
+// own segment, then the gaps between the segments' lists closed); *total = the list's length.
+// npos (optional): the row's count of p > 0, counted on the way. False when some segment
+// overflowed (the list is then unusable).
+__device__ __forceinline__ bool gather_list(const float* p, int V, bool vec, const ListPred& pred, CandShared& cs,
+                                         int* total_out, uint32_t* npos) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint32_t c = 0;
+  const int n = compact_segment(p, V, vec, [&](int i, float x) {
+    c += prob_key(x) != 0u;
+    return pred(i, x);
+  }, cs);
+  if (lane == 0) cs.wn[w] = n;
+  __syncthreads();
+  if (npos) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) c += (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ o) << 2, (int)c);
+    __shared__ uint32_t wc[kSampWaves];
+    if (lane == 0) wc[w] = c;
+    __syncthreads();
+    uint32_t t = 0;
+    for (int i = 0; i < kSampWaves; ++i) t += wc[i];
+    *npos = t;
+  }
+  int total = 0;
+  bool over = false;
+  for (int i = 0; i < kSampWaves; ++i) {
+    over |= cs.wn[i] > kWaveCands;
+    total += cs.wn[i];
+  }
+  if (over) return false;
+  // close the gaps between the segments' lists (moves go to lower slots: read, then write)
+  constexpr int J = kCands / kSampThreads;
+  float mv[J];
+  uint32_t mi[J];
+  int md[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int s = threadIdx.x + j * kSampThreads;
+    const int sw = s / kWaveCands, so = s % kWaveCands;
+    int base = 0;
+    for (int i = 0; i < sw; ++i) base += cs.wn[i];
+    md[j] = so < cs.wn[sw] ? base + so : -1;
+    mv[j] = cs.val[s];
+    mi[j] = cs.idx[s];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    if (md[j] >= 0) { cs.val[md[j]] = mv[j]; cs.idx[md[j]] = mi[j]; }
+  *total_out = total;
+  return true;
+}
+
+// The histogram pass: every bin's count and mass, the row's count of p > 0 and its mass.
+__device__ __forceinline__ void hist_pass(const float* p, int V, bool vec, HistShared& hs, SampleShared& sh,
+                                       int64_t* npos, uint64_t* row_tot) {
+  for (int i = threadIdx.x; i < kBins; i += kSampThreads) { hs.cnt[i] = 0u; hs.mass[i] = 0ull; }
+  __syncthreads();
+  uint32_t c = 0;
+  uint64_t m = 0;
+  for_row(p, V, vec, [&](int, float x) {
+    const uint32_t key = prob_key(x);
+    if (key) {
+      const uint64_t pm = prob_mass(x);
+      ++c;
+      m += pm;
+      atomicAdd(&hs.cnt[key >> kBinShift], 1u);
+      atomicAdd((unsigned long long*)&hs.mass[key >> kBinShift], (unsigned long long)pm);
+    }
+  });
+  *npos = (int64_t)block_sum_u64(c, sh);
+  *row_tot = block_sum_u64(m, sh);
+}
+
+// kTopP: the top_p instantiation (mode 1 only, the histogram path); the other serves modes 0, 2-4.
+// Two kernels, so each gets the registers its own paths need.
+template <bool kTopP>
 __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
   __shared__ SampleShared sh;
   __shared__ CandShared cs;
@@ -721,7 +970,7 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
   const float* p = a.probs + (int64_t)src * a.stride;
   const int V = a.V;
   const bool vec = a.vec != 0;
-  const int mode = a.mode;
+  const int mode = kTopP ? 1 : a.mode;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int32_t k = (mode == 2 || mode == 4) ? (a.top_k ? a.top_k[r] : a.top_k_s) : 0;
   // what the selection runs over: the row (direct passes) or its candidate list
@@ -731,38 +980,11 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
   bool svec = vec;
   int64_t npos = -1;
   uint64_t row_tot = 0;
-  // Copies the elements that satisfy pred into the candidate list and closes the gaps between
-  // the wave segments; false (and the list unused) when some segment overflowed.
-  auto gather = [&](auto&& pred) -> bool {
-    const int n = compact_segment(p, V, vec, pred, cs);
-    if (lane == 0) cs.wn[w] = n;
-    __syncthreads();
-    int total = 0;
-    bool over = false;
-    for (int i = 0; i < kSampWaves; ++i) {
-      over |= cs.wn[i] > kWaveCands;
-      total += cs.wn[i];
-    }
-    if (over) return false;
-    // close the gaps between the segments' lists (moves go to lower slots: read, then write)
-    constexpr int J = kCands / kSampThreads;
-    float mv[J];
-    uint32_t mi[J];
-    int md[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int s = threadIdx.x + j * kSampThreads;
-      const int sw = s / kWaveCands, so = s % kWaveCands;
-      int base = 0;
-      for (int i = 0; i < sw; ++i) base += cs.wn[i];
-      md[j] = so < cs.wn[sw] ? base + so : -1;
-      mv[j] = cs.val[s];
-      mi[j] = cs.idx[s];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-      if (md[j] >= 0) { cs.val[md[j]] = mv[j]; cs.idx[md[j]] = mi[j]; }
+  // Copies the elements that satisfy pred into the candidate list (gather_list) and points the
+  // selection at it; false (and the list unused) when some segment overflowed.
+  auto gather = [&](const ListPred& pred, uint32_t* npos_out = nullptr) -> bool {
+    int total;
+    if (!gather_list(p, V, vec, pred, cs, &total, npos_out)) return false;
     sp = cs.val;
     sidx = cs.idx;
     sV = total;
@@ -770,11 +992,49 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
     return true;
   };
   bool listed = false;
+  uint32_t lo_given = 0u;
+  if constexpr (kTopP) {
+    __shared__ HistShared hs;
+    // top_p: the histogram pass (with the row's count of p > 0 and its mass), then one gather
+    hist_pass(p, V, vec, hs, sh, &npos, &row_tot);
+    const double thr = (double)(a.top_p ? a.top_p[r] : a.top_p_s) * (double)row_tot;
+    select_bin(thr, hs);
+    __syncthreads();
+    const uint32_t bin = hs.bin;
+    if (bin != 0xffffffffu) {
+      const uint32_t bin_lo = bin << kBinShift;
+      // one gather: every key from the threshold's bin up when they fit (the draw then runs over
+      // the list), else the bin's keys alone (their radix search gives the threshold); one call
+      // site, so the list code is inlined once
+      bool got = false;
+      int attempt = hs.n_ge <= (uint32_t)kCands ? 0 : 1;
+      for (; attempt < 2 && !got; ++attempt) {
+        if (attempt == 1 && hs.n_bin > (uint32_t)kCands) break;
+        __syncthreads();
+        got = gather(attempt == 0 ? ListPred{0, bin_lo, 0u, 0.0} : ListPred{2, 0u, bin, 0.0});
+      }
+      listed = got && attempt == 1;  // the loop's increment ran once after the first success
+      // the threshold: a radix search inside the bin (keys of other bins are skipped), over the
+      // list (every key from the bin up, or the bin's keys) or, when neither fit, over the row
+      const double thr_in = thr - (double)hs.above;  // the bin's share of the threshold
+      __syncthreads();
+      lo_given = radix_threshold(got ? cs.val : p, got ? sV : V, got || vec, 1u, true, 0u, thr_in, sh, bin_lo,
+                                 ~((1u << kBinShift) - 1u), kBinShift - 8);
+      lo_given = max(lo_given, 1u);
+      if (!listed) {  // the draw runs over the row
+        sp = p;
+        sidx = nullptr;
+        sV = V;
+        svec = vec;
+      }
+    }
+    __syncthreads();
+  }
   // One read for top_k (alone or before top_p) with a small k over a long row: the k-th largest
   // of the row's first kHeadElems elements is a floor under the row's k-th largest, so one pass
   // collects every element at or above it (about k * V / kHeadElems of them for exchangeable
   // rows) and counts the row's p > 0 on the way. Overflow falls back to the two passes below.
-  if ((mode == 2 || mode == 4) && vec && k > 0 && k <= kOnePassMaxK && V >= kOnePassMinV) {
+  if (!kTopP && (mode == 2 || mode == 4) && vec && k > 0 && k <= kOnePassMaxK && V >= kOnePassMinV) {
     // the floor: the k-th largest of the threads' maxima over their kHeadElems / kSampThreads
     // head elements (a subset of the head, so at most the head's k-th largest; the head's
     // largest keys are nearly always their thread's maximum, so it is about as tight), from a
@@ -795,17 +1055,14 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
     __syncthreads();  // the sort buffer is dead from here: its memory holds the candidates
     if (floor0 > 1u) {
       uint32_t c = 0;
-      listed = gather([&](int, float x) {
-        const uint32_t key = prob_key(x);
-        c += key != 0u;
-        return key >= floor0;
-      });
-      npos = (int64_t)block_sum_u64(c, sh);
+      listed = gather(ListPred{0, floor0, 0u, 0.0}, &c);
+      npos = (int64_t)c;
       __syncthreads();
     }
   }
-  // plain sampling, and top_k with k outside (0, V), keep every p > 0: no candidate list
-  if (!listed && !(mode == 0 || ((mode == 2 || mode == 4) && !(k > 0 && k < V)))) {
+  // plain sampling, and top_k with k outside (0, V), keep every p > 0: no candidate list; top_p
+  // went through the histogram above
+  if (!kTopP && !listed && !(mode == 0 || ((mode == 2 || mode == 4) && !(k > 0 && k < V)))) {
     // pass A
     bool lists = true;
     uint32_t cand_lo = 1u;  // candidates: key >= cand_lo (top_k, top_p) or x >= mthr (min_p)
@@ -837,14 +1094,12 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
     }
     if (lists) {
       // pass B (with too many candidates in some segment, the direct passes run over the row)
-      gather([&](int, float x) {
-        return mode == 3 ? (prob_key(x) != 0 && (double)x >= mthr) : prob_key(x) >= cand_lo;
-      });
+      gather(mode == 3 ? ListPred{1, 0u, 0u, mthr} : ListPred{0, cand_lo, 0u, 0.0});
     }
     __syncthreads();
   }
   sample_row(sp, sidx, sV, svec, a, r, npos, row_tot, sh,
-             sidx ? reinterpret_cast<uint32_t*>(cs.val + kSampThreads) : nullptr);
+             sidx ? reinterpret_cast<uint32_t*>(cs.val + kSampThreads) : nullptr, lo_given);
 }
 
 // safe_scaled_softmax: probs = softmax(logits / T) per row, or the one-hot of the first maximum
@@ -1181,7 +1436,7 @@ extern "C" int pie_hip_sample(const float* probs, int64_t prob_stride, int64_t p
   SampleArgs a{probs, prob_stride, (int32_t)vocab, (int32_t)batch, row_indices, (int32_t)prob_rows, mode, top_k,
                top_k_scalar, top_p, top_p_scalar, min_p, min_p_scalar, uniforms, seed, offset, out,
                (prob_stride % 4 == 0 && aligned16(probs)) ? 1 : 0};
-  hipLaunchKernelGGL(sample_kernel, dim3((unsigned)batch), dim3(kSampThreads), 0,
+  hipLaunchKernelGGL(mode == 1 ? sample_kernel<true> : sample_kernel<false>, dim3((unsigned)batch), dim3(kSampThreads), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("sample");
 }

@@ -788,7 +788,10 @@ int main(int argc, char** argv) {
     case_sample(1, 10003, 4, false, true);  // candidate lists, scalar loads
     case_sample(2, 10003, 4, false, true, 1);  // 16-byte rows whose length is not a multiple of 4
     case_sample(2, 10001, 3, false, true, 3);
-    case_sample(1, 40000, 1, false);        // top_p lists that overflow: direct passes
+    case_sample(1, 40000, 1, false);        // top_p over a flat row: the threshold's histogram bin
+    case_sample(3, 70000, 1, false);        // top_p, flat rows: the bin's keys (and the ties of row 1)
+    case_sample(2, 70000, 1, false, true);  // top_p, peaked rows: every key from the bin up
+    case_sample(2, 70000, 1, false, false, 0, -69990);  // a bin of 69990 equal keys: search over the row
     // top_k over long rows: one read with a floor from the first 8192 entries (a row of ties
     // overflows the list and falls back; a head with fewer than k positives does too)
     case_sample(4, 70000, 2, false, true);

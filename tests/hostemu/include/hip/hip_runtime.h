@@ -29,6 +29,7 @@ struct float2 { float x, y; };
 struct float4 { float x, y, z, w; };
 inline uint4 make_uint4(unsigned a, unsigned b, unsigned c, unsigned d) { return uint4{a, b, c, d}; }
 inline float2 make_float2(float a, float b) { return float2{a, b}; }
+inline float4 make_float4(float a, float b, float c, float d) { return float4{a, b, c, d}; }
 
 #define PIE_HOST_EMULATION 1  // the kernels' compiler-only register fences become identities
 

@@ -67,6 +67,31 @@ def test_sample_exact_vs_oracle(dev, mode, V):
     assert kept[np.arange(B), got].all()
 
 
+@pytest.mark.parametrize("scale", [1.0, 3.0, 6.0, 0.0])
+def test_top_p_regimes_exact(dev, scale):
+    """top_p at Llama-3 vocabulary over rows whose kept sets range from 60% of the vocabulary
+    (logits N(0, 1)) to a few tokens (N(0, 6)) and all-equal rows (scale 0: one histogram bin
+    holds the whole row), with p from 0.001 (one to three tokens kept) to 0.999, exact against
+    the oracle with given uniforms; min_p near 1 and tiny top_p on the same rows (candidate lists
+    of one to three elements)."""
+    print(f"top_p regimes scale={scale}", flush=True)
+    B, V = 12, 128256
+    g = torch.Generator().manual_seed(int(scale * 10) + 5)
+    logits = torch.randn(B, V, generator=g, dtype=torch.float64) * scale
+    p = torch.softmax(logits, -1)
+    probs = (torch.floor(p * 2**30) / 2**30).float()
+    prm = _params(B, V, 90)
+    prm["top_p"] = torch.tensor([0.001, 0.01, 0.1, 0.3, 0.5, 0.7, 0.8, 0.9, 0.95, 0.99, 0.999, 1.0])
+    prm["min_p"] = torch.tensor([0.99, 0.9, 0.5, 0.3, 0.1, 0.05, 0.01, 0.001, 0.0, 0.999, 0.7, 0.2])
+    dp = {k: v.to(dev) for k, v in prm.items()}
+    for mode in ("top_p", "min_p", "top_k_top_p"):
+        got = _call(mode, probs.to(dev), dp, uniforms=dp["u"]).cpu().numpy()
+        want, kept = oracle.sample(probs.numpy(), mode, prm["u"].numpy(), top_k=prm["top_k"].numpy(),
+                                   top_p=prm["top_p"].numpy(), min_p=prm["min_p"].numpy())
+        assert (got == want).all(), f"{mode}: rows {np.nonzero(got != want)[0][:5]}: {got[got != want][:5]} vs {want[got != want][:5]}"
+        assert kept[np.arange(B), got].all()
+
+
 @pytest.mark.parametrize("mode", list(SAMPLERS))
 def test_sample_long_rows(dev, mode):
     """Rows of more than 256 tiles of 4096 (the draw's chunks then span several tiles), one with
