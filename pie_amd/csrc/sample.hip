@@ -172,7 +172,7 @@ __device__ __forceinline__ void for_row(const float* p, int V, bool vec, F&& f) 
 // (4 per lane) to pick the next one. prefix0 / pmask0 / shift0: the search starts inside the
 // bucket of keys k with (k & pmask0) == prefix0 (every key the caller passes lies in it), at the
 // 8-bit digit that starts at bit shift0; the last digit (shift 0) may overlap bits already fixed.
-__device__ uint32_t radix_threshold(const float* p, int V, bool vec, uint32_t lo, bool by_mass,
+__device__ __forceinline__ uint32_t radix_threshold(const float* p, int V, bool vec, uint32_t lo, bool by_mass,
                                     uint32_t need, double thr, SampleShared& sh, uint32_t prefix0 = 0u,
                                     uint32_t pmask0 = 0u, int shift0 = 24) {
   uint32_t prefix = prefix0, pmask = pmask0;
@@ -343,7 +343,7 @@ __device__ __forceinline__ uint32_t sort_desc_keys(uint32_t v, uint32_t* buf) {
 
 // Returns lo for the list p[0, n) (n <= kSampThreads): the smallest kept key under the row's
 // top_k / top_p (modes 1, 2, 4), as sample_row's radix selects would give it.
-__device__ uint32_t list_threshold(const float* p, int n, const SampleArgs& a, int r, int64_t npos,
+__device__ __forceinline__ uint32_t list_threshold(const float* p, int n, const SampleArgs& a, int r, int64_t npos,
                                    uint64_t row_tot, SampleShared& sh, uint32_t* buf) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   uint32_t v = t < n ? prob_key(p[t]) : 0u;
@@ -822,7 +822,7 @@ struct HistShared {
 // The bin holding the top_p threshold for thr = top_p * row mass: the lowest non-empty bin whose
 // mass above it (the bins above) is below thr, or the highest non-empty bin when none is (thr <=
 // 0: the threshold is the maximal key). Wave 0 scans 32 bins per lane from the top.
-__device__ void select_bin(double thr, HistShared& hs) {
+__device__ __forceinline__ void select_bin(double thr, HistShared& hs) {
   if (threadIdx.x >= 64) return;
   const int lane = threadIdx.x;
   uint64_t lm = 0;
