@@ -592,8 +592,22 @@ def _ops_sampling(dev, run):
     def make_sample_skew():
         pr = probs_skew.clone()
         return lambda: sampling.top_k_top_p_sampling_from_probs(pr, k, p, seed=1, offset=0)
+    mp = torch.full((B,), 0.1, device=dev)
+
+    def make_mode(name):
+        pr = probs0.clone()
+        f = {"plain": lambda: sampling.sampling_from_probs(pr, seed=1, offset=0),
+             "top_p": lambda: sampling.top_p_sampling_from_probs(pr, p, seed=1, offset=0),
+             "top_k": lambda: sampling.top_k_sampling_from_probs(pr, k, seed=1, offset=0),
+             "min_p": lambda: sampling.min_p_sampling_from_probs(pr, mp, seed=1, offset=0)}[name]
+        return f
     return [run(f"safe_scaled_softmax bf16 [{B},{V}]", 2 * B * V * 2, make_softmax),
             run(f"top_k_top_p sampling fp32 [{B},{V}] (k 50, p 0.9)", B * V * 4, make_sample),
+            run(f"sampling (plain) fp32 [{B},{V}]", B * V * 4, lambda: make_mode("plain")),
+            run(f"top_p sampling fp32 [{B},{V}] (p 0.9: ~5.6k tokens kept per row)", B * V * 4,
+                lambda: make_mode("top_p")),
+            run(f"top_k sampling fp32 [{B},{V}] (k 50)", B * V * 4, lambda: make_mode("top_k")),
+            run(f"min_p sampling fp32 [{B},{V}] (min_p 0.1)", B * V * 4, lambda: make_mode("min_p")),
             run(f"top_k_top_p sampling fp32 [{B},{V}], mass in the last quarter (two-pass fallback)",
                 B * V * 4, make_sample_skew)]
 

@@ -472,12 +472,50 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
     if (a.mode == 3 && !((double)x >= mthr)) return 0ull;
     return prob_mass(x);
   };
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (idx && V <= kSampThreads) {
+    // a candidate list of at most one element per thread: one block scan of the kept masses in
+    // list (= vocabulary) order; the draw is the first element whose inclusive mass exceeds
+    // u * total (the same element the chunked search below finds)
+    const int t = threadIdx.x;
+    const uint64_t m = t < V ? kept_mass(p[t]) : 0ull;
+    uint64_t incl = m;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t y = shfl_u64(incl, lane >= o ? lane - o : lane);
+      if (lane >= o) incl += y;
+    }
+    int last = m ? t : -1;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) last = max(last, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, last));
+    __syncthreads();
+    if (lane == 63) sh.wsum[w] = incl;
+    if (lane == 0) sh.cnt[w] = (uint32_t)(last + 1);
+    if (t == 0) sh.pick = -1;
+    __syncthreads();
+    uint64_t tot = 0, before = 0;
+    for (int i = 0; i < kSampWaves; ++i) {
+      if (i < w) before += sh.wsum[i];
+      tot += sh.wsum[i];
+      last = max(last, (int)sh.cnt[i] - 1);
+    }
+    const double u = a.uniforms ? a.uniforms[r] : philox_uniform(a.seed, a.offset, (uint32_t)r);
+    const double target = u * (double)tot;
+    incl += before;
+    const uint64_t excl = incl - m;
+    if (m && (double)incl > target && !((double)excl > target)) sh.pick = t;
+    __syncthreads();
+    if (t == 0) {
+      const int j = sh.pick >= 0 ? sh.pick : last;
+      a.out[r] = j >= 0 ? (int32_t)idx[j] : j;
+    }
+    return;
+  }
   // kept-mass pass: the sums of chunks of whole 4096-element tiles (at most 256 chunks), so that
   // the inverse CDF scans only the chunk where the target falls
   constexpr int kTile = 4 * kSampThreads;
   const int ntiles = (V + kTile - 1) / kTile;
   const int tpc = (ntiles + 255) / 256;  // tiles per chunk
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   for (int i = threadIdx.x; i < 256; i += kSampThreads) sh.mass[i] = 0;
   __syncthreads();
   auto load4 = [&](int i0, float (&x)[4]) {
