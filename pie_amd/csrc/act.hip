@@ -16,6 +16,7 @@ namespace {
 
 template <int U, int ACT>
 __global__ __launch_bounds__(256) void silu_and_mul_vec(SiluArgs a) {
+  prefetch_kernarg<(int)sizeof(SiluArgs)>(a);
   act_and_mul_block<U, ACT>(a, blockIdx.x);
 }
 

@@ -29,6 +29,7 @@ struct EmbedArgs {
 // vector's token is re-read per vector (an L1 hit); ids outside [0, V) give zero rows.
 template <int U, bool SCALE>
 __global__ __launch_bounds__(256) void embed_vec(EmbedArgs a) {
+  prefetch_kernarg<(int)sizeof(EmbedArgs)>(a);
   const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
   uint4 v[U];
   int64_t dst[U];

@@ -65,6 +65,7 @@ constexpr int kRowsPerGroup = 1;
 // squares through LDS in a fixed order. The weight row stays in registers across rows.
 template <int VPL, int RPG, bool ADD, bool GEMMA, bool NT>
 __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
+  prefetch_kernarg<(int)sizeof(NormArgs)>(a);
   __shared__ acc_t<GEMMA> part[RPG][8];
   const RowSet& s = a.set[0];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -164,6 +165,7 @@ __global__ __launch_bounds__(512) void rmsnorm_rows_reg(NormArgs a, int W) {
 // (Configuration 2 in one harness: 44.3 us for this shape against 48 us for the row-loop kernel.)
 template <int VPL, bool ADD, bool GEMMA>
 __global__ __launch_bounds__(512) void rmsnorm_row_block(NormArgs a) {
+  prefetch_kernarg<(int)sizeof(NormArgs)>(a);
   __shared__ acc_t<GEMMA> part[8];
   const RowSet& s = a.set[0];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -220,6 +222,7 @@ __global__ __launch_bounds__(512) void rmsnorm_row_block(NormArgs a) {
 // (a copy between them would wait for the loads in flight). No LDS, no barrier.
 template <int VPL, bool GEMMA>
 __global__ __launch_bounds__(256) void rmsnorm_rows_pf(NormArgs a) {
+  prefetch_kernarg<(int)sizeof(NormArgs)>(a);
   const RowSet& s = a.set[0];
   const int lane = threadIdx.x & 63;
   const int64_t nw = (int64_t)gridDim.x * 4;
@@ -299,6 +302,7 @@ struct Chunk<16> {
 
 template <int EPL, bool GEMMA>
 __global__ __launch_bounds__(256) void rmsnorm_heads16(NormArgs a) {
+  prefetch_kernarg<(int)sizeof(NormArgs)>(a);
   const int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;  // 16-lane group
   const int sub = threadIdx.x & 15;
   const int64_t total = a.set[0].rows + a.set[1].rows;
