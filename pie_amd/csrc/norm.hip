@@ -429,11 +429,7 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
   const bool large = in_bytes >= (int64_t)64 << 20;  // far larger than L2
   // (the residual-add form only: a plain norm, one input stream, keeps too few bytes in flight at
   // one vector per lane and stays on the row-loop kernel with 4 vectors per lane)
-  static const bool forced_rowblock = [] {  // tuning override: PIE_HIP_NORM_ROWBLOCK=1
-    const char* e = getenv("PIE_HIP_NORM_ROWBLOCK");
-    return e && atoi(e) == 1;
-  }();
-  if ((ADD || forced_rowblock) && vec && large && a.set[1].rows == 0 && a.cols % 4096 == 0 &&
+  if (ADD && vec && large && a.set[1].rows == 0 && a.cols % 4096 == 0 &&
       a.cols <= 3 * 4096 && rows < 0x7fffffff) {
     const dim3 grd((unsigned)rows), tb(512);
     switch (a.cols / 4096) {
@@ -446,12 +442,8 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
   // Gemma's plain norm of large row lists: the row-prefetching kernel, 2 work groups per CU
   // ([8192, 4096]: 25.2 us against 26.6-28.5 for rows_reg; 1 per CU 26.4, 3 per CU 26.1; two
   // rows ahead 26.9). The standard plain norm measured the same either way (24.0-24.1 us) and
-  // stays on rows_reg. Tuning override: PIE_HIP_NORM_PF=<work groups per CU> (0: off).
-  static const int pf_forced = [] {
-    const char* e = getenv("PIE_HIP_NORM_PF");
-    return e ? atoi(e) : -1;
-  }();
-  const int pf_blocks = pf_forced >= 0 ? pf_forced : (GEMMA ? 2 : 0);
+  // stays on rows_reg.
+  const int pf_blocks = GEMMA ? 2 : 0;
   if (!ADD && vec && large && pf_blocks > 0 && a.set[1].rows == 0 && a.cols % 512 == 0 &&
       a.cols <= 8 * 512) {
     int64_t blocks = (int64_t)num_cus() * pf_blocks;
@@ -475,12 +467,6 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
     int W = 0;
     for (int w = 8; w >= 1; w /= 2)
       if (n512 % w == 0 && n512 / w <= 12 && (ADD || n512 / w >= 4 || w == 1)) { W = w; break; }
-    static const int forced = [] {  // tuning override: PIE_HIP_NORM_WAVES=1|2|4|8
-      const char* e = getenv("PIE_HIP_NORM_WAVES");
-      return e ? atoi(e) : 0;
-    }();
-    if (forced == 1 || forced == 2 || forced == 4 || forced == 8)
-      if (n512 % forced == 0 && n512 / forced <= 12) W = forced;
     if (W > 0) {
       const int threads = W == 8 ? 512 : 256;
       const int64_t G = threads / (64 * W);
@@ -492,15 +478,11 @@ int launch_rows(const NormArgs& a, hipStream_t st, const char* name) {
       // 2, 8 waves per row, steady state: x / r / s / y at 5.6 TB/s cached, 6.7 TB/s
       // non-temporal in a standalone model of this kernel); small lists (decode) keep their
       // outputs in L2 for the next kernel.
-      static const int forced_nt = [] {  // tuning override: PIE_HIP_NORM_NT=0|1
-        const char* e = getenv("PIE_HIP_NORM_NT");
-        return e ? atoi(e) : -1;
-      }();
       // Non-temporal from 8 MB of input on (configuration 1, [2048, 2048] = 8 MiB, steady state:
-      // 4.72 us against 6.05 us cached; a plain copy of the same bytes takes 3.79 us
-      // non-temporal, 4.42 cached). Decode-sized lists keep their outputs in L2 for the next kernel.
-      const bool nt = forced_nt == 0 || forced_nt == 1 ? forced_nt == 1
-                                                       : in_bytes >= (int64_t)8 << 20;
+      // 4.72 us against 6.05 us cached; W = 1 and 2 the same, W = 4 5.58 us; a plain copy of
+      // the same bytes takes 3.79 us non-temporal, 4.42 cached). Decode-sized lists keep their
+      // outputs in L2 for the next kernel.
+      const bool nt = in_bytes >= (int64_t)8 << 20;
       switch ((n512 / W) * 2 + (nt ? 1 : 0)) {
 #define PIE_NV(n)                                                                                      \
   case 2 * n: hipLaunchKernelGGL((rmsnorm_rows_reg<n, kRowsPerGroup, ADD, GEMMA, false>), grd, tb, 0, st, a, W); \

@@ -298,18 +298,11 @@ int launch(RopeAppendArgs& a, bool rope, bool append, int interleave, hipStream_
     if (nunits < (1ll << 31)) {
       AppendFlatArgs f{h, a.c, (uint32_t)nunits, FastDiv::make((uint32_t)(2 * kunits)),
                        FastDiv::make((uint32_t)(h.D / 8)), (uint32_t)kunits};
-      static const int forced_u = [] {  // tuning override: PIE_HIP_APPEND_U=1|2|4
-        const char* e = getenv("PIE_HIP_APPEND_U");
-        return e ? atoi(e) : 0;
-      }();
-      const int U = forced_u == 1 || forced_u == 2 || forced_u == 4 ? forced_u : 1;
+      // one 16-byte unit per thread (2 and 4 per thread measured slower)
       const bool wu = (2 * kunits) % 64 == 0;
-      const dim3 grd((unsigned)((nunits + 256 * U - 1) / (256 * U))), blk(256);
-#define PIE_AF(u)                                                                  \
-  if (wu) hipLaunchKernelGGL((append_flat<u, true>), grd, blk, 0, st, f);           \
-  else hipLaunchKernelGGL((append_flat<u, false>), grd, blk, 0, st, f);
-      if (U == 4) { PIE_AF(4) } else if (U == 2) { PIE_AF(2) } else { PIE_AF(1) }
-#undef PIE_AF
+      const dim3 grd((unsigned)((nunits + 255) / 256)), blk(256);
+      if (wu) hipLaunchKernelGGL((append_flat<1, true>), grd, blk, 0, st, f);
+      else hipLaunchKernelGGL((append_flat<1, false>), grd, blk, 0, st, f);
       return check_launch(name);
     }
   }
