@@ -358,6 +358,26 @@ def _ops_ceiling(dev, run):
                                              dst.data_ptr(), 2 * T, kv_b, st())
     res.append(run(f"ceiling scatter of the cfg3 append pattern T={T}", 2 * T * 2 * kv_b + 2 * T * 16,
                    make_scatter))
+    # the fixed cost of one kernel inside a captured graph (what every launch of a decode step
+    # pays besides its own work): 12 launches of a 16-byte copy in one graph, replayed back to back
+    tiny = [torch.empty(16, dtype=torch.uint8, device=dev) for _ in range(24)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    def tiny_all():
+        for i in range(12):
+            lib.pie_probe_copy(tiny[2 * i].data_ptr(), tiny[2 * i + 1].data_ptr(), 16, 1, st())
+    with torch.cuda.stream(side):
+        tiny_all()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        tiny_all()
+    per = _back_to_back(g.replay, 50) / 12
+    res.append({"op": "ceiling graph launch: one 16-byte copy kernel, 12 per graph", "bytes": 32, "us": round(per, 2),
+                "gbs": None, "frac": None})
+    del g
     return res
 
 
