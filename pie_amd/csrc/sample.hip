@@ -918,15 +918,168 @@ __device__ __forceinline__ void select_bin(double thr, HistShared& hs) {
   }
 }
 
+// The k-th largest of a wave's keys (KPL per lane; 0 for no key): the largest v with at least k
+// keys >= v, found bit by bit from the top with ballots (keys of p > 0 have bit 31 clear); 0 when
+// fewer than k keys are positive.
+template <int KPL>
+__device__ __forceinline__ uint32_t wave_kth_largest(const uint32_t (&key)[KPL], int k) {
+  uint32_t prefix = 0u;
+  for (int b = 30; b >= 0; --b) {
+    const uint32_t cand = prefix | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) cnt += __builtin_popcountll(__builtin_amdgcn_ballot_w64(key[j] >= cand));
+    if (cnt >= k) prefix = cand;
+  }
+  return prefix;
+}
+
+// Raises a wave's floor to the k-th largest key of its candidate list (n entries at val / idx)
+// when that is higher and keeps, in order, the entries at or above the floor; returns the new
+// count. Every read of the list precedes every write (entries only move to lower positions).
+__device__ __forceinline__ int wave_shrink(float* val, uint32_t* idx, int n, int k, uint32_t& f) {
+  constexpr int J = kWaveCands / 64;
+  const int lane = threadIdx.x & 63;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  float v[J];
+  uint32_t ix[J], key[J];
+  __builtin_amdgcn_wave_barrier();  // the list's last appends (other lanes' writes) come first
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int i = 64 * j + lane;
+    v[j] = i < n ? val[i] : 0.f;
+    ix[j] = i < n ? idx[i] : 0u;
+    key[j] = i < n ? prob_key(v[j]) : 0u;
+  }
+  f = max(f, wave_kth_largest<J>(key, k));
+  int base = 0;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const bool keep = key[j] >= f && key[j] != 0u;
+    const uint64_t b = __builtin_amdgcn_ballot_w64(keep);
+    if (keep) {
+      const int pos = base + (int)__builtin_popcountll(b & lt);
+      val[pos] = v[j];
+      idx[pos] = ix[j];
+    }
+    base += (int)__builtin_popcountll(b);
+  }
+  return base;
+}
+
+// One read of the row for top_k (k <= kOnePassMaxK), as wave segments: each wave keeps, in
+// vocabulary order, the candidates at or above its own floor, which starts at f0 (a floor under
+// the row's k-th largest key) and rises to the k-th largest key of the wave's list whenever the
+// list would overflow (wave_shrink; rows whose largest keys sit away from where f0 was taken). A
+// subset's k-th largest never exceeds the row's, so every key at or above the row's k-th largest
+// stays listed; a wave with more than kSampThreads / kSampWaves entries at the end keeps its own
+// top k (ties included), so the lists together usually fit the short-list path. Returns the
+// wave's count, more than kWaveCands when a list of ties would not shrink (unusable); cpos gets
+// this lane's count of p > 0.
+__device__ int topk_segment(const float* p, int V, int k, uint32_t f0, CandShared& cs, uint32_t& cpos) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  float* val = cs.val + w * kWaveCands;
+  uint32_t* idx = cs.idx + w * kWaveCands;
+  int n = 0;
+  bool over = false;
+  uint32_t f = max(f0, 1u), c = 0;
+  // appends the keys >= f of four consecutive elements per lane (up to 256 per call)
+  auto add4 = [&](const float (&x)[4], int i0, bool live) {
+    uint32_t key[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      key[e] = live ? prob_key(x[e]) : 0u;
+      c += key[e] != 0u;
+    }
+    if (over) return;
+    if (n + 256 > kWaveCands) {
+      n = wave_shrink(val, idx, n, k, f);
+      if (n + 256 > kWaveCands) {  // ties that do not shrink: the list is unusable
+        over = true;
+        return;
+      }
+    }
+    uint32_t bits = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bits |= (uint32_t)(key[e] >= f && key[e] != 0u) << e;
+    const uint32_t cnt = __builtin_popcount(bits);
+    if (__builtin_amdgcn_ballot_w64(cnt != 0) == 0) return;
+    const uint64_t b0 = __builtin_amdgcn_ballot_w64(cnt & 1u), b1 = __builtin_amdgcn_ballot_w64(cnt & 2u),
+                   b2 = __builtin_amdgcn_ballot_w64(cnt & 4u);
+    int pos = n + __builtin_popcountll(b0 & lt) + 2 * __builtin_popcountll(b1 & lt) +
+              4 * __builtin_popcountll(b2 & lt);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (bits >> e & 1u) {
+        val[pos] = x[e];
+        idx[pos] = (uint32_t)(i0 + e);
+        ++pos;
+      }
+    n += __builtin_popcountll(b0) + 2 * __builtin_popcountll(b1) + 4 * __builtin_popcountll(b2);
+  };
+  const int nv = V >> 2;
+  const int seg = (nv + kSampWaves - 1) / kSampWaves;
+  const int v0 = w * seg, v1 = min(nv, v0 + seg);
+  int vb = v0;  // wave-uniform position
+  constexpr int kU = 4, kB = kU * 64;
+  auto scan = [&](const float4 (&d)[kU], int at) {
+#pragma unroll
+    for (int q = 0; q < kU; ++q) {
+      const float xe[4] = {d[q].x, d[q].y, d[q].z, d[q].w};
+      add4(xe, 4 * (at + lane + 64 * q), true);
+    }
+  };
+  if (vb + kB <= v1) {
+    float4 x[kU], y[kU];
+    auto load = [&](float4 (&d)[kU], int at) {
+#pragma unroll
+      for (int q = 0; q < kU; ++q) d[q] = *reinterpret_cast<const float4*>(p + 4 * (at + lane + 64 * q));
+    };
+    load(x, vb);
+    if (vb + 2 * kB <= v1) load(y, vb + kB);
+    for (;;) {
+      const bool has_y = vb + 2 * kB <= v1;
+      scan(x, vb);
+      if (has_y && vb + 3 * kB <= v1) load(x, vb + 2 * kB);
+      vb += kB;
+      if (!has_y) break;
+      const bool has_x = vb + 2 * kB <= v1;
+      scan(y, vb);
+      if (has_x && vb + 3 * kB <= v1) load(y, vb + 2 * kB);
+      vb += kB;
+      if (!has_x) break;
+    }
+  }
+  for (; vb < v1; vb += 64) {
+    const int v = vb + lane;
+    float xe[4] = {0.f, 0.f, 0.f, 0.f};
+    if (v < v1) {
+      const float4 x = *reinterpret_cast<const float4*>(p + 4 * v);
+      xe[0] = x.x; xe[1] = x.y; xe[2] = x.z; xe[3] = x.w;
+    }
+    add4(xe, 4 * v, v < v1);
+  }
+  if (w == kSampWaves - 1) {  // the last < 4 elements belong to the last segment
+    const int i = 4 * nv + lane;
+    float xe[4] = {i < V ? p[i] : 0.f, 0.f, 0.f, 0.f};
+    add4(xe, i, i < V);  // elements 1-3 of xe are 0: no key
+  }
+  cpos = c;
+  if (over) return kWaveCands + 1;
+  return n > kSampThreads / kSampWaves ? wave_shrink(val, idx, n, k, f) : n;
+}
+
 // Copies the elements that satisfy pred into cs.val / cs.idx in vocabulary order (each wave its
 // own segment, then the gaps between the segments' lists closed); *total = the list's length.
 // npos (optional): the row's count of p > 0, counted on the way. False when some segment
-// overflowed (the list is then unusable).
+// overflowed (the list is then unusable). topk > 0: the candidates of a top_k (topk_segment, from
+// the floor pred.lo; vec rows only) instead of pred's.
 __device__ __forceinline__ bool gather_list(const float* p, int V, bool vec, const ListPred& pred, CandShared& cs,
-                                         int* total_out, uint32_t* npos) {
+                                         int* total_out, uint32_t* npos, int topk = 0) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   uint32_t c = 0;
-  const int n = compact_segment(p, V, vec, [&](int i, float x) {
+  const int n = topk > 0 ? topk_segment(p, V, topk, pred.lo, cs, c) : compact_segment(p, V, vec, [&](int i, float x) {
     c += prob_key(x) != 0u;
     return pred(i, x);
   }, cs);
@@ -1020,9 +1173,9 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
   uint64_t row_tot = 0;
   // Copies the elements that satisfy pred into the candidate list (gather_list) and points the
   // selection at it; false (and the list unused) when some segment overflowed.
-  auto gather = [&](const ListPred& pred, uint32_t* npos_out = nullptr) -> bool {
+  auto gather = [&](const ListPred& pred, uint32_t* npos_out = nullptr, int topk = 0) -> bool {
     int total;
-    if (!gather_list(p, V, vec, pred, cs, &total, npos_out)) return false;
+    if (!gather_list(p, V, vec, pred, cs, &total, npos_out, topk)) return false;
     sp = cs.val;
     sidx = cs.idx;
     sV = total;
@@ -1068,17 +1221,18 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
     }
     __syncthreads();
   }
-  // One read for top_k (alone or before top_p) with a small k over a long row: the k-th largest
-  // of the row's first kHeadElems elements is a floor under the row's k-th largest, so one pass
-  // collects every element at or above it (about k * V / kHeadElems of them for exchangeable
-  // rows) and counts the row's p > 0 on the way. Overflow falls back to the two passes below.
+  // One read for top_k (alone or before top_p) with k <= kOnePassMaxK over a long row: the k-th
+  // largest of the row's first kHeadElems elements is a floor under the row's k-th largest, so one
+  // pass collects every element at or above it (about k * V / kHeadElems of them for exchangeable
+  // rows; each wave raises its own floor when its list fills, so rows whose largest keys sit past
+  // the head stay on this path) and counts the row's p > 0 on the way. A list of ties that will
+  // not shrink falls back to the passes below.
   if (!kTopP && (mode == 2 || mode == 4) && vec && k > 0 && k <= kOnePassMaxK && V >= kOnePassMinV) {
     // the floor: the k-th largest of the threads' maxima over their kHeadElems / kSampThreads
     // head elements (a subset of the head, so at most the head's k-th largest; the head's
     // largest keys are nearly always their thread's maximum, so it is about as tight), from a
     // bitonic sort of the 1024 maxima (no LDS atomics, which serialise on keys sharing their
-    // top bits). A floor from each wave's ceil(k/16)-th largest maximum (ballot counts, no
-    // sort) measured slower: looser, it lets some rows' lists outgrow the short-list path.
+    // top bits).
     uint32_t hm = 0u;
 #pragma unroll
     for (int j = 0; j < kHeadElems / 4 / kSampThreads; ++j) {
@@ -1091,12 +1245,10 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
     __syncthreads();
     const uint32_t floor0 = sh.u32a;
     __syncthreads();  // the sort buffer is dead from here: its memory holds the candidates
-    if (floor0 > 1u) {
-      uint32_t c = 0;
-      listed = gather(ListPred{0, floor0, 0u, 0.0}, &c);
-      npos = (int64_t)c;
-      __syncthreads();
-    }
+    uint32_t c = 0;
+    listed = gather(ListPred{0, floor0, 0u, 0.0}, &c, k);
+    npos = (int64_t)c;
+    __syncthreads();
   }
   // plain sampling, and top_k with k outside (0, V), keep every p > 0: no candidate list; top_p
   // went through the histogram above

@@ -96,6 +96,8 @@ static void check_equal(const char* what, const T* got, const T* want, size_t n)
   size_t bad = 0;
   for (size_t i = 0; i < n; ++i) bad += got[i] != want[i];
   printf("  %-40s %s (%zu / %zu differ)\n", what, bad ? "FAIL" : "ok", bad, n);
+  for (size_t i = 0, shown = 0; i < n && shown < 3; ++i)
+    if (got[i] != want[i]) { printf("    [%zu] got %lld want %lld\n", i, (long long)got[i], (long long)want[i]); ++shown; }
   failures += bad != 0;
 }
 static void rc_ok(int rc, const char* what) {

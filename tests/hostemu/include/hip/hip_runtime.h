@@ -129,6 +129,10 @@ inline int readfirstlane(int v) {
   return (int)r;
 }
 
+// __builtin_amdgcn_wave_barrier: on the GPU a compiler-only fence (the lanes of a wave run in
+// lockstep); lanes here are threads, so it is a wave barrier.
+inline void wave_sync() { ctx->wave->bar.arrive_and_wait(); }
+
 inline uint64_t ballot(bool v) {
   Wave* w = ctx->wave;
   w->xchg[ctx->lane] = v ? 1u : 0u;
@@ -286,6 +290,7 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 #define __builtin_amdgcn_readfirstlane emu::readfirstlane
 #define __builtin_amdgcn_exp2f exp2f
 #define __builtin_amdgcn_ballot_w64 emu::ballot
+#define __builtin_amdgcn_wave_barrier emu::wave_sync
 #define __builtin_amdgcn_ds_bpermute emu::bpermute
 #define __builtin_amdgcn_permlane16_swap emu::permlane16_swap
 #define __builtin_amdgcn_permlane32_swap emu::permlane32_swap
