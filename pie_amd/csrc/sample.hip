@@ -66,10 +66,37 @@ __device__ __forceinline__ double philox_uniform(uint64_t seed, uint64_t offset,
   return (double)(bits & ((1ull << 53) - 1)) * (1.0 / 9007199254740992.0);
 }
 
-__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
-  const int lo = __builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)v);
-  const int hi = __builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)(v >> 32));
-  return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+// v of lane - n within the lane's 16-lane row (0 for the row's first n lanes): DPP row_shr:n.
+template <int N>
+__device__ __forceinline__ uint64_t row_shr_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x110 + N, 0xf, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x110 + N, 0xf, 0xf, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
+// Inclusive scan over the wave's 64 lanes (all active): within 16-lane rows by DPP shifts, then
+// the totals of the rows before each row.
+__device__ __forceinline__ uint64_t row_incl_scan_u64(uint64_t v) {
+  v += row_shr_u64<1>(v);
+  v += row_shr_u64<2>(v);
+  v += row_shr_u64<4>(v);
+  v += row_shr_u64<8>(v);
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
+  v = row_incl_scan_u64(v);
+  const uint64_t r0 = readlane_u64(v, 15), r1 = readlane_u64(v, 31), r2 = readlane_u64(v, 47);
+  const int row = (threadIdx.x & 63) >> 4;
+  return v + (row > 0 ? r0 : 0ull) + (row > 1 ? r1 : 0ull) + (row > 2 ? r2 : 0ull);
+}
+// The wave's total (all lanes active), the same in every lane.
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+  v = row_incl_scan_u64(v);
+  return readlane_u64(v, 15) + readlane_u64(v, 31) + readlane_u64(v, 47) + readlane_u64(v, 63);
 }
 
 struct SampleShared {
@@ -84,8 +111,7 @@ struct SampleShared {
 // Block-wide sum (all threads get the result).
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, SampleShared& sh) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += shfl_u64(v, lane ^ o);
+  v = wave_sum_u64(v);
   __syncthreads();
   if (lane == 0) sh.wsum[w] = v;
   __syncthreads();
@@ -200,14 +226,8 @@ __device__ __forceinline__ uint32_t radix_threshold(const float* p, int V, bool 
       }
       const uint32_t lc = c[0] + c[1] + c[2] + c[3];
       const uint64_t lm = m[0] + m[1] + m[2] + m[3];
-      uint32_t ic = lc;
-      uint64_t im = lm;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t yc = (uint32_t)__builtin_amdgcn_ds_bpermute((lane >= o ? lane - o : lane) << 2, (int)ic);
-        const uint64_t ym = by_mass ? shfl_u64(im, lane >= o ? lane - o : lane) : 0ull;
-        if (lane >= o) { ic += yc; im += ym; }
-      }
+      const uint32_t ic = (uint32_t)wave_incl_scan_u64(lc);
+      const uint64_t im = by_mass ? wave_incl_scan_u64(lm) : 0ull;
       uint32_t cc = ic - lc;          // keys in the digits above this lane's first
       uint64_t ma = above + im - lm;  // their mass plus the mass above the prefix
       if (!by_mass) {
@@ -281,6 +301,22 @@ struct SampleArgs {
   int32_t vec;  // rows are 16-byte aligned: 16-byte loads
 };
 
+// A row's sampling parameters, read once at the kernel's start (their loads then overlap the
+// row's passes): top_k, top_p, min_p and the draw's uniform u.
+struct RowParams {
+  int32_t k;
+  float tp, mp;
+  double u;
+};
+__device__ __forceinline__ RowParams row_params(const SampleArgs& a, int r) {
+  RowParams q;
+  q.k = a.top_k ? a.top_k[r] : a.top_k_s;
+  q.tp = a.top_p ? a.top_p[r] : a.top_p_s;
+  q.mp = a.min_p ? a.min_p[r] : a.min_p_s;
+  q.u = a.uniforms ? a.uniforms[r] : philox_uniform(a.seed, a.offset, (uint32_t)r);
+  return q;
+}
+
 // min and max of v and the v of lane ^ j (j < 64), in registers: DPP within 16-lane rows
 // (quad_perm for j = 1, 2; row_shl:4 / row_shr:4 for j = 4; row_ror:8 for j = 8), and across
 // rows v_permlane16_swap / v_permlane32_swap, which leave {v, partner} in their two results.
@@ -317,21 +353,27 @@ __device__ __forceinline__ void lane_pair(uint32_t v, int j, uint32_t& lo, uint3
 // kept sets as the radix selects: top_k keeps keys >= the k-th largest (ties stay), top_p keeps
 // keys >= the smallest key whose strictly larger keys' mass is below top_p * mass (the maximal
 // key when that product is <= 0).
+// S (a power of two, 64..kSampThreads) keys, held by threads [0, S); every thread of the block
+// calls it (the cross-wave steps are block barriers), the others idle.
+template <int S = kSampThreads>
 __device__ __forceinline__ uint32_t sort_desc_keys(uint32_t v, uint32_t* buf) {
   const int t = threadIdx.x;
+  const bool act = t < S;  // wave-uniform
 #pragma unroll
-  for (int k = 2; k <= kSampThreads; k <<= 1) {
+  for (int k = 2; k <= S; k <<= 1) {
 #pragma unroll
     for (int j = k >> 1; j > 0; j >>= 1) {
       const bool desc = (t & k) == 0;     // this k-block sorts descending (the whole array at the end)
       const bool first = (t & j) == 0;  // the lower position of the pair
       if (j >= 64) {
         __syncthreads();
-        buf[t] = v;
+        if (act) buf[t] = v;
         __syncthreads();
-        const uint32_t pv = buf[t ^ j];
-        v = (first == desc) ? max(v, pv) : min(v, pv);
-      } else {
+        if (act) {
+          const uint32_t pv = buf[t ^ j];
+          v = (first == desc) ? max(v, pv) : min(v, pv);
+        }
+      } else if (act) {
         uint32_t lo, hi;
         lane_pair(v, j, lo, hi);
         v = (first == desc) ? hi : lo;
@@ -343,30 +385,27 @@ __device__ __forceinline__ uint32_t sort_desc_keys(uint32_t v, uint32_t* buf) {
 
 // Returns lo for the list p[0, n) (n <= kSampThreads): the smallest kept key under the row's
 // top_k / top_p (modes 1, 2, 4), as sample_row's radix selects would give it.
-__device__ __forceinline__ uint32_t list_threshold(const float* p, int n, const SampleArgs& a, int r, int64_t npos,
+__device__ __forceinline__ uint32_t list_threshold(const float* p, int n, const SampleArgs& a, const RowParams& rp, int64_t npos,
                                    uint64_t row_tot, SampleShared& sh, uint32_t* buf) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   uint32_t v = t < n ? prob_key(p[t]) : 0u;
-  v = sort_desc_keys(v, buf);  // position t now holds the (t+1)-th largest key
+  // position t now holds the (t+1)-th largest key (the sort spans the smallest power of two
+  // holding the list; the positions past it hold zero keys, as before)
+  v = n <= 256 ? sort_desc_keys<256>(v, buf) : n <= 512 ? sort_desc_keys<512>(v, buf) : sort_desc_keys(v, buf);
   const uint64_t m = v ? prob_mass(__builtin_bit_cast(float, v)) : 0ull;
   // inclusive block scan of the masses in sorted order
-  uint64_t incl = m;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint64_t y = shfl_u64(incl, lane >= o ? lane - o : lane);
-    if (lane >= o) incl += y;
-  }
+  uint64_t incl = wave_incl_scan_u64(m);
   __syncthreads();
   if (lane == 63) sh.wsum[w] = incl;
   buf[t] = v;
-  if (t == 0) { sh.u32a = 1u; sh.u32b = (uint32_t)n; sh.u64a = 0; }
+  if (t == 0) { sh.u32a = 0u; sh.u32b = (uint32_t)n; sh.u64a = 0; }
   __syncthreads();
   for (int i = 0; i < w; ++i) incl += sh.wsum[i];
   const uint64_t excl = incl - m;
   uint32_t lo = 1u;
   int lim = n;  // positions [0, lim) hold the keys >= lo
   if (a.mode == 2 || a.mode == 4) {
-    const int32_t k = a.top_k ? a.top_k[r] : a.top_k_s;
+    const int32_t k = rp.k;
     int64_t np = npos;
     if (np < 0) {  // the list's count of p > 0 (sorted: the first zero key's position)
       if (t == 0) sh.pick = 0;
@@ -386,7 +425,7 @@ __device__ __forceinline__ uint32_t list_threshold(const float* p, int n, const 
     }
   }
   if (a.mode == 1 || a.mode == 4) {
-    const float tp = a.top_p ? a.top_p[r] : a.top_p_s;
+    const float tp = rp.tp;
     uint64_t tot;
     if (a.mode == 1 && row_tot) {
       tot = row_tot;
@@ -399,9 +438,6 @@ __device__ __forceinline__ uint32_t list_threshold(const float* p, int n, const 
       tot = sh.u64a;
     }
     const double thr = (double)tp * (double)tot;
-    __syncthreads();
-    if (t == 0) sh.u32a = 0u;
-    __syncthreads();
     // the last position whose strictly-before mass is below thr (ties before it share its key)
     if (t < lim && v != 0u && (double)excl < thr && (t + 1 == lim || !((double)incl < thr))) sh.u32a = v;
     __syncthreads();
@@ -421,8 +457,8 @@ __device__ __forceinline__ uint32_t list_threshold(const float* p, int n, const 
 // decide it are the same as over the whole row. lo_given > 0: the kept keys' lower bound is
 // already known (top_p resolved from the row's histogram): no threshold search here.
 __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, int V, bool vec,
-                                           const SampleArgs& a, int r, int64_t npos, uint64_t row_tot,
-                                           SampleShared& sh, uint32_t* list_buf = nullptr,
+                                           const SampleArgs& a, int r, const RowParams& rp, int64_t npos,
+                                           uint64_t row_tot, SampleShared& sh, uint32_t* list_buf = nullptr,
                                            uint32_t lo_given = 0u) {
   if (V == 0) {  // nothing to draw from (an empty candidate list)
     if (threadIdx.x == 0) a.out[r] = -1;
@@ -435,9 +471,9 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
   const bool short_list = !given && list_buf && idx && V <= kSampThreads && a.mode != 3;
   if (given) {
   } else if (short_list) {
-    lo = list_threshold(p, V, a, r, npos, row_tot, sh, list_buf);
+    lo = list_threshold(p, V, a, rp, npos, row_tot, sh, list_buf);
   } else if (a.mode == 2 || a.mode == 4) {
-    const int32_t k = a.top_k ? a.top_k[r] : a.top_k_s;
+    const int32_t k = rp.k;
     if (k > 0 && k < V) {
       if (npos < 0) {
         uint32_t c = 0;
@@ -448,7 +484,7 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
     }
   }
   if (!given && !short_list && (a.mode == 1 || a.mode == 4)) {
-    const float tp = a.top_p ? a.top_p[r] : a.top_p_s;
+    const float tp = rp.tp;
     uint64_t tot = 0;
     if (a.mode == 1 && row_tot) {
       tot = row_tot;
@@ -464,7 +500,7 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
     uint32_t mk = 0;
     for_row(p, V, vec, [&](int, float x) { mk = max(mk, prob_key(x)); });
     mk = block_max_u32(mk, sh);
-    mthr = (double)(a.min_p ? a.min_p[r] : a.min_p_s) * (double)__builtin_bit_cast(float, mk);
+    mthr = (double)rp.mp * (double)__builtin_bit_cast(float, mk);
   }
   auto kept_mass = [&](float x) -> uint64_t {
     const uint32_t k = prob_key(x);
@@ -479,15 +515,9 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
     // u * total (the same element the chunked search below finds)
     const int t = threadIdx.x;
     const uint64_t m = t < V ? kept_mass(p[t]) : 0ull;
-    uint64_t incl = m;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t y = shfl_u64(incl, lane >= o ? lane - o : lane);
-      if (lane >= o) incl += y;
-    }
-    int last = m ? t : -1;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) last = max(last, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, last));
+    uint64_t incl = wave_incl_scan_u64(m);
+    const uint64_t mb = __builtin_amdgcn_ballot_w64(m != 0ull);  // the wave's last kept element
+    int last = mb ? (t & ~63) + 63 - __builtin_clzll(mb) : -1;
     __syncthreads();
     if (lane == 63) sh.wsum[w] = incl;
     if (lane == 0) sh.cnt[w] = (uint32_t)(last + 1);
@@ -499,8 +529,7 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
       tot += sh.wsum[i];
       last = max(last, (int)sh.cnt[i] - 1);
     }
-    const double u = a.uniforms ? a.uniforms[r] : philox_uniform(a.seed, a.offset, (uint32_t)r);
-    const double target = u * (double)tot;
+    const double target = rp.u * (double)tot;
     incl += before;
     const uint64_t excl = incl - m;
     if (m && (double)incl > target && !((double)excl > target)) sh.pick = t;
@@ -535,8 +564,7 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
     if (m) last = max(last, i);
   };
   auto chunk_done = [&](int t) {  // this wave's share of tile t is in acc
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) acc += shfl_u64(acc, lane ^ o);
+    acc = wave_sum_u64(acc);
     if (lane == 0 && acc) atomicAdd((unsigned long long*)&sh.mass[t / tpc], (unsigned long long)acc);
     acc = 0;
   };
@@ -587,8 +615,7 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
         if (i < V) visit(i, p[i]);
       }
       if ((t + 1) % tpc == 0 || t == ntiles - 1) {  // chunk t / tpc ends here
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) acc += shfl_u64(acc, lane ^ o);
+        acc = wave_sum_u64(acc);
         if (lane == 0 && acc) atomicAdd((unsigned long long*)&sh.mass[t / tpc], (unsigned long long)acc);
         acc = 0;
       }
@@ -606,15 +633,9 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
 #pragma unroll
     for (int e = 0; e < 4; ++e) c[e] = sh.mass[4 * lane + e];
     const uint64_t lm = c[0] + c[1] + c[2] + c[3];
-    uint64_t incl = lm;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t y = shfl_u64(incl, lane >= o ? lane - o : lane);
-      if (lane >= o) incl += y;
-    }
-    const uint64_t tot = shfl_u64(incl, 63);
-    const double u = a.uniforms ? a.uniforms[r] : philox_uniform(a.seed, a.offset, (uint32_t)r);
-    const double target = u * (double)tot;
+    const uint64_t incl = wave_incl_scan_u64(lm);
+    const uint64_t tot = readlane_u64(incl, 63);
+    const double target = rp.u * (double)tot;
     uint64_t run = incl - lm;
     int first = 256;
     uint64_t first_excl = 0;
@@ -652,12 +673,7 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
       for (int e = 0; e < 4; ++e) m[e] = kept_mass(x[e]);
       const uint64_t mine = m[0] + m[1] + m[2] + m[3];
       // inclusive scan of `mine` over the block
-      uint64_t incl = mine;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint64_t y = shfl_u64(incl, lane >= o ? lane - o : lane);
-        if (lane >= o) incl += y;
-      }
+      uint64_t incl = wave_incl_scan_u64(mine);
       __syncthreads();
       if (lane == 63) sh.wsum[w] = incl;
       __syncthreads();
@@ -703,6 +719,8 @@ constexpr int kCands = kWaveCands * kSampWaves;
 // rows of at least kOnePassMinV elements (shorter rows gain little from skipping a read).
 constexpr int kHeadElems = 16384;
 constexpr int kOnePassMaxK = 256;
+constexpr int kHeadMaxima = 256;  // the head floor: the k-th largest of this many group maxima
+static_assert(kOnePassMaxK <= kHeadMaxima, "the head floor needs k <= kHeadMaxima");
 constexpr int kOnePassMinV = 65536;
 
 struct alignas(16) CandShared {
@@ -871,14 +889,8 @@ __device__ __forceinline__ void select_bin(double thr, HistShared& hs) {
     lm += hs.mass[d];
     lc += hs.cnt[d];
   }
-  uint64_t im = lm;
-  uint32_t ic = lc;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint64_t ym = shfl_u64(im, lane >= o ? lane - o : lane);
-    const uint32_t yc = (uint32_t)__builtin_amdgcn_ds_bpermute((lane >= o ? lane - o : lane) << 2, (int)ic);
-    if (lane >= o) { im += ym; ic += yc; }
-  }
+  const uint64_t im = wave_incl_scan_u64(lm);
+  const uint32_t ic = (uint32_t)wave_incl_scan_u64(lc);
   // this lane's lowest qualifying bin and its highest non-empty bin
   uint64_t a = im - lm;
   int low = kBins, high = -1;
@@ -968,22 +980,25 @@ __device__ __forceinline__ int wave_shrink(float* val, uint32_t* idx, int n, int
 }
 
 // One read of the row for top_k (k <= kOnePassMaxK), as wave segments: each wave keeps, in
-// vocabulary order, the candidates at or above its own floor, which starts at f0 (a floor under
-// the row's k-th largest key) and rises to the k-th largest key of the wave's list whenever the
+// vocabulary order, the candidates at or above its own floor, which starts at the head floor (a
+// floor under the row's k-th largest key: the k-th largest of the maxima of kHeadMaxima groups of
+// kHeadElems / kHeadMaxima elements of the row's head, a subset of the row; the head's largest
+// keys mostly fall in different groups, so it is nearly as tight as the head's k-th
+// largest) and rises to the k-th largest key of the wave's list whenever the
 // list would overflow (wave_shrink; rows whose largest keys sit away from where f0 was taken). A
 // subset's k-th largest never exceeds the row's, so every key at or above the row's k-th largest
 // stays listed; a wave with more than kSampThreads / kSampWaves entries at the end keeps its own
 // top k (ties included), so the lists together usually fit the short-list path. Returns the
 // wave's count, more than kWaveCands when a list of ties would not shrink (unusable); cpos gets
 // this lane's count of p > 0.
-__device__ int topk_segment(const float* p, int V, int k, uint32_t f0, CandShared& cs, uint32_t& cpos) {
+__device__ int topk_segment(const float* p, int V, int k, CandShared& cs, uint32_t& cpos) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const uint64_t lt = (1ull << lane) - 1ull;
   float* val = cs.val + w * kWaveCands;
   uint32_t* idx = cs.idx + w * kWaveCands;
   int n = 0;
   bool over = false;
-  uint32_t f = max(f0, 1u), c = 0;
+  uint32_t f = 1u, c = 0;
   // appends the keys >= f of four consecutive elements per lane (up to 256 per call)
   auto add4 = [&](const float (&x)[4], int i0, bool live) {
     uint32_t key[4];
@@ -1021,44 +1036,62 @@ __device__ int topk_segment(const float* p, int V, int k, uint32_t f0, CandShare
   const int nv = V >> 2;
   const int seg = (nv + kSampWaves - 1) / kSampWaves;
   const int v0 = w * seg, v1 = min(nv, v0 + seg);
-  int vb = v0;  // wave-uniform position
+  // the segment in batches of kB vectors, two register buffers in turn; the last batch's
+  // loads past the segment are clamped to its last vector and their keys dropped
   constexpr int kU = 4, kB = kU * 64;
+  const int nb = v1 > v0 ? (v1 - v0 + kB - 1) / kB : 0;
   auto scan = [&](const float4 (&d)[kU], int at) {
 #pragma unroll
     for (int q = 0; q < kU; ++q) {
+      const int v = at + lane + 64 * q;
       const float xe[4] = {d[q].x, d[q].y, d[q].z, d[q].w};
-      add4(xe, 4 * (at + lane + 64 * q), true);
+      add4(xe, 4 * v, v < v1);
     }
   };
-  if (vb + kB <= v1) {
-    float4 x[kU], y[kU];
-    auto load = [&](float4 (&d)[kU], int at) {
+  float4 x[kU], y[kU];
+  auto load = [&](float4 (&d)[kU], int at) {
 #pragma unroll
-      for (int q = 0; q < kU; ++q) d[q] = *reinterpret_cast<const float4*>(p + 4 * (at + lane + 64 * q));
-    };
-    load(x, vb);
-    if (vb + 2 * kB <= v1) load(y, vb + kB);
-    for (;;) {
-      const bool has_y = vb + 2 * kB <= v1;
-      scan(x, vb);
-      if (has_y && vb + 3 * kB <= v1) load(x, vb + 2 * kB);
-      vb += kB;
-      if (!has_y) break;
-      const bool has_x = vb + 2 * kB <= v1;
-      scan(y, vb);
-      if (has_x && vb + 3 * kB <= v1) load(y, vb + 2 * kB);
-      vb += kB;
-      if (!has_x) break;
+    for (int q = 0; q < kU; ++q)
+      d[q] = *reinterpret_cast<const float4*>(p + 4 * min(at + lane + 64 * q, v1 - 1));
+  };
+  // the head's loads, then the segment's first two batches, which stay in flight while the
+  // floor is formed (barriers wait for LDS traffic only)
+  float4 hx[kHeadElems / 4 / kSampThreads];
+#pragma unroll
+  for (int j = 0; j < kHeadElems / 4 / kSampThreads; ++j)
+    hx[j] = *reinterpret_cast<const float4*>(p + 4 * (threadIdx.x + j * kSampThreads));
+  // (unconditional, so the compiler's wait counts keep them outstanding: rows of at least
+  // kOnePassMinV elements give every segment more than two batches)
+  load(x, v0);
+  load(y, v0 + kB);
+  {
+    uint32_t hm = 0u;
+#pragma unroll
+    for (int j = 0; j < kHeadElems / 4 / kSampThreads; ++j)
+      hm = max(max(hm, max(prob_key(hx[j].x), prob_key(hx[j].y))), max(prob_key(hx[j].z), prob_key(hx[j].w)));
+    // the maxima of kHeadMaxima groups of the head (threads t, t + kHeadMaxima, ...), then their
+    // bitonic sort (no LDS atomics, which serialise on keys sharing their top bits), in the
+    // candidates' memory, which is dead until the floor is known
+    uint32_t* buf = reinterpret_cast<uint32_t*>(cs.val);
+    buf[threadIdx.x] = hm;
+    __syncthreads();
+    if (threadIdx.x < kHeadMaxima) {
+#pragma unroll
+      for (int i = 1; i < kSampThreads / kHeadMaxima; ++i) hm = max(hm, buf[threadIdx.x + i * kHeadMaxima]);
     }
+    __shared__ uint32_t f0;
+    hm = sort_desc_keys<kHeadMaxima>(hm, buf);
+    if (threadIdx.x == k - 1) f0 = hm;
+    __syncthreads();
+    f = max(f0, 1u);
+    __syncthreads();  // the sort buffer is dead from here: its memory holds the candidates
   }
-  for (; vb < v1; vb += 64) {
-    const int v = vb + lane;
-    float xe[4] = {0.f, 0.f, 0.f, 0.f};
-    if (v < v1) {
-      const float4 x = *reinterpret_cast<const float4*>(p + 4 * v);
-      xe[0] = x.x; xe[1] = x.y; xe[2] = x.z; xe[3] = x.w;
-    }
-    add4(xe, 4 * v, v < v1);
+  for (int b = 0; b < nb; b += 2) {
+    scan(x, v0 + b * kB);
+    if (b + 2 < nb) load(x, v0 + (b + 2) * kB);
+    if (b + 1 >= nb) break;
+    scan(y, v0 + (b + 1) * kB);
+    if (b + 3 < nb) load(y, v0 + (b + 3) * kB);
   }
   if (w == kSampWaves - 1) {  // the last < 4 elements belong to the last segment
     const int i = 4 * nv + lane;
@@ -1074,20 +1107,19 @@ __device__ int topk_segment(const float* p, int V, int k, uint32_t f0, CandShare
 // own segment, then the gaps between the segments' lists closed); *total = the list's length.
 // npos (optional): the row's count of p > 0, counted on the way. False when some segment
 // overflowed (the list is then unusable). topk > 0: the candidates of a top_k (topk_segment, from
-// the floor pred.lo; vec rows only) instead of pred's.
+// the row head's floor; vec rows only) instead of pred's.
 __device__ __forceinline__ bool gather_list(const float* p, int V, bool vec, const ListPred& pred, CandShared& cs,
                                          int* total_out, uint32_t* npos, int topk = 0) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   uint32_t c = 0;
-  const int n = topk > 0 ? topk_segment(p, V, topk, pred.lo, cs, c) : compact_segment(p, V, vec, [&](int i, float x) {
+  const int n = topk > 0 ? topk_segment(p, V, topk, cs, c) : compact_segment(p, V, vec, [&](int i, float x) {
     c += prob_key(x) != 0u;
     return pred(i, x);
   }, cs);
   if (lane == 0) cs.wn[w] = n;
   __syncthreads();
   if (npos) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) c += (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ o) << 2, (int)c);
+    c = (uint32_t)wave_sum_u64(c);
     __shared__ uint32_t wc[kSampWaves];
     if (lane == 0) wc[w] = c;
     __syncthreads();
@@ -1163,7 +1195,8 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
   const bool vec = a.vec != 0;
   const int mode = kTopP ? 1 : a.mode;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int32_t k = (mode == 2 || mode == 4) ? (a.top_k ? a.top_k[r] : a.top_k_s) : 0;
+  const RowParams rp = row_params(a, r);
+  const int32_t k = (mode == 2 || mode == 4) ? rp.k : 0;
   // what the selection runs over: the row (direct passes) or its candidate list
   const float* sp = p;
   const uint32_t* sidx = nullptr;
@@ -1188,7 +1221,7 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
     __shared__ HistShared hs;
     // top_p: the histogram pass (with the row's count of p > 0 and its mass), then one gather
     hist_pass(p, V, vec, hs, sh, &npos, &row_tot);
-    const double thr = (double)(a.top_p ? a.top_p[r] : a.top_p_s) * (double)row_tot;
+    const double thr = (double)rp.tp * (double)row_tot;
     select_bin(thr, hs);
     __syncthreads();
     const uint32_t bin = hs.bin;
@@ -1228,25 +1261,8 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
   // the head stay on this path) and counts the row's p > 0 on the way. A list of ties that will
   // not shrink falls back to the passes below.
   if (!kTopP && (mode == 2 || mode == 4) && vec && k > 0 && k <= kOnePassMaxK && V >= kOnePassMinV) {
-    // the floor: the k-th largest of the threads' maxima over their kHeadElems / kSampThreads
-    // head elements (a subset of the head, so at most the head's k-th largest; the head's
-    // largest keys are nearly always their thread's maximum, so it is about as tight), from a
-    // bitonic sort of the 1024 maxima (no LDS atomics, which serialise on keys sharing their
-    // top bits).
-    uint32_t hm = 0u;
-#pragma unroll
-    for (int j = 0; j < kHeadElems / 4 / kSampThreads; ++j) {
-      const float4 x = *reinterpret_cast<const float4*>(p + 4 * (threadIdx.x + j * kSampThreads));
-      hm = max(max(hm, max(prob_key(x.x), prob_key(x.y))), max(prob_key(x.z), prob_key(x.w)));
-    }
-    uint32_t* buf = reinterpret_cast<uint32_t*>(cs.val);
-    hm = sort_desc_keys(hm, buf);
-    if (threadIdx.x == k - 1) sh.u32a = hm;
-    __syncthreads();
-    const uint32_t floor0 = sh.u32a;
-    __syncthreads();  // the sort buffer is dead from here: its memory holds the candidates
     uint32_t c = 0;
-    listed = gather(ListPred{0, floor0, 0u, 0.0}, &c, k);
+    listed = gather(ListPred{0, 0u, 0u, 0.0}, &c, k);  // the floor comes from the row's head
     npos = (int64_t)c;
     __syncthreads();
   }
@@ -1261,7 +1277,7 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
       uint32_t mk = 0;
       for_row(p, V, vec, [&](int, float x) { mk = max(mk, prob_key(x)); });
       mk = block_max_u32(mk, sh);
-      mthr = (double)(a.min_p ? a.min_p[r] : a.min_p_s) * (double)__builtin_bit_cast(float, mk);
+      mthr = (double)rp.mp * (double)__builtin_bit_cast(float, mk);
     } else {
       const bool by_mass = mode == 1;
       uint32_t c = 0;
@@ -1271,7 +1287,7 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
       if (by_mass) {
         row_tot = block_sum_u64(m, sh);
         tm = block_sum_u64(tm, sh);
-        const double thr = (double)(a.top_p ? a.top_p[r] : a.top_p_s) * (double)row_tot;
+        const double thr = (double)rp.tp * (double)row_tot;
         // a floor needs the subset's mass to reach the threshold
         cand_lo = (double)tm < thr ? 0u : radix_threshold(cs.val, kTops, true, 1u, true, 0u, thr, sh);
       } else if ((int64_t)k < npos) {
@@ -1288,7 +1304,7 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
     }
     __syncthreads();
   }
-  sample_row(sp, sidx, sV, svec, a, r, npos, row_tot, sh,
+  sample_row(sp, sidx, sV, svec, a, r, rp, npos, row_tot, sh,
              sidx ? reinterpret_cast<uint32_t*>(cs.val + kSampThreads) : nullptr, lo_given);
 }
 
