@@ -556,17 +556,19 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
       for (int e = 0; e < 4; ++e) x[e] = i0 + e < V ? p[i0 + e] : 0.f;
     }
   };
-  int last = -1;
-  uint64_t acc = 0;
-  auto visit = [&](int i, float x) {
-    const uint64_t m = kept_mass(x);
-    acc += m;
-    if (m) last = max(last, i);
+  // The pass sums each lane's kept masses in fp64: the terms are integers below 2^41 (p <= 2)
+  // and a lane sums at most 64 of them per tile, so every partial sum is exact (below 2^53) and
+  // converts to the same integer the fixed-point sum gives, at half the per-element cost.
+  double acc = 0.0;
+  auto visit = [&](int, float x) {
+    const uint32_t k = prob_key(x);
+    const bool keep = k >= lo && (a.mode != 3 || (double)x >= mthr);  // lo >= 1: k == 0 never kept
+    acc += keep ? rint((double)x * kMassScale) : 0.0;
   };
   auto chunk_done = [&](int t) {  // this wave's share of tile t is in acc
-    acc = wave_sum_u64(acc);
-    if (lane == 0 && acc) atomicAdd((unsigned long long*)&sh.mass[t / tpc], (unsigned long long)acc);
-    acc = 0;
+    const uint64_t m = wave_sum_u64((uint64_t)acc);
+    if (lane == 0 && m) atomicAdd((unsigned long long*)&sh.mass[t / tpc], (unsigned long long)m);
+    acc = 0.0;
   };
   if (vec) {
     // Wave w takes whole tiles w, w + 16, ...: a tile is 1024 16-byte vectors, 16 per lane, read
@@ -614,20 +616,14 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
         const int i = t * kTile + 4 * threadIdx.x + e;
         if (i < V) visit(i, p[i]);
       }
-      if ((t + 1) % tpc == 0 || t == ntiles - 1) {  // chunk t / tpc ends here
-        acc = wave_sum_u64(acc);
-        if (lane == 0 && acc) atomicAdd((unsigned long long*)&sh.mass[t / tpc], (unsigned long long)acc);
-        acc = 0;
-      }
+      if ((t + 1) % tpc == 0 || t == ntiles - 1) chunk_done(t);  // chunk t / tpc ends here
     }
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) last = max(last, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, last));
-  if (lane == 0) sh.wsum[w] = (uint64_t)(int64_t)last;
-  if (threadIdx.x == 0) sh.pick = -1;
+  if (threadIdx.x == 0) { sh.pick = -1; sh.u32b = 0u; }
   __syncthreads();
-  for (int i = 0; i < kSampWaves; ++i) last = max(last, (int)(int64_t)sh.wsum[i]);
-  // wave 0: the total, the target and the first chunk whose inclusive prefix exceeds it
+  // wave 0: the total, the target and the first chunk whose inclusive prefix exceeds it; when
+  // none does (u * total reaches the total), the last chunk with kept mass, scanned for its last
+  // kept element
   if (threadIdx.x < 64) {
     uint64_t c[4];
 #pragma unroll
@@ -637,22 +633,29 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
     const uint64_t tot = readlane_u64(incl, 63);
     const double target = rp.u * (double)tot;
     uint64_t run = incl - lm;
-    int first = 256;
-    uint64_t first_excl = 0;
+    int first = 256, lastc = -1;
+    uint64_t first_excl = 0, last_excl = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       if (first == 256 && c[e] && (double)(run + c[e]) > target) { first = 4 * lane + e; first_excl = run; }
+      if (c[e]) { lastc = 4 * lane + e; last_excl = run; }
       run += c[e];
     }
     int f = first;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) f = min(f, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, f));
+    const uint64_t lb = __builtin_amdgcn_ballot_w64(lastc >= 0);
+    const int ll = lb ? 63 - __builtin_clzll(lb) : -1;  // the lane holding the last kept chunk
     if (first == f && f < 256) {
       sh.u32a = (uint32_t)f;
       sh.u64a = first_excl;
     }
+    if (f == 256 && lane == ll) {
+      sh.u32a = (uint32_t)lastc;
+      sh.u64a = last_excl;
+    }
     if (lane == 0) {
-      if (f == 256) sh.u32a = 0xffffffffu;
+      if (f == 256 && ll < 0) sh.u32a = 0xffffffffu;  // nothing kept
       sh.u64b = __builtin_bit_cast(uint64_t, target);
     }
   }
@@ -663,6 +666,7 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
     const int chunk = (int)sh.u32a;
     const double target = __builtin_bit_cast(double, sh.u64b);
     uint64_t run = sh.u64a;
+    int last = -1;  // this thread's last kept element of the chunk
     const int end = min(V, (chunk + 1) * tpc * kTile);
     for (int base = chunk * tpc * kTile; base < end; base += kTile) {
       const int i0 = base + 4 * threadIdx.x;
@@ -691,13 +695,18 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
           if (m[e] && (double)c > target) { sh.pick = i0 + e; break; }
         }
       }
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (m[e]) last = i0 + e;  // ascending within the thread and across tiles
       __syncthreads();
       if (sh.pick >= 0) break;
       run += tile;
     }
+    if (sh.pick < 0 && last >= 0) atomicMax((unsigned*)&sh.u32b, (unsigned)(last + 1));
+    __syncthreads();
   }
   if (threadIdx.x == 0) {
-    const int j = sh.pick >= 0 ? sh.pick : last;
+    const int j = sh.pick >= 0 ? sh.pick : (int)sh.u32b - 1;
     a.out[r] = (idx && j >= 0) ? (int32_t)idx[j] : j;
   }
 }

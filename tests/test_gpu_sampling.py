@@ -109,6 +109,29 @@ def test_sample_long_rows(dev, mode):
 
 
 @pytest.mark.parametrize("mode", list(SAMPLERS))
+@pytest.mark.parametrize("V", [4099, 128256])
+def test_sample_uniform_edges(dev, mode, V):
+    """u = 0 draws the first kept token and u = 1 (target = the whole kept mass, which no running
+    sum exceeds) the last one, as in the oracle; rows whose last kept token is not in the row's
+    last chunk (trailing zeros) exercise the draw's search for the last chunk with kept mass."""
+    print(f"sample edges mode={mode} V={V}", flush=True)
+    B = 8
+    probs = _grid_probs(B, V, V + 5, ties=False)
+    probs[4:, V // 2:] = 0  # trailing zeros: the last kept token sits mid-row
+    probs = probs / probs.sum(-1, keepdim=True)
+    probs = (torch.floor(probs.double() * 2**30) / 2**30).float()
+    prm = _params(B, V, V + 6)
+    prm["top_k"] = torch.randint(1, 300, (B,), generator=torch.Generator().manual_seed(V)).to(torch.int32)
+    prm["u"] = torch.tensor([0.0, 1.0] * (B // 2), dtype=torch.float64)
+    dp = {k: v.to(dev) for k, v in prm.items()}
+    got = _call(mode, probs.to(dev), dp, uniforms=dp["u"]).cpu().numpy()
+    want, kept = oracle.sample(probs.numpy(), mode, prm["u"].numpy(), top_k=prm["top_k"].numpy(),
+                               top_p=prm["top_p"].numpy(), min_p=prm["min_p"].numpy())
+    assert (got == want).all(), f"rows {np.nonzero(got != want)[0][:5]}: {got[got != want][:5]} vs {want[got != want][:5]}"
+    assert kept[np.arange(B), got].all()
+
+
+@pytest.mark.parametrize("mode", list(SAMPLERS))
 def test_sample_padded_rows(dev, mode):
     """16-byte aligned rows whose length is not a multiple of 4 (a padded row stride): the
     vector passes and the candidate lists' last elements."""
