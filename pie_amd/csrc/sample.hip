@@ -722,14 +722,15 @@ __device__ __forceinline__ void sample_row(const float* p, const uint32_t* idx, 
 // more than kWaveCands candidates in some wave's segment, sends the row to the direct passes.
 constexpr int kWaveCands = 512;
 constexpr int kCands = kWaveCands * kSampWaves;
-// The one-read top_k path: the floor comes from the row's first kHeadElems elements; it runs for
-// k <= kOnePassMaxK (about k * V / kHeadElems candidates, well inside kCands at V = 128256, and
-// for k = 50 at V = 128256 about 400, inside the short-list path's 1024 for every row) and
-// rows of at least kOnePassMinV elements (shorter rows gain little from skipping a read).
-constexpr int kHeadElems = 16384;
+// The one-read top_k path: the floor comes from a sample of the row (the first three batches of
+// every wave's segment, kSampleElems elements); it runs for k <= kOnePassMaxK (about
+// k * V / kSampleElems candidates: for k = 50 at V = 128256 about 150, inside the short-list
+// path's 1024 for every row) and rows of at least kOnePassMinV elements (shorter rows gain little
+// from skipping a read).
+constexpr int kSampleElems = 3 * 4 * 256 * kSampWaves;
 constexpr int kOnePassMaxK = 256;
-constexpr int kHeadMaxima = 256;  // the head floor: the k-th largest of this many group maxima
-static_assert(kOnePassMaxK <= kHeadMaxima, "the head floor needs k <= kHeadMaxima");
+constexpr int kHeadMaxima = 256;  // the sample floor: the k-th largest of this many group maxima
+static_assert(kOnePassMaxK <= kHeadMaxima, "the sample floor needs k <= kHeadMaxima");
 constexpr int kOnePassMinV = 65536;
 
 struct alignas(16) CandShared {
@@ -776,7 +777,7 @@ struct ListPred {
 };
 
 template <typename P>
-__device__ int compact_segment(const float* p, int V, bool vec, P&& pred, CandShared& cs) {
+__device__ __forceinline__ int compact_segment(const float* p, int V, bool vec, P&& pred, CandShared& cs) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const uint64_t lt = (1ull << lane) - 1ull;
   float* val = cs.val + w * kWaveCands;
@@ -988,47 +989,105 @@ __device__ __forceinline__ int wave_shrink(float* val, uint32_t* idx, int n, int
   return base;
 }
 
+// The wave's largest of v (all lanes active), in every lane.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__builtin_amdgcn_ds_bpermute(((threadIdx.x & 63) ^ o) << 2, (int)v));
+  return v;
+}
+// The largest float at or below min_p * mx (computed in fp64, as the kept test (double)x >=
+// min_p * max does), and at least the smallest positive float: x >= it for every x kept under
+// any maximum >= mx.
+__device__ __forceinline__ float minp_floor(double min_p, float mx) {
+  const double t = min_p * (double)mx;
+  float fl = (float)t;
+  if ((double)fl > t) fl = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, fl) - 1u);
+  return fmaxf(fl, __builtin_bit_cast(float, 1u));
+}
+// min_p's shrink of a wave's candidate list: raises the floor ff to minp_floor of the list's
+// largest key and keeps, in order, the entries at or above it (entries only move to lower
+// positions; every read precedes every write).
+__device__ __forceinline__ int minp_shrink(float* val, uint32_t* idx, int n, double min_p, float& ff) {
+  constexpr int J = kWaveCands / 64;
+  const int lane = threadIdx.x & 63;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  float v[J];
+  uint32_t ix[J];
+  __builtin_amdgcn_wave_barrier();  // the list's last appends (other lanes' writes) come first
+  uint32_t mk = 0u;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int i = 64 * j + lane;
+    v[j] = i < n ? val[i] : 0.f;
+    ix[j] = i < n ? idx[i] : 0u;
+    mk = max(mk, prob_key(v[j]));
+  }
+  ff = fmaxf(ff, minp_floor(min_p, __builtin_bit_cast(float, wave_max_u32(mk))));
+  int base = 0;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const bool keep = 64 * j + lane < n && v[j] >= ff;
+    const uint64_t b = __builtin_amdgcn_ballot_w64(keep);
+    if (keep) {
+      const int pos = base + (int)__builtin_popcountll(b & lt);
+      val[pos] = v[j];
+      idx[pos] = ix[j];
+    }
+    base += (int)__builtin_popcountll(b);
+  }
+  return base;
+}
+
 // One read of the row for top_k (k <= kOnePassMaxK), as wave segments: each wave keeps, in
-// vocabulary order, the candidates at or above its own floor, which starts at the head floor (a
-// floor under the row's k-th largest key: the k-th largest of the maxima of kHeadMaxima groups of
-// kHeadElems / kHeadMaxima elements of the row's head, a subset of the row; the head's largest
-// keys mostly fall in different groups, so it is nearly as tight as the head's k-th
-// largest) and rises to the k-th largest key of the wave's list whenever the
-// list would overflow (wave_shrink; rows whose largest keys sit away from where f0 was taken). A
-// subset's k-th largest never exceeds the row's, so every key at or above the row's k-th largest
-// stays listed; a wave with more than kSampThreads / kSampWaves entries at the end keeps its own
-// top k (ties included), so the lists together usually fit the short-list path. Returns the
-// wave's count, more than kWaveCands when a list of ties would not shrink (unusable); cpos gets
-// this lane's count of p > 0.
-__device__ int topk_segment(const float* p, int V, int k, CandShared& cs, uint32_t& cpos) {
+// vocabulary order, the candidates at or above its own floor, which starts at the sample floor (a
+// floor under the row's k-th largest key: the k-th largest of the maxima of kHeadMaxima disjoint
+// groups of kSampleElems / kHeadMaxima sampled elements, a subset of the row; the sample's
+// largest keys mostly fall in different groups, so it is nearly as tight as the sample's k-th
+// largest) and rises to the k-th largest key of the wave's list whenever the list would overflow
+// (wave_shrink; rows whose largest keys cluster in one segment). A subset's k-th largest never
+// exceeds the row's, so every key at or above the row's k-th largest stays listed; a wave with
+// more than kSampThreads / kSampWaves entries at the end keeps its own top k (ties included), so
+// the lists together usually fit the short-list path. Returns the wave's count, more than
+// kWaveCands when a list of ties would not shrink (unusable).
+template <bool kMinP>
+__device__ __forceinline__ int one_read_segment(const float* p, int V, int k, double min_p, CandShared& cs) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const uint64_t lt = (1ull << lane) - 1ull;
   float* val = cs.val + w * kWaveCands;
   uint32_t* idx = cs.idx + w * kWaveCands;
   int n = 0;
   bool over = false;
-  uint32_t f = 1u, c = 0;
-  // appends the keys >= f of four consecutive elements per lane (up to 256 per call)
-  auto add4 = [&](const float (&x)[4], int i0, bool live) {
-    uint32_t key[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      key[e] = live ? prob_key(x[e]) : 0u;
-      c += key[e] != 0u;
-    }
-    if (over) return;
-    if (n + 256 > kWaveCands) {
+  uint32_t f = 1u;
+  float ff = 0.f;  // the floor as a float: for f >= 1, x >= ff iff prob_key(x) >= f (NaN fails)
+  // the list's shrink when it would overflow: top_k keeps the wave's own top k, min_p the keys at
+  // or above min_p times the wave's largest key (the row's is at least as large)
+  auto shrink = [&]() {
+    if constexpr (kMinP) {
+      n = minp_shrink(val, idx, n, min_p, ff);
+    } else {
       n = wave_shrink(val, idx, n, k, f);
-      if (n + 256 > kWaveCands) {  // ties that do not shrink: the list is unusable
+      ff = __builtin_bit_cast(float, f);
+    }
+  };
+  // appends the keys >= f of four consecutive elements per lane (up to 256 per call); most calls
+  // find none and leave after one ballot
+  auto add4 = [&](const float (&x)[4], int i0, bool live) {
+    if (over) return;
+    uint32_t bits = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bits |= (uint32_t)(live && x[e] >= ff) << e;
+    if (__builtin_amdgcn_ballot_w64(bits != 0u) == 0) return;
+    if (n + 256 > kWaveCands) {
+      shrink();
+      if (n + 256 > kWaveCands) {  // keys that do not shrink: the list is unusable
         over = true;
         return;
       }
-    }
-    uint32_t bits = 0;
+      bits = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) bits |= (uint32_t)(key[e] >= f && key[e] != 0u) << e;
+      for (int e = 0; e < 4; ++e) bits |= (uint32_t)(live && x[e] >= ff) << e;
+    }
     const uint32_t cnt = __builtin_popcount(bits);
-    if (__builtin_amdgcn_ballot_w64(cnt != 0) == 0) return;
     const uint64_t b0 = __builtin_amdgcn_ballot_w64(cnt & 1u), b1 = __builtin_amdgcn_ballot_w64(cnt & 2u),
                    b2 = __builtin_amdgcn_ballot_w64(cnt & 4u);
     int pos = n + __builtin_popcountll(b0 & lt) + 2 * __builtin_popcountll(b1 & lt) +
@@ -1045,8 +1104,8 @@ __device__ int topk_segment(const float* p, int V, int k, CandShared& cs, uint32
   const int nv = V >> 2;
   const int seg = (nv + kSampWaves - 1) / kSampWaves;
   const int v0 = w * seg, v1 = min(nv, v0 + seg);
-  // the segment in batches of kB vectors, two register buffers in turn; the last batch's
-  // loads past the segment are clamped to its last vector and their keys dropped
+  // the segment in batches of kB vectors; the last batch's loads past the segment are clamped to
+  // its last vector and their keys dropped
   constexpr int kU = 4, kB = kU * 64;
   const int nb = v1 > v0 ? (v1 - v0 + kB - 1) / kB : 0;
   auto scan = [&](const float4 (&d)[kU], int at) {
@@ -1057,30 +1116,40 @@ __device__ int topk_segment(const float* p, int V, int k, CandShared& cs, uint32
       add4(xe, 4 * v, v < v1);
     }
   };
-  float4 x[kU], y[kU];
+  float4 x[kU], y[kU], z[kU];
   auto load = [&](float4 (&d)[kU], int at) {
 #pragma unroll
     for (int q = 0; q < kU; ++q)
       d[q] = *reinterpret_cast<const float4*>(p + 4 * min(at + lane + 64 * q, v1 - 1));
   };
-  // the head's loads, then the segment's first two batches, which stay in flight while the
-  // floor is formed (barriers wait for LDS traffic only)
-  float4 hx[kHeadElems / 4 / kSampThreads];
+  auto dmax = [](const float4 (&d)[kU]) {
+    uint32_t m = 0u;
 #pragma unroll
-  for (int j = 0; j < kHeadElems / 4 / kSampThreads; ++j)
-    hx[j] = *reinterpret_cast<const float4*>(p + 4 * (threadIdx.x + j * kSampThreads));
-  // (unconditional, so the compiler's wait counts keep them outstanding: rows of at least
-  // kOnePassMinV elements give every segment more than two batches)
+    for (int q = 0; q < kU; ++q)
+      m = max(m, max(max(prob_key(d[q].x), prob_key(d[q].y)), max(prob_key(d[q].z), prob_key(d[q].w))));
+    return m;
+  };
+  // The floor comes from the segments' first three batches (the start of every wave's segment,
+  // 3 kB vectors per wave): the maxima of kHeadMaxima disjoint groups of them (a lane's 48
+  // elements, then threads t, t + kHeadMaxima, ...), bitonic-sorted (no LDS atomics, which
+  // serialise on keys sharing their top bits) in the candidates' memory, which is dead until the
+  // floor is known. (The loads are unconditional: rows of at least kOnePassMinV elements give
+  // every segment more than three batches.)
   load(x, v0);
   load(y, v0 + kB);
-  {
-    uint32_t hm = 0u;
+  load(z, v0 + 2 * kB);
+  if constexpr (kMinP) {
+    // min_p: min_p times the sample's largest key, rounded down to a float
+    uint32_t hm = max(dmax(x), max(dmax(y), dmax(z)));
+    hm = (uint32_t)wave_max_u32(hm);
+    __shared__ uint32_t wmx[kSampWaves];
+    if (lane == 0) wmx[w] = hm;
+    __syncthreads();
 #pragma unroll
-    for (int j = 0; j < kHeadElems / 4 / kSampThreads; ++j)
-      hm = max(max(hm, max(prob_key(hx[j].x), prob_key(hx[j].y))), max(prob_key(hx[j].z), prob_key(hx[j].w)));
-    // the maxima of kHeadMaxima groups of the head (threads t, t + kHeadMaxima, ...), then their
-    // bitonic sort (no LDS atomics, which serialise on keys sharing their top bits), in the
-    // candidates' memory, which is dead until the floor is known
+    for (int i = 0; i < kSampWaves; ++i) hm = max(hm, wmx[i]);
+    ff = minp_floor(min_p, __builtin_bit_cast(float, hm));
+  } else {
+    uint32_t hm = max(dmax(x), max(dmax(y), dmax(z)));
     uint32_t* buf = reinterpret_cast<uint32_t*>(cs.val);
     buf[threadIdx.x] = hm;
     __syncthreads();
@@ -1093,41 +1162,50 @@ __device__ int topk_segment(const float* p, int V, int k, CandShared& cs, uint32
     if (threadIdx.x == k - 1) f0 = hm;
     __syncthreads();
     f = max(f0, 1u);
+    ff = __builtin_bit_cast(float, f);
     __syncthreads();  // the sort buffer is dead from here: its memory holds the candidates
   }
-  for (int b = 0; b < nb; b += 2) {
+  // three register buffers in turn (no copies between them, which would wait for the loads in
+  // flight)
+  for (int b = 0; b < nb; b += 3) {
     scan(x, v0 + b * kB);
-    if (b + 2 < nb) load(x, v0 + (b + 2) * kB);
+    if (b + 3 < nb) load(x, v0 + (b + 3) * kB);
     if (b + 1 >= nb) break;
     scan(y, v0 + (b + 1) * kB);
-    if (b + 3 < nb) load(y, v0 + (b + 3) * kB);
+    if (b + 4 < nb) load(y, v0 + (b + 4) * kB);
+    if (b + 2 >= nb) break;
+    scan(z, v0 + (b + 2) * kB);
+    if (b + 5 < nb) load(z, v0 + (b + 5) * kB);
   }
   if (w == kSampWaves - 1) {  // the last < 4 elements belong to the last segment
     const int i = 4 * nv + lane;
     float xe[4] = {i < V ? p[i] : 0.f, 0.f, 0.f, 0.f};
     add4(xe, i, i < V);  // elements 1-3 of xe are 0: no key
   }
-  cpos = c;
   if (over) return kWaveCands + 1;
-  return n > kSampThreads / kSampWaves ? wave_shrink(val, idx, n, k, f) : n;
+  if (n > kSampThreads / kSampWaves) shrink();
+  return n;
 }
 
 // Copies the elements that satisfy pred into cs.val / cs.idx in vocabulary order (each wave its
 // own segment, then the gaps between the segments' lists closed); *total = the list's length.
-// npos (optional): the row's count of p > 0, counted on the way. False when some segment
-// overflowed (the list is then unusable). topk > 0: the candidates of a top_k (topk_segment, from
-// the row head's floor; vec rows only) instead of pred's.
+// npos (optional): the row's count of p > 0, counted on the way (a top_k list's length stands in
+// for it, below). False when some segment overflowed (the list is then unusable). topk > 0: the
+// candidates of a top_k (one_read_segment, vec rows only) instead of pred's; minp > 0: those of a
+// min_p the same way.
 __device__ __forceinline__ bool gather_list(const float* p, int V, bool vec, const ListPred& pred, CandShared& cs,
-                                         int* total_out, uint32_t* npos, int topk = 0) {
+                                         int* total_out, uint32_t* npos, int topk = 0, double minp = 0.0) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   uint32_t c = 0;
-  const int n = topk > 0 ? topk_segment(p, V, topk, cs, c) : compact_segment(p, V, vec, [&](int i, float x) {
+  const int n = topk > 0 ? one_read_segment<false>(p, V, topk, 0.0, cs)
+              : minp > 0.0 ? one_read_segment<true>(p, V, 0, minp, cs)
+                           : compact_segment(p, V, vec, [&](int i, float x) {
     c += prob_key(x) != 0u;
     return pred(i, x);
   }, cs);
   if (lane == 0) cs.wn[w] = n;
   __syncthreads();
-  if (npos) {
+  if (npos && topk == 0 && !(minp > 0.0)) {
     c = (uint32_t)wave_sum_u64(c);
     __shared__ uint32_t wc[kSampWaves];
     if (lane == 0) wc[w] = c;
@@ -1143,25 +1221,33 @@ __device__ __forceinline__ bool gather_list(const float* p, int V, bool vec, con
     total += cs.wn[i];
   }
   if (over) return false;
-  // close the gaps between the segments' lists (moves go to lower slots: read, then write)
+  // A top_k list stands in for the row's count of p > 0: it holds every key at or above the
+  // row's k-th largest, so it has at least k entries when the row has k positive keys and
+  // every positive key otherwise; its length then decides k < count and k >= count alike.
+  if (npos && (topk > 0 || minp > 0.0)) *npos = (uint32_t)total;  // (min_p does not use it)
+  // close the gaps between the segments' lists: list position d takes its entry from the wave
+  // whose prefix range holds it (moves go to lower slots: read, then write); positions past the
+  // total are skipped, so a short list costs one read and one write per thread
   constexpr int J = kCands / kSampThreads;
   float mv[J];
   uint32_t mi[J];
-  int md[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const int s = threadIdx.x + j * kSampThreads;
-    const int sw = s / kWaveCands, so = s % kWaveCands;
-    int base = 0;
-    for (int i = 0; i < sw; ++i) base += cs.wn[i];
-    md[j] = so < cs.wn[sw] ? base + so : -1;
-    mv[j] = cs.val[s];
-    mi[j] = cs.idx[s];
+    const int d = threadIdx.x + j * kSampThreads;
+    if (d < total) {
+      int base = 0, sw = 0;
+      for (; sw < kSampWaves - 1 && d >= base + cs.wn[sw]; ++sw) base += cs.wn[sw];
+      const int s = sw * kWaveCands + (d - base);
+      mv[j] = cs.val[s];
+      mi[j] = cs.idx[s];
+    }
   }
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < J; ++j)
-    if (md[j] >= 0) { cs.val[md[j]] = mv[j]; cs.idx[md[j]] = mi[j]; }
+  for (int j = 0; j < J; ++j) {
+    const int d = threadIdx.x + j * kSampThreads;
+    if (d < total) { cs.val[d] = mv[j]; cs.idx[d] = mi[j]; }
+  }
   *total_out = total;
   return true;
 }
@@ -1215,9 +1301,9 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
   uint64_t row_tot = 0;
   // Copies the elements that satisfy pred into the candidate list (gather_list) and points the
   // selection at it; false (and the list unused) when some segment overflowed.
-  auto gather = [&](const ListPred& pred, uint32_t* npos_out = nullptr, int topk = 0) -> bool {
+  auto gather = [&](const ListPred& pred, uint32_t* npos_out = nullptr, int topk = 0, double minp = 0.0) -> bool {
     int total;
-    if (!gather_list(p, V, vec, pred, cs, &total, npos_out, topk)) return false;
+    if (!gather_list(p, V, vec, pred, cs, &total, npos_out, topk, minp)) return false;
     sp = cs.val;
     sidx = cs.idx;
     sV = total;
@@ -1264,15 +1350,22 @@ __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
     __syncthreads();
   }
   // One read for top_k (alone or before top_p) with k <= kOnePassMaxK over a long row: the k-th
-  // largest of the row's first kHeadElems elements is a floor under the row's k-th largest, so one
-  // pass collects every element at or above it (about k * V / kHeadElems of them for exchangeable
-  // rows; each wave raises its own floor when its list fills, so rows whose largest keys sit past
-  // the head stay on this path) and counts the row's p > 0 on the way. A list of ties that will
-  // not shrink falls back to the passes below.
+  // largest of a sample of the row is a floor under the row's k-th largest, so one pass collects
+  // every element at or above it (about k * V / kSampleElems of them for exchangeable rows; each
+  // wave raises its own floor when its list fills, so rows whose largest keys cluster stay on this
+  // path). A list of ties that will not shrink falls back to the passes below.
   if (!kTopP && (mode == 2 || mode == 4) && vec && k > 0 && k <= kOnePassMaxK && V >= kOnePassMinV) {
     uint32_t c = 0;
-    listed = gather(ListPred{0, 0u, 0u, 0.0}, &c, k);  // the floor comes from the row's head
+    listed = gather(ListPred{0, 0u, 0u, 0.0}, &c, k);  // the floor comes from the sample
     npos = (int64_t)c;
+    __syncthreads();
+  }
+  // One read for min_p (0 < min_p <= 1) over a long row: min_p times the largest key of the same
+  // sample is a floor under min_p times the row's largest key, each wave raising its own floor to
+  // min_p times its list's largest key when the list fills; the list holds the row's largest key
+  // and every kept one, and the draw below takes the row's maximum from it.
+  if (!kTopP && mode == 3 && vec && V >= kOnePassMinV && rp.mp > 0.f && rp.mp <= 1.f) {
+    listed = gather(ListPred{0, 0u, 0u, 0.0}, nullptr, 0, (double)rp.mp);
     __syncthreads();
   }
   // plain sampling, and top_k with k outside (0, V), keep every p > 0: no candidate list; top_p

@@ -794,13 +794,17 @@ int main(int argc, char** argv) {
     case_sample(3, 70000, 1, false);        // top_p, flat rows: the bin's keys (and the ties of row 1)
     case_sample(2, 70000, 1, false, true);  // top_p, peaked rows: every key from the bin up
     case_sample(2, 70000, 1, false, false, 0, -69990);  // a bin of 69990 equal keys: search over the row
-    // top_k over long rows: one read with a floor from the first 8192 entries (a row of ties
-    // overflows the list and falls back; a head with fewer than k positives does too)
+    // top_k and min_p over long rows: one read with a floor from a sample of the row (the start
+    // of every wave segment; a row of ties overflows the list and falls back, zeros at the row's
+    // start leave wave 0 without sampled positives, tiny entries there lower the floor)
     case_sample(4, 70000, 2, false, true);
     case_sample(4, 70000, 4, false, true);
     case_sample(3, 70000, 4, false, true, 0, 8192);
     case_sample(3, 70000, 2, false, true, 0, 8190);
-    case_sample(3, 70000, 4, false, true, 0, -8192);  // a low floor: the list overflows
+    case_sample(3, 70000, 4, false, true, 0, -8192);
+    case_sample(4, 70000, 3, false, true);
+    case_sample(3, 70000, 3, false);                  // flat rows: most entries kept, the lists overflow
+    case_sample(3, 70000, 3, false, true, 0, -8192);
     // (rows of more than 256 tiles, whose draw chunks span several tiles, run in the GPU tests)
     case_softmax(3, 1000, false);
     case_softmax(3, 777, true);

@@ -291,27 +291,46 @@ def test_sampling_chain_like_pie(dev):
     assert ((tok >= 0) & (tok < V)).all()
 
 
-@pytest.mark.parametrize("mode", ["top_k", "top_k_top_p"])
-@pytest.mark.parametrize("head", ["plain", "zero", "tiny", "large"])
-def test_sample_top_k_one_read_and_fallbacks(dev, mode, head):
-    """top_k with small k over a long row takes its floor from the row's first 8192 entries:
-    an ordinary head (one read), a head of zeros (fewer than k positives there: the two-pass
-    path), a head of tiny positives (the floor admits almost the whole row: the candidate list
-    overflows and the two-pass path runs) and a head holding the row's largest entries."""
-    print(f"sample {mode} head={head}", flush=True)
+def _sample_positions(V):
+    """The entries the one-read paths sample for their floor: the first three batches of 256
+    16-byte vectors of each of the 16 wave segments of the row."""
+    nv = V // 4
+    seg = (nv + 15) // 16
+    m = torch.zeros(V, dtype=torch.bool)
+    for w in range(16):
+        m[4 * w * seg: 4 * min(nv, w * seg + 3 * 256)] = True
+    return m
+
+
+@pytest.mark.parametrize("mode", ["top_k", "top_k_top_p", "min_p"])
+@pytest.mark.parametrize("case", ["plain", "zero", "tiny", "large", "clustered"])
+def test_sample_one_read_and_fallbacks(dev, mode, case):
+    """top_k with small k and min_p over a long row take their floor from a sample of the row
+    (the start of every wave segment): an ordinary sample (one read), a sample of zeros (no
+    floor: the two-pass path), a sample of tiny positives (the floor admits almost the whole row:
+    the candidate lists overflow and the two-pass path runs), a sample holding the row's largest
+    entries, and the largest entries clustered in one segment outside the sample (that wave's
+    list fills and raises its own floor)."""
+    print(f"sample {mode} case={case}", flush=True)
     B, V = 12, 128256
     g = torch.Generator().manual_seed(91)
     w = torch.randint(1, 4097, (B, V), generator=g).double() ** 2
-    if head == "zero":
-        w[:, :8192] = 0
-    elif head == "tiny":
-        w[:, :8192] = 1e3
-    elif head == "large":
-        w[:, :8192] *= 64
+    sm = _sample_positions(V)
+    if case == "zero":
+        w[:, sm] = 0
+    elif case == "tiny":
+        w[:, sm] = 1e3
+    elif case == "large":
+        w[:, sm] *= 64
+    elif case == "clustered":
+        seg = 4 * ((V // 4 + 15) // 16)
+        w[:, 5 * seg + 4 * 3 * 256: 6 * seg] *= 64  # segment 5 past its sampled batches
     p = (torch.floor(w / w.sum(-1, keepdim=True) * 2**30) / 2**30).float()
     prm = _params(B, V, 92)
     prm["top_k"] = torch.randint(1, 257, (B,), generator=g).to(torch.int32)
     prm["top_k"][1] = 256
+    prm["min_p"][0] = 1.0
+    prm["min_p"][1] = 1e-4
     dp = {k: v.to(dev) for k, v in prm.items()}
     got = _call(mode, p.to(dev), dp, uniforms=dp["u"]).cpu().numpy()
     want, kept = oracle.sample(p.numpy(), mode, prm["u"].numpy(), top_k=prm["top_k"].numpy(),
