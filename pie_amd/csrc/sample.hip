@@ -841,17 +841,19 @@ __device__ __forceinline__ int compact_segment(const float* p, int V, bool vec, 
         if (!has_x) break;
       }
     }
-    for (; vb < v1; vb += 64) {
-      const int v = vb + lane;
-      float xe[4] = {0.f, 0.f, 0.f, 0.f};
-      uint32_t bits = 0;
-      if (v < v1) {
-        const float4 x = *reinterpret_cast<const float4*>(p + 4 * v);
-        xe[0] = x.x; xe[1] = x.y; xe[2] = x.z; xe[3] = x.w;
+    if (vb < v1) {  // the last partial batch: one round trip, loads past the segment clamped
+      float4 x[kU];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bits |= (uint32_t)pred(4 * v + e, xe[e]) << e;
+      for (int k = 0; k < kU; ++k) x[k] = *reinterpret_cast<const float4*>(p + 4 * min(vb + lane + 64 * k, v1 - 1));
+#pragma unroll
+      for (int k = 0; k < kU; ++k) {
+        const int v = vb + lane + 64 * k;
+        const float xe[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+        uint32_t bits = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bits |= (uint32_t)(v < v1 && pred(4 * v + e, xe[e])) << e;
+        emit(bits, 4 * v, xe, 1);
       }
-      emit(bits, 4 * v, xe, 1);
     }
     if (w == kSampWaves - 1) {  // the last < 4 elements belong to the last segment
       const int i = 4 * nv + lane;
