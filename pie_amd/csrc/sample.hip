@@ -1279,6 +1279,7 @@ __device__ __forceinline__ void hist_pass(const float* p, int V, bool vec, HistS
 // Two kernels, so each gets the registers its own paths need.
 template <bool kTopP>
 __global__ __launch_bounds__(kSampThreads) void sample_kernel(SampleArgs a) {
+  prefetch_kernarg<(int)sizeof(SampleArgs)>(a);
   __shared__ SampleShared sh;
   __shared__ CandShared cs;
   const int r = blockIdx.x;
