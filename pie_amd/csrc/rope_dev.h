@@ -232,24 +232,30 @@ __device__ __forceinline__ void qk_norm_rope_append_block(const QkNormArgs& qa, 
     const int* hd = b.hd;
 #pragma unroll
     for (int i = 0; i < UB; ++i) {
-      float f[8], wf[8];
-      unpack8(X[i], f);
-      unpack8(Wt[i], wf);
-      float ss = 0.f;
+      // rows of v heads and slots past the last row need no norm or rotation: a wave whose 16-lane
+      // groups hold only such rows skips them (the test is wave-uniform, so the DPP exchanges
+      // below still run on all 64 lanes when they run)
+      uint4 o = X[i];
+      if (__builtin_amdgcn_ballot_w64(kind[i] <= 1) != 0) {
+        float f[8], wf[8];
+        unpack8(X[i], f);
+        unpack8(Wt[i], wf);
+        float ss = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
-      const float rstd = rsqrtf(row16_sum(ss) / 128.0f + qa.eps);
+        for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+        const float rstd = rsqrtf(row16_sum(ss) / 128.0f + qa.eps);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f[e] = (f[e] * rstd) * wf[e];
-      const uint4 g = pack8(f);  // normalised row, rounded to bf16 as the separate norm stores it
-      const uint4 pg = make_uint4(dpp_ror8(g.x), dpp_ror8(g.y), dpp_ror8(g.z), dpp_ror8(g.w));
-      float own[8], oth[8];
-      unpack8(g, own);
-      unpack8(pg, oth);
+        for (int e = 0; e < 8; ++e) f[e] = (f[e] * rstd) * wf[e];
+        const uint4 g = pack8(f);  // normalised row, rounded to bf16 as the separate norm stores it
+        const uint4 pg = make_uint4(dpp_ror8(g.x), dpp_ror8(g.y), dpp_ror8(g.z), dpp_ror8(g.w));
+        float own[8], oth[8];
+        unpack8(g, own);
+        unpack8(pg, oth);
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        own[e] = is_x ? rot_x(own[e], oth[e], tb[e]) : rot_y(oth[e], own[e], tb[e]);
-      const uint4 o = pack8(own);
+        for (int e = 0; e < 8; ++e)
+          own[e] = is_x ? rot_x(own[e], oth[e], tb[e]) : rot_y(oth[e], own[e], tb[e]);
+        o = pack8(own);
+      }
       if (kind[i] == 0) {
         st16(qa.q_out + tq * qa.qo_ts + (int64_t)hd[i] * qa.qo_hs + sub * 8, o);
       } else {
