@@ -100,8 +100,11 @@ int embedding_impl(const int32_t* ids, int64_t T, const pie_bf16* W, int64_t V, 
     a.nvec = (uint32_t)nvec;
     a.vpr = FastDiv::make((uint32_t)(H / 8));
     // One 16-byte vector per thread (configuration 4 steady state: 6.29 TB/s, against 6.27
-    // with 2 and 5.98 with 4 vectors per thread).
-    hipLaunchKernelGGL((embed_vec<1, SCALE>), dim3((unsigned)((nvec + 255) / 256)), blk, 0, st, a);
+    // with 2 and 5.98 with 4 vectors per thread); the scaled form, whose arithmetic sits between
+    // a vector's load and its store, two (44.2-44.7 us against 45.8-46.0 with one and 45.2-45.3
+    // with four at configuration 4's shape).
+    constexpr int U = SCALE ? 2 : 1;
+    hipLaunchKernelGGL((embed_vec<U, SCALE>), dim3((unsigned)((nvec + 256 * U - 1) / (256 * U))), blk, 0, st, a);
   } else {
     const int64_t blocks = (T + 3) / 4, cap = (int64_t)num_cus() * 64;
     hipLaunchKernelGGL(embed_scalar<SCALE>, dim3((unsigned)(blocks < cap ? blocks : cap)), blk, 0, st, a);
