@@ -313,7 +313,9 @@ int pie_hip_get_batch_indices_positions(const int32_t* append_indptr, const int3
  * kv range is cut into (max_kv_len < 0: unknown). pie_hip_attention_decode launches
  * batch * splits work groups per kv head; each piece's range is derived on the device from the
  * request's current length, so one launch configuration (and one captured graph) serves any
- * lengths, as Pie's graph replay requires (llama3.py:340-414, :905-950). With splits > 1 the
+ * lengths, as Pie's graph replay requires (llama3.py:340-414, :905-950). Batches of at most 256
+ * requests are worked on longest request first (the order is found on the device, per launch);
+ * the results do not depend on the order. With splits > 1 the
  * run needs `workspace` (16-byte aligned) of batch * splits * num_qo_heads * (head_dim + 1) * 4
  * bytes. head_dim in {64, 128, 256}; num_qo_heads / num_kv_heads <= 16. Page ids outside
  * [0, num_pages) are treated as masked positions. window_left >= 0 is flashinfer's sliding

@@ -305,13 +305,49 @@ struct KVTile {
 };
 
 // ------------------------------------------------------------------------------ decode
-// Grid (batch * splits, kv heads): work group x handles request x / splits, split x % splits of
-// its kv range. The split is derived on the device from the request's current kv length
+// Grid (batch * splits * kv heads), one dimension: work group x takes the request of rank
+// x / (splits * kv heads), split (x / kv heads) % splits, kv head x % kv heads. For batches of
+// at most kRankMax requests the rank orders requests by attended length, longest first (ties
+// by request index), so the longest requests' work groups are dispatched first and the short
+// ones fill the tail; larger batches keep request order (rank = request). The split is derived on the device from the request's current kv length
 // (chunks of ceil(kv_len / splits) rounded up to whole 32-token tiles, at least kMinChunk), so a
 // launch depends only on (batch, splits) and a captured graph replays correctly for any lengths.
 // With one split the work group writes the output; otherwise it writes an fp32 partial output
 // and its log2-sum-exp to slot x, and attn_merge_kernel combines the splits.
 constexpr int kMinChunk = 128;
+constexpr int kRankMax = 256;  // one request per thread of the work group
+
+// The request of rank r (B <= kRankMax), with its kv length and first page-table entry. Every
+// work group of the launch ranks the same lengths the same way, so together they cover each
+// (request, split, kv head) once. lens: kRankMax ints of LDS.
+__device__ __forceinline__ int request_of_rank(const PagedKV& kv, int B, int window_left, int r,
+                                               int32_t* lens, int32_t* pick, int& kv_len, int& page0) {
+  const int i = threadIdx.x;
+  int kl = 0, li = -1;  // padding: below every length
+  if (i < B) {
+    kl = kv_length(kv, i);
+    li = window_left >= 0 ? min(kl, window_left + 1) : kl;
+  }
+  lens[i] = li;
+  __syncthreads();
+  if (i < B) {
+    int before = 0;  // requests ordered before i
+    for (int k = 0; k < B; k += 4) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(lens + k);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int le = (int)v[e];
+        before += le > li || (le == li && k + e < i);
+      }
+    }
+    if (before == r) { pick[0] = i; pick[1] = kl; }
+  }
+  __syncthreads();
+  const int b = uniform(pick[0]);
+  kv_len = uniform(pick[1]);
+  page0 = kv.indptr[b];
+  return b;
+}
 
 __device__ __forceinline__ void split_range(int kv_len, int splits, int j, int& kv0, int& kv1) {
   int chunk = (kv_len + splits - 1) / splits;
@@ -322,28 +358,38 @@ __device__ __forceinline__ void split_range(int kv_len, int splits, int j, int& 
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
-    const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv, int G, int Hq,
+    const uint16_t* __restrict__ q, int64_t q_ts, int64_t q_hs, PagedKV kv, int B, int G, int Hq,
     float scale_log2, int splits, int window_left, uint16_t* __restrict__ out, int64_t o_ts,
     int64_t o_hs, float* __restrict__ part_o, float* __restrict__ part_lse,
     const float* __restrict__ sinks) {
   using W = WaveAttn<D>;
   constexpr int kVtile = kTileTokens * D;  // elements of one wave's V tile
   constexpr int kSmem = (4 * kVtile * 2 > 4 * 16 * (D + 2) * 4) ? 4 * kVtile * 2 : 4 * 16 * (D + 2) * 4;
+  static_assert(kSmem >= kRankMax * 4, "the ranked lengths fit in the V tiles' LDS");
   __shared__ __attribute__((aligned(16))) char smem[kSmem];
+  __shared__ int32_t rank_pick[2];
 
-  const int slot = blockIdx.x;
-  const int b = slot / splits;
-  const int kvh = blockIdx.y;
+  const int Hkv = Hq / G;
+  const int per = splits * Hkv;
+  const int r = blockIdx.x / per, rem = blockIdx.x - r * per;
+  const int j = rem / Hkv, kvh = rem - j * Hkv;
+  int b = r, kv_len, page0;
+  if (B <= kRankMax) {
+    // the LDS holds the lengths until the first page window's barrier
+    b = request_of_rank(kv, B, window_left, r, reinterpret_cast<int32_t*>(smem), rank_pick, kv_len, page0);
+  } else {
+    kv_len = kv_length(kv, b);
+    page0 = kv.indptr[b];
+  }
+  const int slot = b * splits + j;
   const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int kv_len = kv_length(kv, b);
   // sliding window: the query (position kv_len - 1) sees positions >= kv_len - 1 - window_left
   const int ws = window_left >= 0 ? max(0, kv_len - 1 - window_left) : 0;
   int kv0, kv1;
-  split_range(kv_len - ws, splits, slot - b * splits, kv0, kv1);
+  split_range(kv_len - ws, splits, j, kv0, kv1);
   kv0 += ws;
   kv1 += ws;
-  const int page0 = kv.indptr[b];
 
   W st;
   st.init();
@@ -1159,16 +1205,19 @@ __global__ __launch_bounds__(256, 2) void attn_prefill32_kernel(
 
 using namespace pie;
 
-// Host: how many splits per request. Aims at ~16 work groups per CU over all (request, kv head,
-// split) triples; when the longest context is known (max_kv_len >= 0) no split is shorter than
-// kMinChunk tokens. The result depends on the batch only, so one plan serves a captured graph.
+// Host: how many splits per request. Aims at ~4 work groups per CU over all (request, kv head,
+// split) triples when the launch takes requests longest first (batches of at most kRankMax), at
+// ~16 otherwise (smaller pieces even out the tail that request order leaves); when the longest
+// context is known (max_kv_len >= 0) no split is shorter than kMinChunk tokens. The result
+// depends on the batch only, so one plan serves a captured graph.
 extern "C" int pie_hip_attention_decode_plan(int64_t batch, int64_t num_kv_heads, int64_t max_kv_len,
                                              int64_t num_cus, int64_t* splits) {
   PIE_REQUIRE(splits && batch >= 0 && num_kv_heads > 0, "decode_plan: bad batch %lld / num_kv_heads %lld",
               (long long)batch, (long long)num_kv_heads);
   const int64_t cus = num_cus > 0 ? num_cus : 256;
   const int64_t per = std::max<int64_t>(1, batch * num_kv_heads);
-  int64_t s = (16 * cus + per - 1) / per;
+  const int64_t groups = (batch <= kRankMax ? 4 : 16) * cus;
+  int64_t s = (groups + per - 1) / per;
   if (max_kv_len >= 0) s = std::min<int64_t>(s, std::max<int64_t>(1, (max_kv_len + kMinChunk - 1) / kMinChunk));
   *splits = std::max<int64_t>(1, std::min<int64_t>(s, 64));
   return PIE_HIP_OK;
@@ -1205,8 +1254,8 @@ static void launch_decode(hipStream_t st, const uint16_t* q, int64_t q_ts, int64
                           const PagedKV& kv, int G, int Hq, int Hkv, float sl2, int B, int splits,
                           int window_left, uint16_t* out, int64_t o_ts, int64_t o_hs, float* po,
                           float* pl, const float* sinks) {
-  hipLaunchKernelGGL(attn_decode_kernel<D>, dim3(B * splits, Hkv), dim3(256), 0, st, q, q_ts, q_hs, kv,
-                     G, Hq, sl2, splits, window_left, out, o_ts, o_hs, po, pl, sinks);
+  hipLaunchKernelGGL(attn_decode_kernel<D>, dim3(B * splits * Hkv), dim3(256), 0, st, q, q_ts, q_hs, kv,
+                     B, G, Hq, sl2, splits, window_left, out, o_ts, o_hs, po, pl, sinks);
   if (splits > 1)
     hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(B, (Hq + 64 / (D / 8) - 1) / (64 / (D / 8))), dim3(64), 0,
                        st, B, Hq, splits, po, pl, out, o_ts, o_hs, sinks);
@@ -1232,7 +1281,7 @@ static int attention_decode_impl(
                   num_kv_heads <= 65535,
               "attention_decode: need num_qo_heads = G * num_kv_heads with G <= 16 (got %lld / %lld)",
               (long long)num_qo_heads, (long long)num_kv_heads);
-  PIE_REQUIRE(batch >= 0 && splits >= 1 && splits <= 64 && batch * splits < (1ll << 31),
+  PIE_REQUIRE(batch >= 0 && splits >= 1 && splits <= 64 && batch * splits * num_kv_heads < (1ll << 31),
               "attention_decode: bad batch %lld / splits %lld", (long long)batch, (long long)splits);
   PIE_REQUIRE(aligned16(q) && aligned16(out) && q_tok_stride % 8 == 0 && q_head_stride % 8 == 0 &&
                   o_tok_stride % 8 == 0 && o_head_stride % 8 == 0,

@@ -69,6 +69,37 @@ def test_decode_vs_oracle(dev, layout, Hq, Hkv, D, P, splits):
     _tight(got, want, "decode")
 
 
+@pytest.mark.parametrize("B", [256, 257])
+def test_decode_request_order(dev, B):
+    """Batches of at most 256 requests are worked on longest first (ranked on the device, ties by
+    request index), larger ones in request order: tied and distinct lengths against the oracle,
+    and the same requests given in another order give the same rows bit for bit."""
+    print(f"decode request order B={B}", flush=True)
+    g = torch.Generator().manual_seed(B)
+    ctx = torch.tensor([0, 1, 15, 16, 17, 40, 95])[torch.randint(0, 7, (B,), generator=g)].to(torch.int32)
+    ctx[: B // 4] = torch.randint(0, 200, (B // 4,), generator=g).to(torch.int32)
+    a = wl.attn_batch(ctx, torch.ones(B, dtype=torch.int32), Hq=8, Hkv=2, D=128, page_size=16,
+                      seed=B + 7)
+    want = _want(a)
+    perm = torch.randperm(B, generator=g)
+    ap = wl.attn_batch(ctx[perm], torch.ones(B, dtype=torch.int32), Hq=8, Hkv=2, D=128,
+                       page_size=16, seed=B + 7)
+    # the same k/v rows and q rows per request: copy them over into the permuted layout
+    pb, pbp = a["batch"], ap["batch"]
+    for i in range(B):
+        b = int(perm[i])
+        src = pb.kv_indices[int(pb.kv_indptr[b]):int(pb.kv_indptr[b + 1])].long()
+        dst = pbp.kv_indices[int(pbp.kv_indptr[i]):int(pbp.kv_indptr[i + 1])].long()
+        ap["cache"][dst] = a["cache"][src]
+    ap["q"] = a["q"][perm].clone()
+    for splits in (None, 2):
+        got = _decode(dev, a, splits)
+        assert_bf16_close(N(got), want, what=f"decode B={B} splits {splits}")
+        _tight(got, want, f"decode B={B} splits {splits}")
+        gotp = _decode(dev, ap, splits)
+        assert torch.equal(gotp.cpu(), got.cpu()[perm]), f"B={B} splits {splits}: permuted batch differs"
+
+
 def test_decode_page_size_one_long_context(dev):
     """Page size 1: a 1500-token context spans several 510-page windows of the staged table."""
     a = wl.attn_batch(torch.tensor([1499, 700, 3]), torch.ones(3, dtype=torch.int32), Hq=8, Hkv=2,
