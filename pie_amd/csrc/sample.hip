@@ -1572,6 +1572,34 @@ __device__ __forceinline__ int block_min_i(int v, float* red) {
   return t;
 }
 
+// Wave-wide max / sum: DPP within each 16-lane row (row_ror 8, 4; quad_perm), after which every
+// lane of a row holds the row's value, then the four rows' values read from lanes 0, 16, 32, 48
+// and combined in that order, so every lane gets the same result.
+template <bool kMax>
+__device__ __forceinline__ float wave_reduce_dpp(float v) {
+  auto op = [](float x, float y) { return kMax ? fmaxf(x, y) : x + y; };
+  auto dpp = [](float x, auto ctrl) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(ctrl)::value, 0xF, 0xF, false));
+  };
+  v = op(v, dpp(v, std::integral_constant<int, 0x128>{}));  // row_ror:8
+  v = op(v, dpp(v, std::integral_constant<int, 0x124>{}));  // row_ror:4
+  v = op(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+  v = op(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+  auto rd = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
+  return op(op(rd(0), rd(16)), op(rd(32), rd(48)));
+}
+// Block-wide max / sum with one barrier: red holds kSampWaves floats used by this call alone.
+template <bool kMax>
+__device__ __forceinline__ float block_reduce_once(float v, float* red) {
+  v = wave_reduce_dpp<kMax>(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int i = 1; i < kSampWaves; ++i) t = kMax ? fmaxf(t, red[i]) : t + red[i];
+  return t;
+}
+
 template <bool BF16, int NV>
 __global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
     const void* __restrict__ logits, int64_t stride, int V, const float* __restrict__ temps, float greedy,
@@ -1579,18 +1607,24 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
   using IO = RowIO<BF16>;
   constexpr int E = IO::E;
   __shared__ float red[kSampWaves];
+  __shared__ float red_max[kSampWaves], red_sum[kSampWaves];
   const int r = blockIdx.x;
   const char* row = reinterpret_cast<const char*>(logits) + (int64_t)r * stride * (BF16 ? 2 : 4);
   char* orow = reinterpret_cast<char*>(out) + (int64_t)r * out_stride * (BF16 ? 2 : 4);
   const int nv = V / E;
+  // Every load is issued unconditionally (indices clamped into the row; the values past it are
+  // never used) and the tail element's first, so the loads complete in the order the online
+  // pass below consumes them and each vector is waited for alone. (Loads under conditions made
+  // the compiler wait for all of them before the first use.)
+  const int it = nv * E + threadIdx.x;  // this thread's tail element, if any
+  const float xt_raw = IO::get(row, min(it, V - 1));
   uint4 d[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int v = threadIdx.x + j * kSampThreads;
-    d[j] = v < nv ? ld16(row + (int64_t)v * 16) : make_uint4(0u, 0u, 0u, 0u);
+    const int v = min((int)threadIdx.x + j * kSampThreads, max(nv - 1, 0));
+    d[j] = ld16(row + (int64_t)v * 16);
   }
-  const int it = nv * E + threadIdx.x;  // this thread's tail element, if any
-  const float xt = it < V ? IO::get(row, it) : -INFINITY;
+  const float xt = it < V ? xt_raw : -INFINITY;
   const float T = temps[r];
   const bool greedy_row = T < greedy;
   const float c = greedy_row ? 1.f : 1.4426950408889634f / T;
@@ -1664,7 +1698,8 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
       }
     }
   }
-  const float M = block_max_f(m, red);
+  float S;
+  const float M = kKeep ? block_reduce_once<true>(m, red_max) : block_max_f(m, red);
   if (greedy_row) {
     int am = 0x7fffffff;  // first index holding the maximum
 #pragma unroll
@@ -1693,6 +1728,7 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
   }
   if constexpr (kKeep) {
     s = m == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f((m - M) * c);
+    S = block_reduce_once<false>(s, red_sum);
   } else {
     s = it < V ? __builtin_amdgcn_exp2f((xt - M) * c) : 0.f;
 #pragma unroll
@@ -1703,8 +1739,9 @@ __global__ __launch_bounds__(kSampThreads) void scaled_softmax_resident_kernel(
 #pragma unroll
       for (int e = 0; e < E; ++e) s += __builtin_amdgcn_exp2f((x[e] - M) * c);
     }
+    S = block_sum_f(s, red);
   }
-  const float inv = 1.f / block_sum_f(s, red);
+  const float inv = 1.f / S;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int v = threadIdx.x + j * kSampThreads;
