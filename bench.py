@@ -306,9 +306,11 @@ def _ops_ceiling(dev, run):
         a = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         return lambda: lib.pie_probe_read(a.data_ptr(), nbytes, threads, vpt, sink.data_ptr(), st())
     # read-only ceilings (all of a work group's loads issued before any is used): the softmax's
-    # read phase (one 1024-thread work group per 256 KB row, 16 vectors per thread) and the best
-    # read-only shape measured (256-thread groups, 16 vectors each), over the softmax's bytes and
-    # over the sampler's fp32 rows
+    # read phase on its own rows (one 1024-thread work group per 250.5 KiB row, 16 vectors per
+    # thread); the same shape over rows 256 KiB apart (a power-of-two stride, which measured
+    # slower: every work group starts on the same memory channels); and the best read-only shape
+    # measured (256-thread groups, 16 vectors each), over the softmax's bytes and over the
+    # sampler's fp32 rows
     # the dense bf16 MFMA rate a kernel can reach (32x32x16, 2 work groups of 4 waves per CU,
     # 4 independent accumulator chains per wave), alone and with as much independent fp32 VALU
     # work interleaved: the matrix pipe's practical ceiling, and whether vector work overlaps it
@@ -330,8 +332,16 @@ def _ops_ceiling(dev, run):
         mf.append(e)
     n_rd = 256 * 1024 * 256  # 256 rows of 256 KiB (softmax rows are 250.5 KiB)
     n_rd2 = 2 * n_rd
-    res = mf + [run("ceiling read 64 MiB, 1 work group x 1024 threads x 16 vectors per 256 KiB (softmax read phase)",
-               n_rd, lambda: make_read(n_rd, 1024, 16)),
+    lib.pie_probe_read_rows.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int64, C.c_void_p, C.c_void_p]
+    sm_vec = 128256 * 2 // 16  # a [256, 128256] bf16 row in 16-byte vectors (also its stride)
+
+    def make_read_rows():
+        a = torch.empty(256 * sm_vec * 16, dtype=torch.uint8, device=dev)
+        return lambda: lib.pie_probe_read_rows(a.data_ptr(), 256, sm_vec, sm_vec, sink.data_ptr(), st())
+    res = mf + [run("ceiling read [256, 128256] bf16 rows, 1 work group x 1024 threads x 16 vectors per row "
+                    "(softmax read phase)", 256 * sm_vec * 16, make_read_rows),
+           run("ceiling read 64 MiB, 1 work group x 1024 threads x 16 vectors per 256 KiB (row stride a "
+               "power of two)", n_rd, lambda: make_read(n_rd, 1024, 16)),
            run("ceiling read 64 MiB, 256 threads x 16 vectors per work group", n_rd, lambda: make_read(n_rd, 256, 16)),
            run("ceiling read 128 MiB (sampler rows' bytes), 256 threads x 16 vectors per work group", n_rd2,
                lambda: make_read(n_rd2, 256, 16))]
