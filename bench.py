@@ -310,7 +310,7 @@ def _ops_ceiling(dev, run):
     # thread); the same shape over rows 256 KiB apart (a power-of-two stride, which measured
     # slower: every work group starts on the same memory channels); and the best read-only shape
     # measured (256-thread groups, 16 vectors each), over the softmax's bytes and over the
-    # sampler's fp32 rows
+    # sampler's fp32 rows; and the sampler's own row layout (one work group per fp32 row)
     # the dense bf16 MFMA rate a kernel can reach (32x32x16, 2 work groups of 4 waves per CU,
     # 4 independent accumulator chains per wave), alone and with as much independent fp32 VALU
     # work interleaved: the matrix pipe's practical ceiling, and whether vector work overlaps it
@@ -335,16 +335,18 @@ def _ops_ceiling(dev, run):
     lib.pie_probe_read_rows.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int64, C.c_void_p, C.c_void_p]
     sm_vec = 128256 * 2 // 16  # a [256, 128256] bf16 row in 16-byte vectors (also its stride)
 
-    def make_read_rows():
-        a = torch.empty(256 * sm_vec * 16, dtype=torch.uint8, device=dev)
-        return lambda: lib.pie_probe_read_rows(a.data_ptr(), 256, sm_vec, sm_vec, sink.data_ptr(), st())
+    def make_read_rows(vec):
+        a = torch.empty(256 * vec * 16, dtype=torch.uint8, device=dev)
+        return lambda: lib.pie_probe_read_rows(a.data_ptr(), 256, vec, vec, sink.data_ptr(), st())
     res = mf + [run("ceiling read [256, 128256] bf16 rows, 1 work group x 1024 threads x 16 vectors per row "
-                    "(softmax read phase)", 256 * sm_vec * 16, make_read_rows),
+                    "(softmax read phase)", 256 * sm_vec * 16, lambda: make_read_rows(sm_vec)),
            run("ceiling read 64 MiB, 1 work group x 1024 threads x 16 vectors per 256 KiB (row stride a "
                "power of two)", n_rd, lambda: make_read(n_rd, 1024, 16)),
            run("ceiling read 64 MiB, 256 threads x 16 vectors per work group", n_rd, lambda: make_read(n_rd, 256, 16)),
            run("ceiling read 128 MiB (sampler rows' bytes), 256 threads x 16 vectors per work group", n_rd2,
-               lambda: make_read(n_rd2, 256, 16))]
+               lambda: make_read(n_rd2, 256, 16)),
+           run("ceiling read [256, 128256] fp32 rows, 1 work group x 1024 threads per row, two rounds of "
+               "16 vectors (sampler rows)", 256 * 2 * sm_vec * 16, lambda: make_read_rows(2 * sm_vec))]
     res += [run("ceiling copy 8 MiB -> 8 MiB (cfg1 bytes), cached", 2 * n1, lambda: make_copy(0)),
            run("ceiling copy 8 MiB -> 8 MiB (cfg1 bytes), non-temporal", 2 * n1, lambda: make_copy(1)),
            run("ceiling copy 64 MB -> 64 MB (softmax bytes, [256,128256] bf16), non-temporal",

@@ -11,10 +11,12 @@
 //                       threads x vpt vectors with all of a thread's vpt loads issued before any
 //                       is used (the resident softmax's pattern at 1024 threads and vpt 16),
 //                       one xor per work group written out.
-//   pie_probe_read_rows: the resident softmax's read phase on its own rows: one 1024-thread work
-//                       group per row of row_vec 16-byte vectors at a row stride of stride_vec
-//                       vectors, 16 loads per thread (indices past the row clamped to its last
-//                       vector), all issued before any is used.
+//   pie_probe_read_rows: a row-per-work-group read on the kernels' own row layout: one 1024-thread
+//                       work group per row of row_vec 16-byte vectors at a row stride of
+//                       stride_vec vectors, in rounds of 16 loads per thread (indices past the
+//                       row clamped to its last vector), each round's loads all issued before
+//                       any is used (one round: the resident softmax's read phase; two: a
+//                       sampler row of fp32 probabilities).
 //   pie_probe_mfma:     dense bf16 v_mfma_f32_32x32x16 throughput, 2 work groups of 4 waves per
 //                       CU: 4 independent accumulator chains per wave (valu = 0), with 128
 //                       independent fp32 fma per 16 MFMAs (1: does vector work overlap the
@@ -112,23 +114,29 @@ extern "C" int pie_probe_mfma(float* out, int blocks, int iters, int valu, void*
 }
 
 __global__ __launch_bounds__(1024) void probe_read_rows_kernel(const u32x4* __restrict__ src, int row_vec,
-                                                               int64_t stride_vec, uint32_t* __restrict__ out) {
+                                                               int64_t stride_vec, int rounds,
+                                                               uint32_t* __restrict__ out) {
   const u32x4* p = src + (int64_t)blockIdx.x * stride_vec;
-  u32x4 v[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) v[j] = __builtin_nontemporal_load(p + min((int)threadIdx.x + 1024 * j, row_vec - 1));
   uint32_t x = 0;
+  for (int q = 0; q < rounds; ++q) {
+    u32x4 v[16];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) x ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    for (int j = 0; j < 16; ++j)
+      v[j] = __builtin_nontemporal_load(p + min((int)threadIdx.x + 1024 * (16 * q + j), row_vec - 1));
+#pragma unroll
+    for (int j = 0; j < 16; ++j) x ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  }
   if (x == 0x9e3779b9u) out[blockIdx.x] = x;  // keeps the loads; practically never written
 }
 
 extern "C" int pie_probe_read_rows(const void* src, int rows, int row_vec, int64_t stride_vec, uint32_t* out,
                                    void* stream) {
-  if (rows <= 0 || row_vec <= 0 || row_vec > 16 * 1024 || stride_vec < row_vec || (reinterpret_cast<uintptr_t>(src) & 15))
+  if (rows <= 0 || row_vec <= 0 || row_vec > 2 * 16 * 1024 || stride_vec < row_vec ||
+      (reinterpret_cast<uintptr_t>(src) & 15))
     return 1;
+  const int rounds = (row_vec + 16 * 1024 - 1) / (16 * 1024);
   hipLaunchKernelGGL(probe_read_rows_kernel, dim3((unsigned)rows), dim3(1024), 0, (hipStream_t)stream,
-                     (const u32x4*)src, row_vec, stride_vec, out);
+                     (const u32x4*)src, row_vec, stride_vec, rounds, out);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
