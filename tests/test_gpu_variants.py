@@ -44,6 +44,28 @@ def test_gemma_rms_norm_large_row_lists(dev, T, H):
     assert_bits_equal(N(out), oracle.gemma_rmsnorm(N(x), N(w), 1e-6), f"gemma {T}x{H}")
 
 
+def test_gemma_rms_norm_mean_near_midpoint(dev):
+    """The correctly rounded mean of the squares at and just above a bf16 rounding midpoint, on
+    the row-prefetching kernel (64 MiB of rows): rows whose exact mean is a midpoint (a quarter
+    1.0078125, the rest 1.0: squares 1.015625 and 1.0, mean 1.00390625, a tie that rounds to
+    1.0) or sits 2^-18 above it (one more 1.0078125: rounds to 1.0078125) among ordinary rows;
+    bit-exact on the full output, and the two kinds of rows differ."""
+    T, H = 8192, 4096  # 64 MiB of rows: the row-prefetching kernel
+    x = wl.normal((T, H), 45)
+    special = (0, 1, 4095, 8191)
+    for r in special:
+        x[r] = 1.0
+        x[r, : H // 4 + (r % 2)] = 1.0078125  # odd rows: the mean 2^-18 above the midpoint
+        x[r, 1::2] = -x[r, 1::2]
+    w = wl.normal((H,), 46, 0.0, 0.5)
+    out = ops.gemma_rms_norm(x.to(dev), w.to(dev), 0.0)
+    torch.cuda.synchronize()
+    want = oracle.gemma_rmsnorm(N(x), N(w), 0.0)
+    assert_bits_equal(N(out), want, "gemma near-midpoint means")
+    wf = oracle.bf16_to_f32(want)
+    assert not np.array_equal(wf[0, H - 2:], wf[1, H - 2:]), "the tie and the row above it round apart"
+
+
 def test_gemma_rms_norm_every_scale(dev):
     """Rows of one repeated value a, eps = 0: the variance is bf16(a^2) and the kernel's rsqrt
     meets t = bf16(a^2) for every bf16 a in [2^-40, 2^40) (10240 rows), so every correction step
