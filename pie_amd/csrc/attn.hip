@@ -309,9 +309,10 @@ struct KVTile {
 // x / (splits * kv heads), split (x / kv heads) % splits, kv head x % kv heads. For batches of
 // at most kRankMax requests the rank orders requests by attended length, longest first (ties
 // by request index), so the longest requests' work groups are dispatched first and the short
-// ones fill the tail; larger batches keep request order (rank = request). The split is derived on the device from the request's current kv length
-// (chunks of ceil(kv_len / splits) rounded up to whole 32-token tiles, at least kMinChunk), so a
-// launch depends only on (batch, splits) and a captured graph replays correctly for any lengths.
+// ones fill the tail; larger batches keep request order (rank = request). The split is derived
+// on the device from the request's current kv length (chunks of ceil(kv_len / splits) rounded
+// up to whole 32-token tiles, at least kMinChunk), and so is the rank, so a launch depends only
+// on (batch, splits) and a captured graph replays correctly for any lengths.
 // With one split the work group writes the output; otherwise it writes an fp32 partial output
 // and its log2-sum-exp to slot x, and attn_merge_kernel combines the splits.
 constexpr int kMinChunk = 128;
