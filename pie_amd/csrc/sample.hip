@@ -1808,7 +1808,9 @@ extern "C" int pie_hip_scaled_softmax(const void* logits, int32_t is_bf16, int64
 #define PIE_SOFTMAX_RESIDENT(BF, NV)                                                                      \
   hipLaunchKernelGGL((scaled_softmax_resident_kernel<BF, NV>), grid, block, 0, st, logits, stride, (int)vocab, \
                      temperatures, greedy_threshold, out, out_stride)
-  if (vec && per_thread <= (is_bf16 ? 20 : 16)) {
+  // (rows shorter than one 16-byte vector take the streaming kernel: the resident one reads
+  // whole vectors)
+  if (vec && vocab >= e && per_thread <= (is_bf16 ? 20 : 16)) {
     if (is_bf16) {
       if (per_thread <= 8) PIE_SOFTMAX_RESIDENT(true, 8);
       else if (per_thread <= 16) PIE_SOFTMAX_RESIDENT(true, 16);

@@ -67,6 +67,20 @@ def test_one_entry_vocabulary(dev):
     assert out.flatten().tolist() == [1.0] * 64  # exp(x - max) = exp(0), as torch computes it
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_softmax_rows_shorter_than_a_vector(dev, dtype):
+    """Rows of 3 entries in a 16-byte-aligned padded layout (stride 8): shorter than one 16-byte
+    vector, they take the streaming softmax; against the oracle, greedy rows one-hot."""
+    g = torch.Generator().manual_seed(9)
+    full = (torch.randn(16, 8, generator=g) * 3).to(dtype)
+    temps = torch.linspace(0, 2, 16)
+    out = sampling.safe_scaled_softmax(full.to(dev)[:, :3], temps.to(dev))
+    want = oracle.scaled_softmax(full[:, :3].float().numpy(), temps.numpy())
+    got = out.float().cpu().numpy().astype(np.float64)
+    rel = 2 ** -7 if dtype == torch.bfloat16 else 1e-5
+    assert np.all(np.abs(got - want) <= rel * np.abs(want) + 1e-30)
+
+
 def test_prefill_with_requests_appending_nothing(dev):
     """A ragged prefill batch where some requests have no query tokens (cached context only) and
     one holds no context at all: the others match the oracle, and the empty ones write nothing."""
